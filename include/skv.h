@@ -1,0 +1,140 @@
+/*
+ * skv.h -- C ABI of the MI355X (gfx950) KV-cache hot path.
+ *
+ * Every pointer argument is a device pointer (HBM) unless marked "host".
+ * The library never allocates device memory in these entry points: the
+ * caller owns the cache, the inputs, the outputs and the split-K workspace.
+ * Every entry point only enqueues work on `stream` (a hipStream_t passed as an
+ * opaque pointer; NULL = the legacy default stream) and returns without
+ * synchronising.
+ *
+ * Return value: 0 on success, a negative SKV_E* code otherwise. The message
+ * for the most recent failure on the calling thread is skv_last_error().
+ *
+ * Cache layout (contiguous), from the reference's cache indexing
+ * (simple-llm/src/gpu/gpu_kernels.py:2791-2793, 2858-2859):
+ *   element (b, t, h, d) of a [B, T_cap, H_kv, D] cache sits at
+ *   ((b * T_cap + t) * H_kv + h) * D + d.
+ * Paged layout (extension; no reference counterpart): a pool of
+ *   [n_blocks][block_size][H_kv][D] rows, and token t of sequence b lives in
+ *   block block_table[b * max_blocks + t / block_size], row t % block_size.
+ *
+ * Lengths: lens[b] is the number of filled positions of sequence b. The
+ * single-token append writes at position lens[b] and then increments
+ * lens[b]; decode attention of sequence b attends positions [0, lens[b]).
+ * The reference keeps one scalar for the whole batch
+ * (simple-llm/src/gpu/gpu_types.py:443); equal lens[b] reproduce it.
+ */
+#ifndef SKV_H_
+#define SKV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* skv_stream_t; /* a hipStream_t */
+
+enum skv_dtype { SKV_F32 = 0, SKV_BF16 = 1 };
+
+enum skv_status {
+  SKV_OK = 0,
+  SKV_E_INVALID = -22,     /* bad argument (shape, dtype, null pointer)   */
+  SKV_E_UNSUPPORTED = -95, /* valid request this build has no kernel for   */
+  SKV_E_WORKSPACE = -28,   /* workspace smaller than required              */
+  SKV_E_HIP = -5           /* a HIP runtime call failed                    */
+};
+
+/* Thread-local message describing the last failure ("" if none). */
+const char* skv_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int skv_version(void);
+
+/*
+ * Append one token per sequence into a contiguous cache.
+ * Replaces kv_cache_update (simple-llm/src/gpu/gpu_kv_cache.py:113-186) and
+ * its WGSL kernel create_kv_cache_update_kernel
+ * (simple-llm/src/gpu/gpu_kernels.py:2725-2798):
+ *   k_cache[b, lens[b], :, :] = k_new[b, :, :]   (same for v), then lens[b]++.
+ * A sequence with lens[b] >= T_cap is full: nothing is written and lens[b]
+ * is left unchanged (the host checks capacity first, as the reference does
+ * at gpu_kv_cache.py:148-152).
+ * k_new, v_new: [B, H_kv, D] of in_dt. k_cache, v_cache: [B, T_cap, H_kv, D]
+ * of cache_dt (fp32 copy is exact; bf16 storage rounds to nearest even).
+ */
+int skv_append(void* k_cache, void* v_cache, const void* k_new, const void* v_new,
+               int32_t* lens, int B, int H_kv, int D, int T_cap, int cache_dt,
+               int in_dt, skv_stream_t stream);
+
+/* Paged variant of skv_append (extension; same semantics, paged layout). */
+int skv_append_paged(void* k_pool, void* v_pool, const void* k_new,
+                     const void* v_new, int32_t* lens, const int32_t* block_table,
+                     int max_blocks, int block_size, int B, int H_kv, int D,
+                     int cache_dt, int in_dt, skv_stream_t stream);
+
+/*
+ * Append a chunk of up to C tokens per sequence without advancing lens.
+ * Row i < n_new[b] of k_new[b] goes to position lens[b] + i. Rows that would
+ * land at or beyond T_cap are not written (the host rejects such calls).
+ * n_new may be NULL, meaning C for every sequence.
+ * k_new, v_new: [B, C, H_kv, D] of in_dt.
+ * The reference appends one token per call only (gpu_kv_cache.py:157-159);
+ * this is the chunked-prefill extension.
+ */
+int skv_append_chunk(void* k_cache, void* v_cache, const void* k_new,
+                     const void* v_new, const int32_t* lens, const int32_t* n_new,
+                     int B, int C, int H_kv, int D, int T_cap, int cache_dt,
+                     int in_dt, skv_stream_t stream);
+
+/* lens[b] = min(lens[b] + (n_new ? n_new[b] : n_const), T_cap). */
+int skv_advance(int32_t* lens, const int32_t* n_new, int n_const, int B, int T_cap,
+                skv_stream_t stream);
+
+/*
+ * Split-K sizing for decode attention (host-only, no device work).
+ * Given the longest sequence the call may see, picks chunk_tokens (tokens
+ * per workgroup) and n_chunks_max = ceil(max_len / chunk_tokens).
+ * chunk_hint > 0 forces that chunk size (rounded up to a multiple of 256).
+ */
+int skv_decode_plan(int B, int H_kv, int max_len, int chunk_hint,
+                    int* chunk_tokens /* host */, int* n_chunks_max /* host */);
+
+/* Bytes of workspace skv_decode_attn needs for this plan. */
+size_t skv_decode_workspace_bytes(int B, int H_q, int D, int n_chunks_max);
+
+/*
+ * Single-query attention over the cache (decode step).
+ * Replaces attention_with_kv_cache (simple-llm/src/gpu/gpu_kv_cache.py:194-289)
+ * and create_attention_with_kv_cache_kernel
+ * (simple-llm/src/gpu/gpu_kernels.py:2801-2938):
+ *   out[b, h, :] = softmax(scale * q[b, h, :] . K[b, 0:lens[b], h/G, :]^T)
+ *                  . V[b, 0:lens[b], h/G, :],           G = H_q / H_kv.
+ * No length cap (the reference caps lens at 256). lens[b] == 0 gives zeros.
+ * q, out: [B, H_q, D] of q_dt / out_dt. D in {64, 128}; G in {1, 2, 4, 8}.
+ * Split-K: pass 1 writes per-chunk (max, sum, unnormalised o) partials into
+ * ws; pass 2 merges them. Requires lens[b] <= n_chunks_max * chunk_tokens
+ * (violations produce NaN outputs, never out-of-bounds reads).
+ */
+int skv_decode_attn(void* out, const void* q, const void* k_cache,
+                    const void* v_cache, const int32_t* lens, int B, int H_q,
+                    int H_kv, int D, int T_cap, float scale, int chunk_tokens,
+                    int n_chunks_max, void* ws, size_t ws_bytes, int cache_dt,
+                    int q_dt, int out_dt, skv_stream_t stream);
+
+/* Paged variant of skv_decode_attn (extension; block_size a power of two). */
+int skv_decode_attn_paged(void* out, const void* q, const void* k_pool,
+                          const void* v_pool, const int32_t* lens,
+                          const int32_t* block_table, int max_blocks,
+                          int block_size, int B, int H_q, int H_kv, int D,
+                          float scale, int chunk_tokens, int n_chunks_max,
+                          void* ws, size_t ws_bytes, int cache_dt, int q_dt,
+                          int out_dt, skv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SKV_H_ */

@@ -1,0 +1,213 @@
+// K/V append into the preallocated cache: a coalesced strided store.
+//
+// Reference behaviour: kv_cache_update (simple-llm/src/gpu/gpu_kv_cache.py:113-186)
+// drives create_kv_cache_update_kernel (simple-llm/src/gpu/gpu_kernels.py:2725-2798),
+// which copies new_k[b, :] to k_cache[(b*T_cap + pos)*E + :] for every b.
+//
+// Design: one workgroup per sequence for the single-token append. Each lane
+// moves 16 bytes per tensor per iteration (a whole E = H_kv*D row is 1-8 KB),
+// and after a workgroup barrier lane 0 advances lens[b]; no other workgroup
+// touches lens[b], so the position update is race free and the whole decode
+// step stays on the device.
+#include "skv_common.h"
+
+namespace skv {
+namespace {
+
+template <typename TI>
+struct In16;  // 16 bytes of input converted to fp32
+template <>
+struct In16<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void load(const float* p, float* o) {
+    float4 x = *reinterpret_cast<const float4*>(p);
+    o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w;
+  }
+};
+template <>
+struct In16<uint16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void load(const uint16_t* p, float* o) {
+    uint4 x = *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { o[2 * i] = bf16w_lo(w[i]); o[2 * i + 1] = bf16w_hi(w[i]); }
+  }
+};
+
+// Copy (TI == TC) keeps the input bits; fp32 -> bf16 rounds to nearest even;
+// bf16 -> fp32 is exact.
+template <typename TC, typename TI>
+__device__ __forceinline__ void copy_row(TC* __restrict__ dst, const TI* __restrict__ src, int n,
+                                         int tid, int nthreads) {
+  if constexpr (sizeof(TC) == sizeof(TI)) {
+    // same type: move raw 16-byte vectors
+    const uint4* s = reinterpret_cast<const uint4*>(src);
+    uint4* d = reinterpret_cast<uint4*>(dst);
+    const int nv = n * (int)sizeof(TC) / 16;
+    for (int i = tid; i < nv; i += nthreads) d[i] = s[i];
+  } else {
+    constexpr int V = In16<TI>::N;
+    for (int i = tid * V; i < n; i += nthreads * V) {
+      float f[V];
+      In16<TI>::load(src + i, f);
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        if constexpr (sizeof(TC) == 2) dst[i + e] = f32_to_bf16(f[e]);
+        else dst[i + e] = f[e];
+      }
+    }
+  }
+}
+
+template <typename TC, typename TI, bool PAGED>
+__global__ __launch_bounds__(256) void k_append_one(TC* __restrict__ kc, TC* __restrict__ vc,
+                                                    const TI* __restrict__ kn,
+                                                    const TI* __restrict__ vn,
+                                                    int32_t* __restrict__ lens,
+                                                    const int32_t* __restrict__ block_table,
+                                                    int max_blocks, int bs_shift, int E,
+                                                    int T_cap) {
+  const int b = blockIdx.x;
+  const int pos = lens[b];
+  // PAGED: capacity is max_blocks << bs_shift tokens.
+  const int cap = PAGED ? (max_blocks << bs_shift) : T_cap;
+  if (pos < 0 || pos >= cap) return;  // full (or corrupt): write nothing
+  size_t row;
+  if constexpr (PAGED) {
+    const int blk = block_table[(size_t)b * max_blocks + (pos >> bs_shift)];
+    row = ((size_t)blk << bs_shift) + (pos & ((1 << bs_shift) - 1));
+  } else {
+    row = (size_t)b * T_cap + pos;
+  }
+  const size_t src = (size_t)b * E;
+  copy_row<TC, TI>(kc + row * E, kn + src, E, threadIdx.x, blockDim.x);
+  copy_row<TC, TI>(vc + row * E, vn + src, E, threadIdx.x, blockDim.x);
+  __syncthreads();  // every lane has read lens[b] before it moves
+  if (threadIdx.x == 0) lens[b] = pos + 1;
+}
+
+// Chunk append: grid (row tiles, B). Rows i < n_new[b] of sequence b go to
+// position lens[b] + i. lens is read only.
+template <typename TC, typename TI>
+__global__ __launch_bounds__(256) void k_append_chunk(TC* __restrict__ kc, TC* __restrict__ vc,
+                                                      const TI* __restrict__ kn,
+                                                      const TI* __restrict__ vn,
+                                                      const int32_t* __restrict__ lens,
+                                                      const int32_t* __restrict__ n_new, int C,
+                                                      int E, int T_cap, int rows_per_block) {
+  const int b = blockIdx.y;
+  const int n = n_new ? min(n_new[b], C) : C;
+  const int pos0 = lens[b];
+  const int r0 = blockIdx.x * rows_per_block;
+  const int r1 = min(r0 + rows_per_block, n);
+  for (int r = r0; r < r1; ++r) {
+    const int pos = pos0 + r;
+    if (pos < 0 || pos >= T_cap) break;
+    const size_t dst = ((size_t)b * T_cap + pos) * E;
+    const size_t src = ((size_t)b * C + r) * E;
+    copy_row<TC, TI>(kc + dst, kn + src, E, threadIdx.x, blockDim.x);
+    copy_row<TC, TI>(vc + dst, vn + src, E, threadIdx.x, blockDim.x);
+  }
+}
+
+__global__ void k_advance(int32_t* __restrict__ lens, const int32_t* __restrict__ n_new,
+                          int n_const, int B, int T_cap) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int n = n_new ? n_new[b] : n_const;
+  lens[b] = min(lens[b] + n, T_cap);
+}
+
+int log2_exact(int x) {
+  if (x <= 0 || (x & (x - 1))) return -1;
+  int s = 0;
+  while ((1 << s) < x) ++s;
+  return s;
+}
+
+template <bool PAGED>
+int launch_append_one(void* kc, void* vc, const void* kn, const void* vn, int32_t* lens,
+                      const int32_t* bt, int max_blocks, int bs_shift, int B, int E, int T_cap,
+                      int cache_dt, int in_dt, hipStream_t s) {
+  dim3 grid(B), block(256);
+#define SKV_APPEND_CASE(TC, TI)                                                                   \
+  hipLaunchKernelGGL((k_append_one<TC, TI, PAGED>), grid, block, 0, s, (TC*)kc, (TC*)vc,          \
+                     (const TI*)kn, (const TI*)vn, lens, bt, max_blocks, bs_shift, E, T_cap)
+  if (cache_dt == SKV_F32 && in_dt == SKV_F32) SKV_APPEND_CASE(float, float);
+  else if (cache_dt == SKV_F32 && in_dt == SKV_BF16) SKV_APPEND_CASE(float, uint16_t);
+  else if (cache_dt == SKV_BF16 && in_dt == SKV_F32) SKV_APPEND_CASE(uint16_t, float);
+  else SKV_APPEND_CASE(uint16_t, uint16_t);
+#undef SKV_APPEND_CASE
+  return check_launch("skv_append");
+}
+
+bool dt_ok(int dt) { return dt == SKV_F32 || dt == SKV_BF16; }
+
+}  // namespace
+}  // namespace skv
+
+using namespace skv;
+
+extern "C" int skv_append(void* k_cache, void* v_cache, const void* k_new, const void* v_new,
+                          int32_t* lens, int B, int H_kv, int D, int T_cap, int cache_dt,
+                          int in_dt, skv_stream_t stream) {
+  SKV_REQUIRE(k_cache && v_cache && k_new && v_new && lens, SKV_E_INVALID,
+              "skv_append: null pointer argument");
+  SKV_REQUIRE(B > 0 && H_kv > 0 && D > 0 && T_cap > 0, SKV_E_INVALID,
+              "skv_append: dims must be > 0 (B=%d H_kv=%d D=%d T_cap=%d)", B, H_kv, D, T_cap);
+  SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(in_dt), SKV_E_INVALID, "skv_append: bad dtype");
+  SKV_REQUIRE(D % 8 == 0, SKV_E_UNSUPPORTED, "skv_append: D=%d must be a multiple of 8", D);
+  return launch_append_one<false>(k_cache, v_cache, k_new, v_new, lens, nullptr, 0, 0, B,
+                                  H_kv * D, T_cap, cache_dt, in_dt, (hipStream_t)stream);
+}
+
+extern "C" int skv_append_paged(void* k_pool, void* v_pool, const void* k_new, const void* v_new,
+                                int32_t* lens, const int32_t* block_table, int max_blocks,
+                                int block_size, int B, int H_kv, int D, int cache_dt, int in_dt,
+                                skv_stream_t stream) {
+  SKV_REQUIRE(k_pool && v_pool && k_new && v_new && lens && block_table, SKV_E_INVALID,
+              "skv_append_paged: null pointer argument");
+  SKV_REQUIRE(B > 0 && H_kv > 0 && D > 0 && max_blocks > 0, SKV_E_INVALID,
+              "skv_append_paged: dims must be > 0");
+  const int shift = log2_exact(block_size);
+  SKV_REQUIRE(shift >= 0, SKV_E_INVALID, "skv_append_paged: block_size=%d not a power of two",
+              block_size);
+  SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(in_dt), SKV_E_INVALID, "skv_append_paged: bad dtype");
+  SKV_REQUIRE(D % 8 == 0, SKV_E_UNSUPPORTED, "skv_append_paged: D=%d must be a multiple of 8", D);
+  return launch_append_one<true>(k_pool, v_pool, k_new, v_new, lens, block_table, max_blocks,
+                                 shift, B, H_kv * D, 0, cache_dt, in_dt, (hipStream_t)stream);
+}
+
+extern "C" int skv_append_chunk(void* k_cache, void* v_cache, const void* k_new,
+                                const void* v_new, const int32_t* lens, const int32_t* n_new,
+                                int B, int C, int H_kv, int D, int T_cap, int cache_dt, int in_dt,
+                                skv_stream_t stream) {
+  SKV_REQUIRE(k_cache && v_cache && k_new && v_new && lens, SKV_E_INVALID,
+              "skv_append_chunk: null pointer argument");
+  SKV_REQUIRE(B > 0 && C > 0 && H_kv > 0 && D > 0 && T_cap > 0, SKV_E_INVALID,
+              "skv_append_chunk: dims must be > 0");
+  SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(in_dt), SKV_E_INVALID, "skv_append_chunk: bad dtype");
+  SKV_REQUIRE(D % 8 == 0, SKV_E_UNSUPPORTED, "skv_append_chunk: D=%d must be a multiple of 8", D);
+  const int E = H_kv * D;
+  const int rows = 4;
+  dim3 grid((C + rows - 1) / rows, B), block(256);
+  hipStream_t s = (hipStream_t)stream;
+#define SKV_CHUNK_CASE(TC, TI)                                                                \
+  hipLaunchKernelGGL((k_append_chunk<TC, TI>), grid, block, 0, s, (TC*)k_cache, (TC*)v_cache, \
+                     (const TI*)k_new, (const TI*)v_new, lens, n_new, C, E, T_cap, rows)
+  if (cache_dt == SKV_F32 && in_dt == SKV_F32) SKV_CHUNK_CASE(float, float);
+  else if (cache_dt == SKV_F32 && in_dt == SKV_BF16) SKV_CHUNK_CASE(float, uint16_t);
+  else if (cache_dt == SKV_BF16 && in_dt == SKV_F32) SKV_CHUNK_CASE(uint16_t, float);
+  else SKV_CHUNK_CASE(uint16_t, uint16_t);
+#undef SKV_CHUNK_CASE
+  return check_launch("skv_append_chunk");
+}
+
+extern "C" int skv_advance(int32_t* lens, const int32_t* n_new, int n_const, int B, int T_cap,
+                           skv_stream_t stream) {
+  SKV_REQUIRE(lens && B > 0 && T_cap > 0, SKV_E_INVALID, "skv_advance: bad arguments");
+  hipLaunchKernelGGL(k_advance, dim3((B + 255) / 256), dim3(256), 0, (hipStream_t)stream, lens,
+                     n_new, n_const, B, T_cap);
+  return check_launch("skv_advance");
+}

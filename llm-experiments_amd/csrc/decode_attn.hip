@@ -1,0 +1,350 @@
+// Cached single-query decode attention: split-K (flash-decoding) on gfx950.
+//
+// Reference behaviour: attention_with_kv_cache
+// (simple-llm/src/gpu/gpu_kv_cache.py:194-289) launches
+// create_attention_with_kv_cache_kernel (simple-llm/src/gpu/gpu_kernels.py:2801-2938):
+// per (b, h), s_t = scale * q . K[t] for t < len, softmax over [0, len),
+// o = sum_t p_t V[t]. One workgroup per (b, h) and len <= 256 there.
+//
+// Design (HBM-bound GEMV, no MFMA):
+//  * Pass 1, grid (chunk, kv_head, seq), 256 threads = 4 wavefronts = 16 DPP
+//    rows of 16 lanes. A row owns TPG consecutive tokens per iteration; lane i
+//    of the row owns elements [i*D/16, (i+1)*D/16) of each token's K and V
+//    row, loaded as 16-byte vectors (a bf16 D=128 row is 256 contiguous bytes
+//    = 16 lanes x 16 B). The q.k partial dot is summed across the row with
+//    four DPP steps, so every lane of the row holds every score and the
+//    online softmax (running max m, sum l, accumulator o) needs no further
+//    cross-lane traffic. GQA: a workgroup serves all G = H_q/H_kv query heads
+//    of its kv head, so each K/V byte is read once per G heads.
+//  * The 16 rows of a workgroup merge through LDS and write one partial
+//    (m, l, o[D]) per (seq, q head, chunk) into the workspace. Scores are kept
+//    in log2 units (log2(e) is folded into the query scale) so exp is a single
+//    v_exp_f32.
+//  * Pass 2, grid (q_head, seq): log-sum-exp merge of the chunk partials.
+#include "skv_common.h"
+
+namespace skv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRows = kThreads / 16;  // DPP rows per workgroup
+
+struct DecodeArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* lens;
+  const int32_t* block_table;
+  int max_blocks;
+  int bs_shift;
+  int Hq, Hkv, T_cap;
+  int cap;       // tokens a sequence can hold: T_cap, or max_blocks * block_size
+  float qscale;  // softmax scale * log2(e)
+  int chunk;
+  int n_chunks_max;
+  int q_dt;
+  float* ws_o;   // [B][Hq][n_chunks_max][D]
+  float* ws_ml;  // [B][Hq][n_chunks_max][2]  (m in log2 units, l)
+};
+
+template <typename TC, int D, bool PAGED>
+__device__ __forceinline__ const TC* row_ptr(const TC* base, const DecodeArgs& a, int b, int t,
+                                             int hk) {
+  size_t row;
+  if constexpr (PAGED) {
+    const int blk = a.block_table[(size_t)b * a.max_blocks + (t >> a.bs_shift)];
+    row = ((size_t)blk << a.bs_shift) + (t & ((1 << a.bs_shift) - 1));
+  } else {
+    row = (size_t)b * a.T_cap + t;
+  }
+  return base + (row * a.Hkv + hk) * D;
+}
+
+template <typename TC, int D, int G, int TPG, bool PAGED>
+__global__ __launch_bounds__(kThreads) void k_decode_partial(DecodeArgs a) {
+  constexpr int EPL = D / 16;
+  const int c = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  // Lengths beyond the capacity are clamped so no row outside the cache (or
+  // block table entry outside the table) is ever addressed.
+  const int len = min(a.lens[b], a.cap);
+  const int start = c * a.chunk;
+  if (start >= len) return;  // uniform over the workgroup
+  const int end = min(start + a.chunk, len);
+
+  const int tid = threadIdx.x;
+  const int rid = tid >> 4;  // DPP row (0..15)
+  const int li = tid & 15;   // lane within the row
+  const int e0 = li * EPL;
+
+  float q[G][EPL];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const size_t qoff = ((size_t)b * a.Hq + hk * G + h) * D + e0;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) q[h][e] = load_elem(a.q, qoff + e, a.q_dt) * a.qscale;
+  }
+
+  float m[G], l[G], acc[G][EPL];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[h][e] = 0.f;
+  }
+
+  const TC* kb = static_cast<const TC*>(a.k);
+  const TC* vb = static_cast<const TC*>(a.v);
+
+  for (int t0 = start + rid * TPG; t0 < end; t0 += kRows * TPG) {
+    Frag<TC, EPL> kf[TPG], vf[TPG];
+#pragma unroll
+    for (int u = 0; u < TPG; ++u) {
+      const int t = min(t0 + u, end - 1);  // clamp: masked below, never out of bounds
+      kf[u].load(row_ptr<TC, D, PAGED>(kb, a, b, t, hk) + e0);
+    }
+#pragma unroll
+    for (int u = 0; u < TPG; ++u) {
+      const int t = min(t0 + u, end - 1);
+      vf[u].load(row_ptr<TC, D, PAGED>(vb, a, b, t, hk) + e0);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float s[TPG];
+#pragma unroll
+      for (int u = 0; u < TPG; ++u) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) d = fmaf(q[h][e], kf[u].get(e), d);
+        d = row16_sum(d);
+        s[u] = (t0 + u < end) ? d : -INFINITY;
+      }
+      float mx = m[h];
+#pragma unroll
+      for (int u = 0; u < TPG; ++u) mx = fmaxf(mx, s[u]);
+      const float alpha = fast_exp2(m[h] - mx);  // 0 on the first tile (m = -inf)
+      m[h] = mx;
+      float ls = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[h][e] *= alpha;
+#pragma unroll
+      for (int u = 0; u < TPG; ++u) {
+        const float p = fast_exp2(s[u] - mx);
+        ls += p;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(p, vf[u].get(e), acc[h][e]);
+      }
+      l[h] = l[h] * alpha + ls;
+    }
+  }
+
+  // Merge the 16 rows of the workgroup, one query head at a time. Rows that
+  // saw no token keep m = -inf, l = 0, o = 0 and drop out through
+  // exp2(-inf) = 0.
+  __shared__ float sm_ml[kRows][2];
+  __shared__ float sm_o[kRows][D + 1];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    if (li == 0) {
+      sm_ml[rid][0] = m[h];
+      sm_ml[rid][1] = l[h];
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) sm_o[rid][e0 + e] = acc[h][e];
+    __syncthreads();
+    if (tid < D) {
+      const int d = tid;
+      float M = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) M = fmaxf(M, sm_ml[r][0]);
+      float L = 0.f, O = 0.f;
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) {
+        const float w = fast_exp2(sm_ml[r][0] - M);
+        L = fmaf(w, sm_ml[r][1], L);
+        O = fmaf(w, sm_o[r][d], O);
+      }
+      const size_t pidx = ((size_t)b * a.Hq + hk * G + h) * a.n_chunks_max + c;
+      a.ws_o[pidx * D + d] = O;
+      if (d == 0) {
+        a.ws_ml[pidx * 2 + 0] = M;
+        a.ws_ml[pidx * 2 + 1] = L;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Pass 2: grid (Hq, B), D threads. Merges ceil(len / chunk) partials.
+__global__ __launch_bounds__(128) void k_decode_merge(void* __restrict__ out, int out_dt,
+                                                      const int32_t* __restrict__ lens,
+                                                      const float* __restrict__ ws_o,
+                                                      const float* __restrict__ ws_ml, int Hq,
+                                                      int D, int chunk, int n_chunks_max,
+                                                      int cap) {
+  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  if (d >= D) return;
+  const size_t oidx = ((size_t)b * Hq + hq) * D + d;
+  const int len = min(lens[b], cap);
+  if (len <= 0) {
+    store_elem(out, oidx, out_dt, 0.f);
+    return;
+  }
+  const int nc = (len + chunk - 1) / chunk;
+  if (nc > n_chunks_max) {  // plan too small for this length: flag, never read past it
+    store_elem(out, oidx, out_dt, __builtin_nanf(""));
+    return;
+  }
+  const size_t base = ((size_t)b * Hq + hq) * n_chunks_max;
+  float M = -INFINITY;
+  for (int n = 0; n < nc; ++n) M = fmaxf(M, ws_ml[(base + n) * 2]);
+  float L = 0.f, O = 0.f;
+  for (int n = 0; n < nc; ++n) {
+    const float w = fast_exp2(ws_ml[(base + n) * 2] - M);
+    L = fmaf(w, ws_ml[(base + n) * 2 + 1], L);
+    O = fmaf(w, ws_o[(base + n) * D + d], O);
+  }
+  store_elem(out, oidx, out_dt, O / L);
+}
+
+template <typename TC, int D, int G, bool PAGED>
+void launch_partial(const DecodeArgs& a, int B, hipStream_t s) {
+  // 8 tokens per DPP row per iteration: 8 x 16 B in flight per lane for K and
+  // as many for V.
+  constexpr int TPG = (sizeof(TC) == 4 && D == 128) ? 4 : 8;
+  dim3 grid(a.n_chunks_max, a.Hkv, B);
+  hipLaunchKernelGGL((k_decode_partial<TC, D, G, TPG, PAGED>), grid, dim3(kThreads), 0, s, a);
+}
+
+template <typename TC, bool PAGED>
+int dispatch_partial(const DecodeArgs& a, int B, int D, int G, hipStream_t s) {
+#define SKV_DEC(DD, GG)                                    \
+  if (D == DD && G == GG) {                                \
+    launch_partial<TC, DD, GG, PAGED>(a, B, s);            \
+    return 0;                                              \
+  }
+  SKV_DEC(64, 1) SKV_DEC(64, 2) SKV_DEC(64, 4) SKV_DEC(64, 8)
+  SKV_DEC(128, 1) SKV_DEC(128, 2) SKV_DEC(128, 4) SKV_DEC(128, 8)
+#undef SKV_DEC
+  return set_error(SKV_E_UNSUPPORTED, "skv_decode_attn: no kernel for D=%d G=%d", D, G);
+}
+
+bool dt_ok(int dt) { return dt == SKV_F32 || dt == SKV_BF16; }
+
+int log2_exact(int x) {
+  if (x <= 0 || (x & (x - 1))) return -1;
+  int s = 0;
+  while ((1 << s) < x) ++s;
+  return s;
+}
+
+template <bool PAGED>
+int decode_common(void* out, const void* q, const void* k, const void* v, const int32_t* lens,
+                  const int32_t* bt, int max_blocks, int block_size, int B, int Hq, int Hkv,
+                  int D, int T_cap, float scale, int chunk, int n_chunks_max, void* ws,
+                  size_t ws_bytes, int cache_dt, int q_dt, int out_dt, hipStream_t s) {
+  const char* fn = PAGED ? "skv_decode_attn_paged" : "skv_decode_attn";
+  SKV_REQUIRE(out && q && k && v && lens && ws, SKV_E_INVALID, "%s: null pointer argument", fn);
+  SKV_REQUIRE(!PAGED || bt, SKV_E_INVALID, "%s: null block table", fn);
+  SKV_REQUIRE(B > 0 && Hq > 0 && Hkv > 0, SKV_E_INVALID, "%s: dims must be > 0", fn);
+  SKV_REQUIRE(PAGED || T_cap > 0, SKV_E_INVALID, "%s: T_cap must be > 0", fn);
+  SKV_REQUIRE(Hq % Hkv == 0, SKV_E_INVALID, "%s: H_q=%d not a multiple of H_kv=%d", fn, Hq, Hkv);
+  SKV_REQUIRE(D == 64 || D == 128, SKV_E_UNSUPPORTED, "%s: D=%d (supported: 64, 128)", fn, D);
+  SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(q_dt) && dt_ok(out_dt), SKV_E_INVALID, "%s: bad dtype",
+              fn);
+  SKV_REQUIRE(chunk > 0 && chunk % kThreads == 0, SKV_E_INVALID,
+              "%s: chunk_tokens=%d must be a positive multiple of %d", fn, chunk, kThreads);
+  SKV_REQUIRE(n_chunks_max > 0 && n_chunks_max <= 65535, SKV_E_INVALID,
+              "%s: n_chunks_max=%d out of range", fn, n_chunks_max);
+  const size_t need = skv_decode_workspace_bytes(B, Hq, D, n_chunks_max);
+  SKV_REQUIRE(ws_bytes >= need, SKV_E_WORKSPACE, "%s: workspace %zu bytes < %zu required", fn,
+              ws_bytes, need);
+  int shift = 0;
+  if (PAGED) {
+    shift = log2_exact(block_size);
+    SKV_REQUIRE(shift >= 0, SKV_E_INVALID, "%s: block_size=%d not a power of two", fn,
+                block_size);
+    SKV_REQUIRE(max_blocks > 0 && (long)max_blocks << shift < (1L << 31), SKV_E_INVALID,
+                "%s: max_blocks=%d out of range", fn, max_blocks);
+  }
+  DecodeArgs a;
+  a.q = q; a.k = k; a.v = v; a.lens = lens; a.block_table = bt;
+  a.max_blocks = max_blocks; a.bs_shift = shift;
+  a.Hq = Hq; a.Hkv = Hkv; a.T_cap = T_cap;
+  a.cap = PAGED ? (max_blocks << shift) : T_cap;
+  a.qscale = scale * LOG2E;
+  a.chunk = chunk; a.n_chunks_max = n_chunks_max; a.q_dt = q_dt;
+  const size_t o_elems = (size_t)B * Hq * n_chunks_max * D;
+  a.ws_o = static_cast<float*>(ws);
+  a.ws_ml = a.ws_o + o_elems;
+  const int G = Hq / Hkv;
+  int rc = cache_dt == SKV_BF16 ? dispatch_partial<uint16_t, PAGED>(a, B, D, G, s)
+                                : dispatch_partial<float, PAGED>(a, B, D, G, s);
+  if (rc) return rc;
+  rc = check_launch(fn);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_decode_merge, dim3(Hq, B), dim3(D), 0, s, out, out_dt, lens, a.ws_o,
+                     a.ws_ml, Hq, D, chunk, n_chunks_max, a.cap);
+  return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace skv
+
+using namespace skv;
+
+extern "C" int skv_decode_plan(int B, int H_kv, int max_len, int chunk_hint, int* chunk_tokens,
+                               int* n_chunks_max) {
+  SKV_REQUIRE(chunk_tokens && n_chunks_max, SKV_E_INVALID, "skv_decode_plan: null output");
+  SKV_REQUIRE(B > 0 && H_kv > 0 && max_len > 0, SKV_E_INVALID,
+              "skv_decode_plan: dims must be > 0 (B=%d H_kv=%d max_len=%d)", B, H_kv, max_len);
+  int chunk;
+  if (chunk_hint > 0) {
+    chunk = (chunk_hint + kThreads - 1) / kThreads * kThreads;
+  } else {
+    // Aim for >= 2048 workgroups (8 per CU on 256 CUs) without chunks
+    // shorter than one 256-token sweep of the workgroup, and no longer than
+    // 2048 tokens so long contexts still spread over every CU.
+    const long pairs = (long)B * H_kv;
+    const long target = 2048;
+    long per = ((long)max_len * pairs + target - 1) / target;
+    per = (per + kThreads - 1) / kThreads * kThreads;
+    if (per < kThreads) per = kThreads;
+    if (per > 2048) per = 2048;
+    chunk = (int)per;
+  }
+  const int n = (max_len + chunk - 1) / chunk;
+  SKV_REQUIRE(n <= 65535, SKV_E_UNSUPPORTED, "skv_decode_plan: %d chunks exceed the grid limit",
+              n);
+  *chunk_tokens = chunk;
+  *n_chunks_max = n;
+  return SKV_OK;
+}
+
+extern "C" size_t skv_decode_workspace_bytes(int B, int H_q, int D, int n_chunks_max) {
+  if (B <= 0 || H_q <= 0 || D <= 0 || n_chunks_max <= 0) return 0;
+  const size_t parts = (size_t)B * H_q * n_chunks_max;
+  return parts * (size_t)(D + 2) * sizeof(float);
+}
+
+extern "C" int skv_decode_attn(void* out, const void* q, const void* k_cache, const void* v_cache,
+                               const int32_t* lens, int B, int H_q, int H_kv, int D, int T_cap,
+                               float scale, int chunk_tokens, int n_chunks_max, void* ws,
+                               size_t ws_bytes, int cache_dt, int q_dt, int out_dt,
+                               skv_stream_t stream) {
+  return decode_common<false>(out, q, k_cache, v_cache, lens, nullptr, 0, 0, B, H_q, H_kv, D,
+                              T_cap, scale, chunk_tokens, n_chunks_max, ws, ws_bytes, cache_dt,
+                              q_dt, out_dt, (hipStream_t)stream);
+}
+
+extern "C" int skv_decode_attn_paged(void* out, const void* q, const void* k_pool,
+                                     const void* v_pool, const int32_t* lens,
+                                     const int32_t* block_table, int max_blocks, int block_size,
+                                     int B, int H_q, int H_kv, int D, float scale,
+                                     int chunk_tokens, int n_chunks_max, void* ws,
+                                     size_t ws_bytes, int cache_dt, int q_dt, int out_dt,
+                                     skv_stream_t stream) {
+  return decode_common<true>(out, q, k_pool, v_pool, lens, block_table, max_blocks, block_size, B,
+                             H_q, H_kv, D, 0, scale, chunk_tokens, n_chunks_max, ws, ws_bytes,
+                             cache_dt, q_dt, out_dt, (hipStream_t)stream);
+}

@@ -1,0 +1,152 @@
+// Shared device helpers for the simple-kv (skv) HIP kernels on gfx950 (CDNA4).
+//
+// Storage types: fp32 (`float`) and bf16 (raw `uint16_t`, round-to-nearest-even
+// on store). All arithmetic is fp32. Cross-lane reductions use DPP row
+// operations, which stay inside one 16-lane row of a 64-lane wavefront.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "skv.h"
+
+namespace skv {
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32
+// ---------------------------------------------------------------------------
+
+// fp32 -> bf16 with round-to-nearest-even; NaN maps to a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+
+// A 32-bit word holding two bf16 values: element 0 in bits 0..15, element 1
+// in bits 16..31 (little-endian memory order).
+__device__ __forceinline__ float bf16w_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16w_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// ---------------------------------------------------------------------------
+// Per-lane fragments of one K/V row.
+//
+// A token row of D elements is split over the 16 lanes of a DPP row: lane i
+// owns elements [i*EPL, (i+1)*EPL), EPL = D/16. Frag<TC, EPL> keeps the raw
+// words (so bf16 rows stay packed in registers until use) and converts one
+// element at a time.
+// ---------------------------------------------------------------------------
+
+template <typename TC, int EPL>
+struct Frag;
+
+template <int EPL>
+struct Frag<float, EPL> {
+  static constexpr int NW = EPL;  // 32-bit words
+  uint32_t w[NW];
+  __device__ __forceinline__ void load(const float* p) {
+    static_assert(EPL % 4 == 0, "fp32 fragment must be a multiple of 16 bytes");
+#pragma unroll
+    for (int i = 0; i < NW / 4; ++i) {
+      uint4 x = reinterpret_cast<const uint4*>(p)[i];
+      w[4 * i + 0] = x.x; w[4 * i + 1] = x.y; w[4 * i + 2] = x.z; w[4 * i + 3] = x.w;
+    }
+  }
+  __device__ __forceinline__ float get(int e) const { return __uint_as_float(w[e]); }
+};
+
+template <int EPL>
+struct Frag<uint16_t, EPL> {
+  static constexpr int NW = EPL / 2;
+  uint32_t w[NW];
+  __device__ __forceinline__ void load(const uint16_t* p) {
+    if constexpr (NW % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < NW / 4; ++i) {
+        uint4 x = reinterpret_cast<const uint4*>(p)[i];
+        w[4 * i + 0] = x.x; w[4 * i + 1] = x.y; w[4 * i + 2] = x.z; w[4 * i + 3] = x.w;
+      }
+    } else {
+      static_assert(NW == 2, "bf16 fragment must be 8 or a multiple of 16 bytes");
+      uint2 x = *reinterpret_cast<const uint2*>(p);
+      w[0] = x.x; w[1] = x.y;
+    }
+  }
+  __device__ __forceinline__ float get(int e) const {
+    return (e & 1) ? bf16w_hi(w[e >> 1]) : bf16w_lo(w[e >> 1]);
+  }
+};
+
+// Element loads/stores with runtime dtype (used off the hot loops).
+__device__ __forceinline__ float load_elem(const void* p, size_t i, int dt) {
+  return dt == SKV_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i])
+                        : static_cast<const float*>(p)[i];
+}
+__device__ __forceinline__ void store_elem(void* p, size_t i, int dt, float v) {
+  if (dt == SKV_BF16) static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  else static_cast<float*>(p)[i] = v;
+}
+
+// ---------------------------------------------------------------------------
+// DPP reductions over one 16-lane row. Every lane of the row ends with the
+// same bit pattern: each step combines a lane with a partner that holds the
+// mirror-image partial, and fp add/max are commutative.
+//   quad_perm [1,0,3,2]  partner = lane ^ 1
+//   quad_perm [2,3,0,1]  partner = lane ^ 2
+//   row_half_mirror      partner = 7 - lane (within each half-row)
+//   row_mirror           partner = 15 - lane
+// ---------------------------------------------------------------------------
+
+constexpr int DPP_QUAD_XOR1 = 0xB1;
+constexpr int DPP_QUAD_XOR2 = 0x4E;
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+constexpr int DPP_ROW_NEWBCAST0 = 0x150;  // + lane: broadcast lane n of each row
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp<DPP_QUAD_XOR1>(x);
+  x += dpp<DPP_QUAD_XOR2>(x);
+  x += dpp<DPP_ROW_HALF_MIRROR>(x);
+  x += dpp<DPP_ROW_MIRROR>(x);
+  return x;
+}
+
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp<DPP_QUAD_XOR1>(x));
+  x = fmaxf(x, dpp<DPP_QUAD_XOR2>(x));
+  x = fmaxf(x, dpp<DPP_ROW_HALF_MIRROR>(x));
+  x = fmaxf(x, dpp<DPP_ROW_MIRROR>(x));
+  return x;
+}
+
+// 2^x on the hardware exp unit (v_exp_f32). exp2(-inf) = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+
+}  // namespace skv
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting shared by every C entry point.
+// ---------------------------------------------------------------------------
+namespace skv {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace skv
+
+#define SKV_REQUIRE(cond, code, ...)                          \
+  do {                                                        \
+    if (!(cond)) return ::skv::set_error((code), __VA_ARGS__); \
+  } while (0)

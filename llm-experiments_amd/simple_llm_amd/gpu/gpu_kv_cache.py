@@ -1,0 +1,309 @@
+"""KV-cache management and cached attention on gfx950.
+
+Drop-in for simple-llm/src/gpu/gpu_kv_cache.py: same functions, arguments,
+checks and error messages:
+  kv_cache_create          gpu_kv_cache.py:26-87
+  kv_cache_reset           gpu_kv_cache.py:90-105
+  kv_cache_update          gpu_kv_cache.py:113-186
+  attention_with_kv_cache  gpu_kv_cache.py:194-289
+The work is done by hand-written HIP kernels behind the C ABI in
+include/skv.h (append: skv_append; attention: skv_decode_attn). There is no
+CPU path: without libskv.so every call raises.
+
+Differences from the reference, all supersets of its behaviour:
+  * lengths are per layer and per sequence, kept on the device and advanced
+    by the append kernel (see KVCache in gpu_types.py for the position rule);
+  * decode attention has no length cap (the reference raises above
+    attention_workgroup_size = 256, gpu_kv_cache.py:250-257);
+  * bf16 storage, grouped-query heads and a paged layout are options of
+    KVCacheConfig; the defaults reproduce the reference's fp32 MHA cache.
+
+Extensions beyond the reference's four functions:
+  kv_cache_append           append with per-sequence positions (no
+                            full-cache error: full sequences are skipped)
+  kv_cache_set_block_table  install the page table of a paged cache
+  kv_cache_prefill          append a chunk of tokens (prefill), optionally
+                            followed by causal attention over prefix + chunk
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional
+
+import numpy as np
+import torch
+
+from .. import _lib
+from .gpu_ops import batch_count, validate_buffer_shape_2d
+from .gpu_types import (
+    GPUBuffer2D,
+    GPUContext,
+    KVCache,
+    KVCacheConfig,
+    KVCacheLayer,
+)
+
+# ============================================================================
+# KV-CACHE CREATION
+# ============================================================================
+
+
+def kv_cache_create(ctx: GPUContext, config: KVCacheConfig) -> KVCache:
+    """Allocate zero-filled K/V storage for every layer; current_len = 0.
+
+    Same validation as the reference (gpu_kv_cache.py:55-64). Contiguous
+    caches are [batch_size * max_seq_len, n_kv_heads * head_dim] per tensor;
+    paged caches are a pool [n_blocks * block_size, n_kv_heads * head_dim]
+    whose page table starts as the identity mapping (sequence b owns pages
+    b*max_blocks .. b*max_blocks + max_blocks - 1) when the pool is big enough.
+    """
+    if config.batch_size <= 0:
+        raise ValueError(f"batch_size must be > 0, got {config.batch_size}")
+    if config.max_seq_len <= 0:
+        raise ValueError(f"max_seq_len must be > 0, got {config.max_seq_len}")
+    if config.n_layers <= 0:
+        raise ValueError(f"n_layers must be > 0, got {config.n_layers}")
+    if config.n_heads <= 0:
+        raise ValueError(f"n_heads must be > 0, got {config.n_heads}")
+    if config.head_dim <= 0:
+        raise ValueError(f"head_dim must be > 0, got {config.head_dim}")
+    n_kv = config.n_kv_heads or config.n_heads
+    if n_kv <= 0 or config.n_heads % n_kv != 0:
+        raise ValueError(f"n_heads ({config.n_heads}) must be a multiple of n_kv_heads ({n_kv})")
+    if config.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"dtype must be torch.float32 or torch.bfloat16, got {config.dtype}")
+    if config.head_dim % 8 != 0:
+        raise ValueError(f"head_dim must be a multiple of 8, got {config.head_dim}")
+
+    e_kv = n_kv * config.head_dim
+    B = config.batch_size
+    block_table = None
+    n_blocks = 0
+    if config.block_size > 0:
+        bs = config.block_size
+        if bs & (bs - 1):
+            raise ValueError(f"block_size must be a power of two, got {bs}")
+        max_blocks = -(-config.max_seq_len // bs)
+        n_blocks = config.n_blocks or B * max_blocks
+        rows = n_blocks * bs
+        ident = torch.arange(B * max_blocks, dtype=torch.int32).reshape(B, max_blocks)
+        if n_blocks < B * max_blocks:
+            ident = ident % n_blocks  # placeholder: caller installs a real table
+        block_table = ident.to(ctx.device)
+    else:
+        rows = B * config.max_seq_len
+
+    layers: List[KVCacheLayer] = []
+    for _ in range(config.n_layers):
+        k = torch.zeros((rows, e_kv), dtype=config.dtype, device=ctx.device)
+        v = torch.zeros((rows, e_kv), dtype=config.dtype, device=ctx.device)
+        layers.append(KVCacheLayer(
+            k_cache=GPUBuffer2D(buffer=k, shape=(rows, e_kv), size=rows * e_kv),
+            v_cache=GPUBuffer2D(buffer=v, shape=(rows, e_kv), size=rows * e_kv),
+            lens=torch.zeros(B, dtype=torch.int32, device=ctx.device),
+            host_lens=np.zeros(B, dtype=np.int64)))
+
+    return KVCache(layers=layers, batch_size=B, max_seq_len=config.max_seq_len, current_len=0,
+                   n_heads=config.n_heads, head_dim=config.head_dim, n_kv_heads=n_kv,
+                   dtype=config.dtype, block_size=config.block_size, n_blocks=n_blocks,
+                   block_table=block_table)
+
+
+def kv_cache_reset(cache: KVCache) -> None:
+    """Empty the cache without touching its contents (reference :90-105)."""
+    cache.current_len = 0
+
+
+def kv_cache_set_block_table(cache: KVCache, block_table: torch.Tensor) -> None:
+    """Install a page table [batch_size, ceil(max_seq_len / block_size)] of pool page ids."""
+    if not cache.paged:
+        raise ValueError("kv_cache_set_block_table: cache is not paged")
+    max_blocks = -(-cache.max_seq_len // cache.block_size)
+    if tuple(block_table.shape) != (cache.batch_size, max_blocks):
+        raise ValueError(f"block_table shape mismatch: got {tuple(block_table.shape)}, "
+                         f"expected {(cache.batch_size, max_blocks)}")
+    host = block_table.detach().to("cpu")
+    if host.numel() and (int(host.min()) < 0 or int(host.max()) >= cache.n_blocks):
+        raise ValueError(f"block_table entries must lie in [0, {cache.n_blocks})")
+    cache.block_table = block_table.to(device=cache.layers[0].lens.device,
+                                       dtype=torch.int32).contiguous()
+
+
+# ============================================================================
+# KV-CACHE UPDATE
+# ============================================================================
+
+
+def _check_layer(cache: KVCache, layer_idx: int) -> None:
+    if layer_idx < 0 or layer_idx >= len(cache.layers):
+        raise ValueError(f"layer_idx {layer_idx} out of range [0, {len(cache.layers)})")
+
+
+def _check_tensor(t: torch.Tensor, name: str, device: torch.device) -> None:
+    # Kernels dereference these pointers on the GPU: host tensors never reach them.
+    if device.type != "cuda" or not t.is_cuda:
+        raise ValueError(f"{name}: the KV cache and its operands must live on the ROCm "
+                         f"device (cache on {device}, {name} on {t.device})")
+    if t.device.index != (device.index or 0):
+        raise ValueError(f"{name} must live on {device}, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.data_ptr() % 16:
+        raise ValueError(f"{name} must be 16-byte aligned")
+
+
+def _launch_append(ctx: GPUContext, cache: KVCache, layer: KVCacheLayer, k: torch.Tensor,
+                   v: torch.Tensor) -> None:
+    dev = layer.lens.device
+    for t, n in ((k, "new_k"), (v, "new_v")):
+        _check_tensor(t, n, dev)
+    if k.dtype != v.dtype:
+        raise ValueError("new_k and new_v must share a dtype")
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    cdt, idt = _lib.dtype_code(cache.dtype), _lib.dtype_code(k.dtype)
+    if cache.paged:
+        max_blocks = cache.block_table.shape[1]
+        rc = L.skv_append_paged(layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr(),
+                                k.data_ptr(), v.data_ptr(), layer.lens.data_ptr(),
+                                cache.block_table.data_ptr(), max_blocks, cache.block_size,
+                                cache.batch_size, cache.n_kv_heads, cache.head_dim, cdt, idt,
+                                stream)
+    else:
+        rc = L.skv_append(layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr(),
+                          k.data_ptr(), v.data_ptr(), layer.lens.data_ptr(), cache.batch_size,
+                          cache.n_kv_heads, cache.head_dim, cache.max_seq_len, cdt, idt, stream)
+    _lib.check(rc, "skv_append")
+    # mirror the kernel's rule: write and advance where pos < capacity
+    cap = cache.block_table.shape[1] * cache.block_size if cache.paged else cache.max_seq_len
+    layer.host_lens = np.where(layer.host_lens < cap, layer.host_lens + 1, layer.host_lens)
+
+
+def kv_cache_update(ctx: GPUContext, cache: KVCache, layer_idx: int, new_k: GPUBuffer2D,
+                    new_v: GPUBuffer2D) -> None:
+    """Append one token per sequence to one layer (reference :113-186).
+
+    new_k, new_v: [batch_size, n_kv_heads * head_dim]. Raises ValueError on a
+    bad layer index, a full cache or a shape mismatch, before any GPU work.
+    The layer's fill advances by one.
+    """
+    _check_layer(cache, layer_idx)
+    layer = cache.layers[layer_idx]
+    cur = int(layer.host_lens.max())
+    if cur >= cache.max_seq_len:
+        raise ValueError(
+            f"Cache is full: current_len={cur}, max_seq_len={cache.max_seq_len}")
+    e_kv = cache.n_kv_heads * cache.head_dim
+    expected_rows = cache.batch_size * 1
+    validate_buffer_shape_2d(new_k, (expected_rows, e_kv), "new_k")
+    validate_buffer_shape_2d(new_v, (expected_rows, e_kv), "new_v")
+    batch_count(ctx)
+    _launch_append(ctx, cache, layer, new_k.buffer, new_v.buffer)
+
+
+def kv_cache_append(ctx: GPUContext, cache: KVCache, layer_idx: int, new_k: torch.Tensor,
+                    new_v: torch.Tensor) -> np.ndarray:
+    """Per-sequence append (extension): sequence b writes at its own fill.
+
+    new_k, new_v: tensors of [batch_size, n_kv_heads, head_dim] (or
+    [batch_size, n_kv_heads * head_dim]). Sequences that are already full are
+    skipped (retired). Returns the host mirror of the new fills.
+    """
+    _check_layer(cache, layer_idx)
+    e_kv = cache.n_kv_heads * cache.head_dim
+    for t, n in ((new_k, "new_k"), (new_v, "new_v")):
+        if t.numel() != cache.batch_size * e_kv:
+            raise ValueError(f"{n} must hold batch_size*n_kv_heads*head_dim = "
+                             f"{cache.batch_size * e_kv} elements, got {t.numel()}")
+    batch_count(ctx)
+    layer = cache.layers[layer_idx]
+    _launch_append(ctx, cache, layer, new_k, new_v)
+    return layer.host_lens.copy()
+
+
+# ============================================================================
+# ATTENTION WITH KV-CACHE
+# ============================================================================
+
+
+def _workspace(ctx: GPUContext, nbytes: int) -> torch.Tensor:
+    ws = ctx.decode_workspace
+    if ws is None or ws.numel() < nbytes or ws.device != ctx.device:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=ctx.device)
+        ctx.decode_workspace = ws
+    return ws
+
+
+def decode_plan(ctx: GPUContext, batch_size: int, n_kv_heads: int,
+                max_len: int) -> tuple[int, int]:
+    """(chunk_tokens, n_chunks_max) of the split-K decode for these sizes."""
+    L = _lib.lib()
+    c, n = ctypes.c_int(), ctypes.c_int()
+    rc = L.skv_decode_plan(batch_size, n_kv_heads, max(int(max_len), 1),
+                           int(ctx.config.decode_chunk_tokens), ctypes.byref(c), ctypes.byref(n))
+    _lib.check(rc, "skv_decode_plan")
+    return c.value, n.value
+
+
+def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.Tensor,
+                     out: torch.Tensor, scale: Optional[float] = None,
+                     max_len: Optional[int] = None) -> None:
+    """Single-query attention of every sequence over its filled prefix.
+
+    q, out: contiguous device tensors of [batch_size, n_heads, head_dim]
+    elements (float32 or bfloat16). max_len: an upper bound of the fills
+    (default: the host mirror's maximum), used to size the split-K grid.
+    """
+    layer = cache.layers[layer_idx]
+    dev = layer.lens.device
+    _check_tensor(q, "q_new", dev)
+    _check_tensor(out, "output", dev)
+    e_q = cache.n_heads * cache.head_dim
+    if q.numel() != cache.batch_size * e_q or out.numel() != cache.batch_size * e_q:
+        raise ValueError(f"q_new/output must hold batch_size*n_heads*head_dim = "
+                         f"{cache.batch_size * e_q} elements")
+    if max_len is None:
+        max_len = int(layer.host_lens.max())
+    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_kv_heads, max_len)
+    L = _lib.lib()
+    need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
+    ws = _workspace(ctx, need)
+    sc = float(scale) if scale is not None else 1.0 / float(np.sqrt(cache.head_dim))
+    stream = _lib.stream_handle(dev)
+    cdt, qdt, odt = (_lib.dtype_code(cache.dtype), _lib.dtype_code(q.dtype),
+                     _lib.dtype_code(out.dtype))
+    if cache.paged:
+        rc = L.skv_decode_attn_paged(out.data_ptr(), q.data_ptr(), layer.k_cache.buffer.data_ptr(),
+                                     layer.v_cache.buffer.data_ptr(), layer.lens.data_ptr(),
+                                     cache.block_table.data_ptr(), cache.block_table.shape[1],
+                                     cache.block_size, cache.batch_size, cache.n_heads,
+                                     cache.n_kv_heads, cache.head_dim, sc, chunk, nchunks,
+                                     ws.data_ptr(), ws.numel(), cdt, qdt, odt, stream)
+    else:
+        rc = L.skv_decode_attn(out.data_ptr(), q.data_ptr(), layer.k_cache.buffer.data_ptr(),
+                               layer.v_cache.buffer.data_ptr(), layer.lens.data_ptr(),
+                               cache.batch_size, cache.n_heads, cache.n_kv_heads, cache.head_dim,
+                               cache.max_seq_len, sc, chunk, nchunks, ws.data_ptr(), ws.numel(),
+                               cdt, qdt, odt, stream)
+    _lib.check(rc, "skv_decode_attn")
+
+
+def attention_with_kv_cache(ctx: GPUContext, cache: KVCache, layer_idx: int, q_new: GPUBuffer2D,
+                            output: GPUBuffer2D) -> None:
+    """Attention of the newest query over the cached K/V (reference :194-289).
+
+    q_new, output: [batch_size, n_heads * head_dim]. Sequence b attends
+    positions [0, fill_b) of layer layer_idx, which include the token the
+    last update appended. Raises ValueError on a bad layer index, an empty
+    layer or a shape mismatch. No length cap.
+    """
+    _check_layer(cache, layer_idx)
+    layer = cache.layers[layer_idx]
+    if int(layer.host_lens.max()) == 0:
+        raise ValueError("Cache is empty: current_len=0")
+    e_q = cache.n_heads * cache.head_dim
+    expected_q_rows = cache.batch_size * 1
+    validate_buffer_shape_2d(q_new, (expected_q_rows, e_q), "q_new")
+    validate_buffer_shape_2d(output, (expected_q_rows, e_q), "output")
+    batch_count(ctx)
+    decode_attention(ctx, cache, layer_idx, q_new.buffer, output.buffer)

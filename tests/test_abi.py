@@ -1,0 +1,91 @@
+"""The C ABI library loads, exports what include/skv.h declares and rejects
+bad arguments before any device work. CPU only: no call here reaches a
+kernel launch."""
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+from simple_llm_amd import _lib
+
+
+def test_library_exports_every_header_function():
+    names = _lib.header_functions()
+    assert len(names) >= 10
+    L = _lib.lib()
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, f"libskv.so lacks {missing}"
+    # the ctypes signature table covers the header exactly
+    assert sorted(names) == sorted(_lib._SIGNATURES)
+
+
+def test_version():
+    assert _lib.lib().skv_version() == 100
+
+
+def _plan(B, Hkv, max_len, hint=0):
+    c, n = ctypes.c_int(), ctypes.c_int()
+    rc = _lib.lib().skv_decode_plan(B, Hkv, max_len, hint, ctypes.byref(c), ctypes.byref(n))
+    return rc, c.value, n.value
+
+
+@pytest.mark.parametrize("B,Hkv,L", [(4, 16, 32256), (8, 8, 2048), (64, 8, 8192), (1, 1, 1),
+                                     (16, 12, 1024), (1, 4, 256)])
+def test_decode_plan_covers_every_length(B, Hkv, L):
+    rc, chunk, n = _plan(B, Hkv, L)
+    assert rc == 0
+    assert chunk % 256 == 0 and 256 <= chunk <= 2048
+    assert n * chunk >= L > (n - 1) * chunk
+
+
+def test_decode_plan_hint_and_errors():
+    rc, chunk, n = _plan(4, 16, 32768, hint=1000)
+    assert rc == 0 and chunk == 1024 and n == 32
+    assert _plan(0, 16, 100)[0] == _lib.SKV_E_INVALID
+    assert _plan(4, 16, 0)[0] == _lib.SKV_E_INVALID
+    assert b"dims must be > 0" in _lib.lib().skv_last_error()
+
+
+def test_workspace_bytes():
+    L = _lib.lib()
+    assert L.skv_decode_workspace_bytes(4, 16, 128, 32) == 4 * 16 * 32 * (128 + 2) * 4
+    assert L.skv_decode_workspace_bytes(0, 16, 128, 32) == 0
+
+
+def test_entry_points_reject_bad_arguments():
+    L = _lib.lib()
+    fake = 4096  # never dereferenced: each call below fails validation first
+    rc = L.skv_append(None, None, None, None, None, 2, 4, 64, 128, 0, 0, None)
+    assert rc == _lib.SKV_E_INVALID
+    rc = L.skv_append(fake, fake, fake, fake, fake, 2, 4, 64, 128, 7, 0, None)
+    assert rc == _lib.SKV_E_INVALID and b"dtype" in L.skv_last_error()
+    rc = L.skv_append_paged(fake, fake, fake, fake, fake, fake, 4, 12, 2, 4, 64, 0, 0, None)
+    assert rc == _lib.SKV_E_INVALID and b"power of two" in L.skv_last_error()
+    ws = L.skv_decode_workspace_bytes(2, 4, 64, 1)
+    args = dict(B=2, Hq=4, Hkv=4, D=64, T=128, scale=0.125, chunk=256, n=1)
+
+    def dec(**kw):
+        a = {**args, **kw}
+        return L.skv_decode_attn(fake, fake, fake, fake, fake, a["B"], a["Hq"], a["Hkv"], a["D"],
+                                 a["T"], a["scale"], a["chunk"], a["n"], fake,
+                                 kw.get("ws", ws), 0, 0, 0, None)
+
+    assert dec(D=96) == _lib.SKV_E_UNSUPPORTED
+    assert dec(Hq=6, Hkv=4) == _lib.SKV_E_INVALID
+    assert dec(chunk=100) == _lib.SKV_E_INVALID
+    assert dec(ws=ws - 1) == _lib.SKV_E_WORKSPACE
+    ws48 = L.skv_decode_workspace_bytes(2, 48, 64, 1)
+    assert dec(Hq=48, Hkv=3, ws=ws48) == _lib.SKV_E_UNSUPPORTED  # G = 16 has no kernel
+    rc = L.skv_append_chunk(fake, fake, fake, fake, fake, None, 2, 0, 4, 64, 128, 0, 0, None)
+    assert rc == _lib.SKV_E_INVALID
+    assert L.skv_advance(None, None, 1, 2, 128, None) == _lib.SKV_E_INVALID
+
+
+def test_check_maps_status_to_exceptions():
+    L = _lib.lib()
+    L.skv_append(None, None, None, None, None, 1, 1, 64, 1, 0, 0, None)
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.check(_lib.SKV_E_INVALID, "x")
+    with pytest.raises(_lib.SkvError):
+        _lib.check(_lib.SKV_E_HIP, "x")

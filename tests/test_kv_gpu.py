@@ -1,0 +1,418 @@
+"""Parity of the HIP KV-cache path (append + split-K decode attention) with the
+CPU oracle, through the drop-in API and the C ABI. Needs the MI355X.
+
+Tolerances (the north star's): outputs within 1e-4 relative error for fp32
+storage and 2e-2 for bf16 storage with fp32 accumulation, relative error
+taken norm-wise per (sequence, head) against the float64 oracle fed the same
+(bf16-rounded) K/V. Positions, lengths and appended cache bytes: bit-exact.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, banner
+from oracle import kv_oracle as ko
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+def _gpu():
+    from simple_llm_amd.gpu import gpu
+    return gpu
+
+
+def rel_err(got: np.ndarray, want: np.ndarray) -> float:
+    """max over (b, h) of ||got - want|| / ||want|| (last axis = head_dim)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    num = np.linalg.norm(got - want, axis=-1)
+    den = np.maximum(np.linalg.norm(want, axis=-1), 1e-30)
+    return float((num / den).max())
+
+
+def to_dev(x: np.ndarray, dtype=torch.float32, dev="cuda"):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev).to(dtype)
+
+
+def cache_host(layer, cache, dtype=np.float32):
+    """Device cache of one layer as a host array [B, T_cap, Hkv, D] (or pool)."""
+    k = layer.k_cache.buffer.detach().float().cpu().numpy()
+    v = layer.v_cache.buffer.detach().float().cpu().numpy()
+    shp = (-1, cache.n_kv_heads, cache.head_dim)
+    if not cache.paged:
+        shp = (cache.batch_size, cache.max_seq_len) + shp[1:]
+    return k.reshape(shp), v.reshape(shp)
+
+
+# ---------------------------------------------------------------------------
+# The reference's own KV test, replayed through the drop-in API
+# ---------------------------------------------------------------------------
+
+
+def test_reference_kv_cache_operations(gpu_ctx):
+    """test_kv_cache_operations (simple-llm/src/gpu_test.py:2200-2406)."""
+    banner("reference kv_cache_operations KAT")
+    gpu = _gpu()
+    ctx = gpu_ctx
+    z = np.load(os.path.join(GOLDEN, "kv_kat_seed42.npz"))
+    B, T_cap, n_layers, H, D = (int(x) for x in z["config"])
+    E = H * D
+    cache = gpu.kv_cache_create(ctx, gpu.KVCacheConfig(batch_size=B, max_seq_len=T_cap,
+                                                       n_layers=n_layers, n_heads=H, head_dim=D))
+    assert len(cache.layers) == n_layers
+    assert cache.current_len == 0
+    cache.current_len = 50
+    gpu.kv_cache_reset(cache)
+    assert cache.current_len == 0
+    for step in range(1, 6):
+        k = gpu.gpu_buffer_2d_create(ctx, B, E, z["k_steps"][step - 1].reshape(B, E))
+        v = gpu.gpu_buffer_2d_create(ctx, B, E, z["v_steps"][step - 1].reshape(B, E))
+        gpu.batch_begin(ctx)
+        gpu.kv_cache_update(ctx, cache, 0, k, v)
+        gpu.batch_commit(ctx)
+        assert cache.current_len == step
+    q = gpu.gpu_buffer_2d_create(ctx, B, E, z["q"].reshape(B, E))
+    o = gpu.gpu_buffer_2d_create(ctx, B, E)
+    gpu.batch_begin(ctx)
+    gpu.attention_with_kv_cache(ctx, cache, 0, q, o)
+    gpu.batch_commit(ctx)
+    out = np.zeros((B, E), np.float32)
+    gpu.gpu_buffer_2d_read(ctx, o, out)
+    want = z["expected_o"].reshape(B, E)
+    # the reference's own comparison (gpu_test.py:83-85, :2431) and the north star's
+    assert np.allclose(out, want, rtol=1e-4, atol=1e-3)
+    assert rel_err(out.reshape(B, H, D), want.reshape(B, H, D)) < FP32_TOL
+    # device lengths and cache bytes: bit-exact against the oracle's scatter
+    assert cache.layers[0].lens.cpu().tolist() == [5, 5]
+    assert cache.layers[1].lens.cpu().tolist() == [0, 0]
+    kc, vc = cache_host(cache.layers[0], cache)
+    kw = np.zeros_like(kc)
+    vw = np.zeros_like(vc)
+    lens = np.zeros(B, np.int64)
+    for s in range(5):
+        lens = ko.append(kw, vw, z["k_steps"][s], z["v_steps"][s], lens)
+    np.testing.assert_array_equal(kc, kw)
+    np.testing.assert_array_equal(vc, vw)
+
+
+def test_update_errors_match_reference(gpu_ctx):
+    gpu = _gpu()
+    ctx = gpu_ctx
+    cache = gpu.kv_cache_create(ctx, gpu.KVCacheConfig(2, 3, 1, 2, 64))
+    E = 128
+    k = gpu.gpu_buffer_2d_create(ctx, 2, E)
+    with pytest.raises(ValueError, match="out of range"):
+        gpu.kv_cache_update(ctx, cache, 1, k, k)
+    with pytest.raises(ValueError, match="Cache is empty"):
+        gpu.attention_with_kv_cache(ctx, cache, 0, k, k)
+    with pytest.raises(ValueError, match="new_k shape mismatch"):
+        gpu.kv_cache_update(ctx, cache, 0, gpu.gpu_buffer_2d_create(ctx, 1, E), k)
+    for _ in range(3):
+        gpu.kv_cache_update(ctx, cache, 0, k, k)
+    with pytest.raises(ValueError, match="Cache is full"):
+        gpu.kv_cache_update(ctx, cache, 0, k, k)
+    gpu.batch_begin(ctx)
+    gpu.batch_commit(ctx)
+    with pytest.raises(RuntimeError, match="Batch already submitted"):
+        gpu.batch_commit(ctx)
+
+
+# ---------------------------------------------------------------------------
+# Append: bit-exact
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("cache_dt,in_dt", [(torch.float32, torch.float32),
+                                            (torch.bfloat16, torch.float32),
+                                            (torch.bfloat16, torch.bfloat16),
+                                            (torch.float32, torch.bfloat16)])
+@pytest.mark.parametrize("paged", [False, True])
+def test_append_bit_exact(gpu_ctx, cache_dt, in_dt, paged):
+    banner(f"append cache={cache_dt} in={in_dt} paged={paged}")
+    gpu = _gpu()
+    ctx = gpu_ctx
+    rng = np.random.default_rng(7)
+    B, T, Hkv, D = 5, 48, 2, 128
+    cfg = gpu.KVCacheConfig(B, T, 1, 2 * Hkv, D, n_kv_heads=Hkv, dtype=cache_dt,
+                            block_size=16 if paged else 0)
+    cache = gpu.kv_cache_create(ctx, cfg)
+    if paged:
+        table = rng.permutation(cache.n_blocks).reshape(B, -1).astype(np.int32)
+        gpu.kv_cache_set_block_table(cache, torch.from_numpy(table))
+    start = np.array([0, 7, 47, 48, 20])
+    cache.layers[0].lens.copy_(torch.from_numpy(start.astype(np.int32)))
+    cache.layers[0].host_lens[:] = start
+    kw = np.zeros((B, T, Hkv, D), np.float32)
+    vw = np.zeros_like(kw)
+    lens = start.copy()
+    sdt = "bf16" if cache_dt == torch.bfloat16 else "fp32"
+    for _ in range(3):
+        k = rng.standard_normal((B, Hkv, D)).astype(np.float32) * 3
+        v = rng.standard_normal((B, Hkv, D)).astype(np.float32)
+        if in_dt == torch.bfloat16:  # the input itself is bf16
+            k, v = ko.bf16_round(k), ko.bf16_round(v)
+        host = gpu.kv_cache_append(ctx, cache, 0, to_dev(k, in_dt), to_dev(v, in_dt))
+        lens = ko.append(kw, vw, k, v, lens, dtype=sdt)
+        np.testing.assert_array_equal(host, lens)
+    np.testing.assert_array_equal(cache.layers[0].lens.cpu().numpy(), lens)
+    kc, vc = cache_host(cache.layers[0], cache)
+    if paged:
+        kc = ko.paged_gather(kc, table, lens, 16, T)
+        vc = ko.paged_gather(vc, table, lens, 16, T)
+        for b in range(B):
+            kw[b, lens[b]:] = 0
+            vw[b, lens[b]:] = 0
+    np.testing.assert_array_equal(kc, kw)
+    np.testing.assert_array_equal(vc, vw)
+
+
+def test_append_chunk_and_advance(gpu_ctx):
+    from simple_llm_amd import _lib
+    banner("append_chunk + advance")
+    rng = np.random.default_rng(3)
+    B, T, H, D, C = 3, 40, 2, 64, 9
+    kc = torch.zeros((B, T, H, D), device="cuda")
+    vc = torch.zeros_like(kc)
+    lens = torch.tensor([0, 30, 35], dtype=torch.int32, device="cuda")
+    n_new = torch.tensor([9, 4, 9], dtype=torch.int32, device="cuda")
+    k = rng.standard_normal((B, C, H, D)).astype(np.float32)
+    v = rng.standard_normal((B, C, H, D)).astype(np.float32)
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    kd, vd = to_dev(k), to_dev(v)  # keep both alive until the launch is enqueued
+    rc = L.skv_append_chunk(kc.data_ptr(), vc.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                            lens.data_ptr(), n_new.data_ptr(), B, C, H, D, T, 0, 0, s)
+    _lib.check(rc, "append_chunk")
+    _lib.check(L.skv_advance(lens.data_ptr(), n_new.data_ptr(), 0, B, T, s), "advance")
+    kw = np.zeros((B, T, H, D), np.float32)
+    vw = np.zeros_like(kw)
+    ko.append_chunk(kw, vw, k, v, np.array([0, 30, 35]), np.array([9, 4, 9]))
+    np.testing.assert_array_equal(kc.cpu().numpy(), kw)
+    np.testing.assert_array_equal(vc.cpu().numpy(), vw)
+    assert lens.cpu().tolist() == [9, 34, 40]  # the third one is clamped at T
+
+
+# ---------------------------------------------------------------------------
+# Decode attention
+# ---------------------------------------------------------------------------
+
+
+def _filled_cache(gpu, ctx, rng, B, T, Hq, Hkv, D, dtype, lens, paged=False, scale_kv=1.0):
+    cfg = gpu.KVCacheConfig(B, T, 1, Hq, D, n_kv_heads=Hkv, dtype=dtype,
+                            block_size=16 if paged else 0)
+    cache = gpu.kv_cache_create(ctx, cfg)
+    k = (rng.standard_normal((B, T, Hkv, D)) * scale_kv).astype(np.float32)
+    v = rng.standard_normal((B, T, Hkv, D)).astype(np.float32)
+    if dtype == torch.bfloat16:
+        k, v = ko.bf16_round(k), ko.bf16_round(v)
+    table = None
+    layer = cache.layers[0]
+    if paged:
+        table = rng.permutation(cache.n_blocks).reshape(B, -1).astype(np.int32)
+        gpu.kv_cache_set_block_table(cache, torch.from_numpy(table))
+        pool_k = np.zeros((cache.n_blocks * 16, Hkv, D), np.float32)
+        pool_v = np.zeros_like(pool_k)
+        for b in range(B):
+            for t in range(T):
+                r = table[b, t // 16] * 16 + t % 16
+                pool_k[r], pool_v[r] = k[b, t], v[b, t]
+        layer.k_cache.buffer.copy_(to_dev(pool_k.reshape(-1, Hkv * D), dtype))
+        layer.v_cache.buffer.copy_(to_dev(pool_v.reshape(-1, Hkv * D), dtype))
+    else:
+        layer.k_cache.buffer.copy_(to_dev(k.reshape(-1, Hkv * D), dtype))
+        layer.v_cache.buffer.copy_(to_dev(v.reshape(-1, Hkv * D), dtype))
+    layer.lens.copy_(torch.from_numpy(np.asarray(lens, np.int32)))
+    layer.host_lens[:] = lens
+    return cache, k, v, table
+
+
+def _decode(gpu, ctx, cache, q_np, q_dtype=torch.float32, out_dtype=torch.float32, **kw):
+    q = to_dev(q_np, q_dtype)
+    out = torch.empty(q.shape, dtype=out_dtype, device="cuda")
+    gpu.decode_attention(ctx, cache, 0, q, out, **kw)
+    return out.float().cpu().numpy()
+
+
+CASES = [
+    # B, T, Hq, Hkv, D, dtype, paged
+    (8, 2048, 8, 8, 64, torch.float32, False),   # C2 shape
+    (4, 4096, 16, 16, 128, torch.bfloat16, False),  # C4 head shape, shorter
+    (6, 1500, 32, 8, 128, torch.bfloat16, True),  # C5 GQA paged
+    (3, 700, 8, 4, 64, torch.float32, False),
+    (3, 700, 16, 2, 128, torch.float32, True),
+    (2, 900, 16, 2, 64, torch.bfloat16, False),  # G = 8
+    (16, 1024, 12, 12, 64, torch.float32, False),  # C3 head shape
+]
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,D,dtype,paged", CASES)
+def test_decode_matches_oracle(gpu_ctx, B, T, Hq, Hkv, D, dtype, paged):
+    banner(f"decode B={B} T={T} Hq={Hq} Hkv={Hkv} D={D} {dtype} paged={paged}")
+    gpu = _gpu()
+    rng = np.random.default_rng(B * 1000 + T)
+    lens = rng.integers(1, T + 1, B)
+    lens[0] = T
+    cache, k, v, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, Hq, Hkv, D, dtype, lens, paged)
+    q = (rng.standard_normal((B, Hq, D))).astype(np.float32)
+    got = _decode(gpu, gpu_ctx, cache, q)
+    want = ko.decode_attention(q, k, v, lens)
+    err = rel_err(got, want)
+    print(f"rel_err={err:.3e}")
+    assert err < (BF16_TOL if dtype == torch.bfloat16 else FP32_TOL)
+    # the bf16 path accumulates in fp32 over the same rounded inputs
+    assert err < 1e-4
+
+
+def test_paged_equals_contiguous_bitwise(gpu_ctx):
+    """C5's check: the paged cache gives the result of the same data gathered
+    into a contiguous cache (same kernel arithmetic, so bit-identical)."""
+    banner("paged vs contiguous")
+    gpu = _gpu()
+    rng = np.random.default_rng(11)
+    B, T, Hq, Hkv, D = 8, 640, 32, 8, 128
+    lens = np.clip(np.exp(rng.normal(np.log(300), 0.8, B)), 16, T).astype(np.int64)
+    cp, k, v, _ = _filled_cache(gpu, gpu_ctx, np.random.default_rng(5), B, T, Hq, Hkv, D,
+                                torch.bfloat16, lens, paged=True)
+    cc, k2, v2, _ = _filled_cache(gpu, gpu_ctx, np.random.default_rng(5), B, T, Hq, Hkv, D,
+                                  torch.bfloat16, lens, paged=False)
+    np.testing.assert_array_equal(k, k2)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float32)
+    a = _decode(gpu, gpu_ctx, cp, q, max_len=T)
+    b = _decode(gpu, gpu_ctx, cc, q, max_len=T)
+    np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("L", [1, 2, 15, 16, 17, 255, 256, 257, 1023, 1024, 1025, 2047, 2048])
+def test_decode_chunk_boundaries(gpu_ctx, L):
+    banner(f"decode boundary L={L}")
+    gpu = _gpu()
+    gpu_ctx.config.decode_chunk_tokens = 256
+    try:
+        rng = np.random.default_rng(L)
+        B, T, H, D = 2, 2048, 4, 128
+        lens = np.array([L, max(1, L // 2)])
+        cache, k, v, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, H, H, D, torch.float32, lens)
+        q = rng.standard_normal((B, H, D)).astype(np.float32)
+        got = _decode(gpu, gpu_ctx, cache, q)
+        want = ko.decode_attention(q, k, v, lens)
+        assert rel_err(got, want) < FP32_TOL
+        if L == 1:  # one token: exactly its value row
+            np.testing.assert_array_equal(got[0], v[0, 0])
+    finally:
+        gpu_ctx.config.decode_chunk_tokens = 0
+
+
+def test_decode_empty_sequence_and_plan_overflow(gpu_ctx):
+    banner("decode len=0 and under-sized plan")
+    gpu = _gpu()
+    rng = np.random.default_rng(2)
+    B, T, H, D = 3, 1024, 2, 64
+    lens = np.array([0, 300, 1024])
+    cache, k, v, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, H, H, D, torch.float32, lens)
+    q = rng.standard_normal((B, H, D)).astype(np.float32)
+    got = _decode(gpu, gpu_ctx, cache, q)
+    assert not got[0].any()
+    want = ko.decode_attention(q, k, v, lens)
+    assert rel_err(got[1:], want[1:]) < FP32_TOL
+    # a plan sized for 256 tokens: longer sequences are flagged with NaN
+    gpu_ctx.config.decode_chunk_tokens = 256
+    try:
+        got = _decode(gpu, gpu_ctx, cache, q, max_len=256)
+    finally:
+        gpu_ctx.config.decode_chunk_tokens = 0
+    assert np.isnan(got[1]).all() and np.isnan(got[2]).all()
+
+
+@pytest.mark.parametrize("kind", ["shift+50", "peaky*100", "zeros"])
+def test_decode_softmax_stability(gpu_ctx, kind):
+    """The reference's softmax stability cases (gpu_test.py:1647-1657) applied
+    to the attention scores."""
+    banner(f"decode stability {kind}")
+    gpu = _gpu()
+    rng = np.random.default_rng(4)
+    B, T, H, D = 2, 3000, 4, 128
+    lens = np.array([3000, 1777])
+    cache, k, v, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, H, H, D, torch.float32, lens)
+    q = rng.standard_normal((B, H, D)).astype(np.float32)
+    if kind == "peaky*100":
+        q *= 100.0 / np.sqrt(D)
+    elif kind == "zeros":
+        q[:] = 0
+    elif kind == "shift+50":  # add 50 to every score: keys += 50*sqrt(D) q/|q|^2
+        c = 50.0 * np.sqrt(D) * q / (q * q).sum(-1, keepdims=True)
+        k = (k + c[:, None]).astype(np.float32)
+        cache.layers[0].k_cache.buffer.copy_(to_dev(k.reshape(-1, H * D)))
+    got = _decode(gpu, gpu_ctx, cache, q)
+    want = ko.decode_attention(q, k, v, lens)
+    assert np.isfinite(got).all()
+    tol = 2e-4 if kind == "peaky*100" else FP32_TOL  # |s| ~ 1e3: fp32 rounding of s
+    assert rel_err(got, want) < tol
+    if kind == "zeros":  # uniform weights: mean of V
+        np.testing.assert_allclose(got[1], v[1, :1777].astype(np.float64).mean(0), atol=1e-5)
+
+
+@pytest.mark.parametrize("q_dt,o_dt", [(torch.bfloat16, torch.float32),
+                                       (torch.float32, torch.bfloat16),
+                                       (torch.bfloat16, torch.bfloat16)])
+def test_decode_io_dtypes(gpu_ctx, q_dt, o_dt):
+    banner(f"decode q={q_dt} out={o_dt}")
+    gpu = _gpu()
+    rng = np.random.default_rng(9)
+    B, T, H, D = 2, 1000, 8, 128
+    lens = np.array([1000, 640])
+    cache, k, v, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, H, H, D, torch.bfloat16, lens)
+    q = rng.standard_normal((B, H, D)).astype(np.float32)
+    qr = ko.bf16_round(q) if q_dt == torch.bfloat16 else q
+    got = _decode(gpu, gpu_ctx, cache, qr, q_dtype=q_dt, out_dtype=o_dt)
+    want = ko.decode_attention(qr, k, v, lens)
+    assert rel_err(got, want) < (BF16_TOL if o_dt == torch.bfloat16 else 1e-4)
+
+
+def test_decode_deterministic(gpu_ctx):
+    banner("decode determinism")
+    gpu = _gpu()
+    rng = np.random.default_rng(12)
+    B, T, H, D = 4, 5000, 16, 128
+    lens = rng.integers(1000, T + 1, B)
+    cache, k, v, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, H, H, D, torch.bfloat16, lens)
+    q = rng.standard_normal((B, H, D)).astype(np.float32)
+    a = _decode(gpu, gpu_ctx, cache, q)
+    b = _decode(gpu, gpu_ctx, cache, q)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_decode_full_size_c4_sampled(gpu_ctx):
+    """C4 at full size (B=4, H=16, D=128, T_cap=32768, bf16, filled to 32000),
+    one append + decode step; the oracle checks sampled (b, h) pairs."""
+    banner("decode C4 full size, sampled oracle")
+    gpu = _gpu()
+    B, T, H, D, fill = 4, 32768, 16, 128, 32000
+    cache = gpu.kv_cache_create(gpu_ctx, gpu.KVCacheConfig(B, T, 1, H, D,
+                                                           dtype=torch.bfloat16))
+    g = torch.Generator(device="cuda").manual_seed(0)
+    layer = cache.layers[0]
+    kv = layer.k_cache.buffer.view(B, T, H, D)
+    vv = layer.v_cache.buffer.view(B, T, H, D)
+    kv[:, :fill].copy_(torch.randn((B, fill, H, D), generator=g, device="cuda"))
+    vv[:, :fill].copy_(torch.randn((B, fill, H, D), generator=g, device="cuda"))
+    cache.current_len = fill
+    rng = np.random.default_rng(0)
+    kn = rng.standard_normal((B, H, D)).astype(np.float32)
+    vn = rng.standard_normal((B, H, D)).astype(np.float32)
+    q = rng.standard_normal((B, H, D)).astype(np.float32)
+    gpu.kv_cache_append(gpu_ctx, cache, 0, to_dev(kn), to_dev(vn))
+    got = _decode(gpu, gpu_ctx, cache, q)
+    assert cache.layers[0].lens.cpu().tolist() == [fill + 1] * B
+    for b, h in [(0, 0), (1, 7), (2, 15), (3, 3)]:
+        kh = kv[b, :fill + 1, h].float().cpu().numpy()[:, None, :]
+        vh = vv[b, :fill + 1, h].float().cpu().numpy()[:, None, :]
+        np.testing.assert_array_equal(kh[fill, 0], ko.bf16_round(kn[b, h]))
+        want = ko.decode_attention(q[b:b + 1, h:h + 1], kh[None], vh[None], [fill + 1])
+        assert rel_err(got[b:b + 1, h:h + 1], want) < 1e-4
