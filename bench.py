@@ -1,0 +1,251 @@
+"""Benchmark of the KV-cache decode hot path on one MI355X.
+
+Workload ("C4"): long-context decode, batch 4,
+16 heads x head_dim 128, cache capacity 32768 with bf16 storage and fp32
+accumulation, filled to 32000 with N(0,1) K/V. One step = the append of one
+new k/v row per sequence into the cache, then single-query attention of
+every sequence over its filled prefix (QK^T, softmax, PV): the reference's
+kv_cache_update + attention_with_kv_cache
+(simple-llm/src/gpu/gpu_kv_cache.py:113-186, 194-289), driven through this
+build's drop-in API. The timed steps go 32000 -> 32000+K filled positions
+(the cache is rewound to 32000 after warm-up), exactly as the config states
+for K = 256.
+
+Output: one JSON line (rank 0) with
+  value      decode tokens/s = B * K / wall time of the K timed steps
+  roofline   decode attention (split-K pass 1 + merge pass 2, bracketed by
+             HIP events on the launch stream) against 8 TB/s HBM:
+             achieved = algorithmic bytes per call / mean call time, where
+             bytes = sum_b 2*H_kv*L_b*D*2 (K and V rows read) + H_q*D*(4+4)
+             (q read, out written); traffic = HBM bytes per call measured by
+             rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/), or null
+  cpu_baseline  the C restatement of the reference's decode attention
+             (oracle/c/kv_attn_ref.c, OpenMP over (sequence, head)) plus the
+             host append, timed on this box's cores over the first steps of
+             the same workload (~10 s of CPU work)
+
+Inputs (q, k, v of every step) are generated on the device before timing.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "llm-experiments_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+
+# C4 workload
+B, H, D, T_CAP, FILL = 4, 16, 128, 32768, 32000
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=256)
+    p.add_argument("--warmup", type=int, default=16)
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="CPU time budget of the cpu_baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="instead of the benchmark, time a plain 1 GiB device copy (the "
+                        "reference kernel for the HBM counters and the measured copy GB/s)")
+    return p.parse_args()
+
+
+def copy_calibration():
+    """A plain device-to-device copy of 1 GiB, 10 times: its FETCH_SIZE and
+    WRITE_SIZE per dispatch calibrate the counters (1 GiB each way), and its
+    rate is the measured copy bandwidth (bytes read + bytes written)."""
+    import torch
+
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    s = e0.elapsed_time(e1) * 1e-3 / 10
+    print(json.dumps({"copy_bytes_each_way": n, "mean_copy_us": s * 1e6,
+                      "copy_GBps_read_plus_write": 2 * n / s / 1e9}), flush=True)
+
+
+def algorithmic_bytes(lens, h_q=H, h_kv=H, d=D, s_kv=2, s_q=4, s_o=4) -> int:
+    """Bytes one decode-attention call must move at minimum."""
+    return int(sum(2 * h_kv * int(L) * d * s_kv + h_q * d * (s_q + s_o) for L in lens))
+
+
+def measured_traffic():
+    """HBM bytes per decode-attention call from the committed rocprofv3 PMC
+    summary (profiles/decode_attn_c4_pmc.md), or None if absent."""
+    path = os.path.join(ROOT, "profiles", "decode_attn_c4_pmc.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        m = re.search(r"^traffic_bytes_per_call:\s*([0-9.eE+]+)", f.read(), flags=re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(args, k_dev, v_dev, q_all, k_all, v_all):
+    """Time the CPU restatement on the first steps of the same workload."""
+    import numpy as np
+    import torch
+
+    from oracle import c_oracle
+
+    # the same cache contents, as bf16 bit patterns on the host
+    kc = k_dev.view(torch.int16).cpu().numpy().view(np.uint16).reshape(B, T_CAP, H, D).copy()
+    vc = v_dev.view(torch.int16).cpu().numpy().view(np.uint16).reshape(B, T_CAP, H, D).copy()
+    qs = q_all.cpu().numpy()
+    ks = k_all.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+    vs = v_all.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+    lens = np.full(B, FILL, np.int32)
+    c_oracle.decode_attn(qs[0], kc, vc, lens + 1, cache_bf16=True)  # warm-up (pages, threads)
+    steps = 0
+    t0 = time.perf_counter()
+    while steps < args.steps and (time.perf_counter() - t0) < args.cpu_seconds:
+        for b in range(B):  # host append at lens[b]
+            kc[b, lens[b]] = ks[steps, b]
+            vc[b, lens[b]] = vs[steps, b]
+        lens += 1
+        c_oracle.decode_attn(qs[steps], kc, vc, lens, cache_bf16=True)
+        steps += 1
+    dt = time.perf_counter() - t0
+    return {
+        "value": B * steps / dt,
+        "unit": "tokens/s",
+        "cores": c_oracle.threads(),
+        "kind": "port",
+        "sample": f"first {steps} of the {args.steps} C4 decode steps (append + decode attention "
+                  f"over 32001.. positions, B={B} H={H} D={D} bf16 KV, fp32 math); "
+                  f"oracle/c/kv_attn_ref.c with OpenMP, {dt:.1f} s",
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build runs on one GPU only (the decode path shards over "
+              "sequences/kv heads with no exchange; see the sharding note in DESIGN.md); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if FILL + args.steps > T_CAP or args.steps < 1 or args.warmup < 0:
+        print(f"bench.py: --steps must lie in [1, {T_CAP - FILL}]", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from simple_llm_amd.gpu import gpu
+
+    ctx = gpu.context_create()
+    dev = ctx.device
+    cache = gpu.kv_cache_create(ctx, gpu.KVCacheConfig(B, T_CAP, 1, H, D, dtype=torch.bfloat16))
+    layer = cache.layers[0]
+    g = torch.Generator(device=dev).manual_seed(0)
+    kv = layer.k_cache.buffer.view(B, T_CAP, H, D)
+    vv = layer.v_cache.buffer.view(B, T_CAP, H, D)
+    for b in range(B):  # fill [0, FILL) with N(0,1), one sequence at a time
+        kv[b, :FILL].copy_(torch.randn((FILL, H, D), generator=g, device=dev))
+        vv[b, :FILL].copy_(torch.randn((FILL, H, D), generator=g, device=dev))
+    n_in = args.warmup + args.steps
+    q_all = torch.randn((n_in, B, H, D), generator=g, device=dev)
+    k_all = torch.randn((n_in, B, H, D), generator=g, device=dev)
+    v_all = torch.randn((n_in, B, H, D), generator=g, device=dev)
+    out = torch.empty((B, H, D), device=dev)
+    max_len = FILL + args.steps  # split-K plan sized for the longest step
+
+    def step(i, ev=None):
+        gpu.kv_cache_append(ctx, cache, 0, k_all[i], v_all[i])
+        if ev is not None:
+            ev[0].record()
+        gpu.decode_attention(ctx, cache, 0, q_all[i], out, max_len=max_len)
+        if ev is not None:
+            ev[1].record()
+
+    # warm-up, then rewind the fill to FILL
+    cache.current_len = FILL
+    for i in range(args.warmup):
+        step(args.steps + i)
+    torch.cuda.synchronize()
+    cache.current_len = FILL
+    torch.cuda.synchronize()
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    attn_ms = np.array([a.elapsed_time(b) for a, b in evs])
+    lens_per_step = [[FILL + i + 1] * B for i in range(args.steps)]
+    bytes_per_call = float(np.mean([algorithmic_bytes(ls) for ls in lens_per_step]))
+    mean_s = float(attn_ms.mean()) * 1e-3
+    achieved = bytes_per_call / mean_s / 1e9
+    assert cache.layers[0].lens.cpu().tolist() == [FILL + args.steps] * B
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args, layer.k_cache.buffer, layer.v_cache.buffer, q_all, k_all,
+                           v_all)
+
+    traffic = measured_traffic()
+    rec = {
+        "metric": "decode tokens/sec",
+        "value": B * args.steps / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C4 long-context decode: B=4, H=16 (MHA), D=128, KV cap 32768 bf16 "
+                        "storage / fp32 accumulation, filled to 32000, per step append + "
+                        "decode attention",
+            "batch": B, "n_heads": H, "head_dim": D, "kv_capacity": T_CAP,
+            "start_fill": FILL, "kv_dtype": "bf16", "accumulate": "fp32",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "kernel": "decode attention (k_decode_partial + k_decode_merge)",
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "mean_call_us": mean_s * 1e6,
+            "algorithmic_bytes_per_call": bytes_per_call,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()
