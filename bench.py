@@ -55,6 +55,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU time budget of the cpu_baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--chunk-tokens", type=int, default=0,
+                   help="split-K chunk size of decode attention (0: the library's plan)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="instead of the benchmark, time a plain 1 GiB device copy (the "
                         "reference kernel for the HBM counters and the measured copy GB/s)")
@@ -156,6 +158,7 @@ def main():
     from simple_llm_amd.gpu import gpu
 
     ctx = gpu.context_create()
+    ctx.config.decode_chunk_tokens = args.chunk_tokens
     dev = ctx.device
     cache = gpu.kv_cache_create(ctx, gpu.KVCacheConfig(B, T_CAP, 1, H, D, dtype=torch.bfloat16))
     layer = cache.layers[0]
@@ -204,6 +207,7 @@ def main():
     achieved = bytes_per_call / mean_s / 1e9
     assert cache.layers[0].lens.cpu().tolist() == [FILL + args.steps] * B
 
+    chunk, n_chunks = gpu.decode_plan(ctx, B, H, max_len)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args, layer.k_cache.buffer, layer.v_cache.buffer, q_all, k_all,
@@ -240,6 +244,7 @@ def main():
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
             "mean_call_us": mean_s * 1e6,
+            "split_k": {"chunk_tokens": chunk, "n_chunks": n_chunks},
             "algorithmic_bytes_per_call": bytes_per_call,
         },
         "cpu_baseline": cpu,

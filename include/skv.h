@@ -95,11 +95,13 @@ int skv_advance(int32_t* lens, const int32_t* n_new, int n_const, int B, int T_c
 
 /*
  * Split-K sizing for decode attention (host-only, no device work).
- * Given the longest sequence the call may see, picks chunk_tokens (tokens
- * per workgroup) and n_chunks_max = ceil(max_len / chunk_tokens).
- * chunk_hint > 0 forces that chunk size (rounded up to a multiple of 256).
+ * Given the longest sequence the call may see (max_len) and the filled
+ * tokens of the whole batch (total_len; <= 0 means B * max_len), picks
+ * chunk_tokens (tokens per workgroup) for about 1024 workgroups per call and
+ * n_chunks_max = ceil(max_len / chunk_tokens).
+ * chunk_hint > 0 forces that chunk size (rounded up to a multiple of 16).
  */
-int skv_decode_plan(int B, int H_kv, int max_len, int chunk_hint,
+int skv_decode_plan(int B, int H_kv, int max_len, long long total_len, int chunk_hint,
                     int* chunk_tokens /* host */, int* n_chunks_max /* host */);
 
 /* Bytes of workspace skv_decode_attn needs for this plan. */

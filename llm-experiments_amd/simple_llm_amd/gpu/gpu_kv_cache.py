@@ -234,12 +234,14 @@ def _workspace(ctx: GPUContext, nbytes: int) -> torch.Tensor:
     return ws
 
 
-def decode_plan(ctx: GPUContext, batch_size: int, n_kv_heads: int,
-                max_len: int) -> tuple[int, int]:
-    """(chunk_tokens, n_chunks_max) of the split-K decode for these sizes."""
+def decode_plan(ctx: GPUContext, batch_size: int, n_kv_heads: int, max_len: int,
+                total_len: int = 0) -> tuple[int, int]:
+    """(chunk_tokens, n_chunks_max) of the split-K decode for these sizes.
+
+    total_len: filled tokens over the batch (0: batch_size * max_len)."""
     L = _lib.lib()
     c, n = ctypes.c_int(), ctypes.c_int()
-    rc = L.skv_decode_plan(batch_size, n_kv_heads, max(int(max_len), 1),
+    rc = L.skv_decode_plan(batch_size, n_kv_heads, max(int(max_len), 1), int(total_len),
                            int(ctx.config.decode_chunk_tokens), ctypes.byref(c), ctypes.byref(n))
     _lib.check(rc, "skv_decode_plan")
     return c.value, n.value
@@ -252,7 +254,8 @@ def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.T
 
     q, out: contiguous device tensors of [batch_size, n_heads, head_dim]
     elements (float32 or bfloat16). max_len: an upper bound of the fills
-    (default: the host mirror's maximum), used to size the split-K grid.
+    (default: the host mirror's maximum), used to size the split-K grid; the
+    chunk size follows the batch's total fill (host mirror).
     """
     layer = cache.layers[layer_idx]
     dev = layer.lens.device
@@ -264,7 +267,8 @@ def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.T
                          f"{cache.batch_size * e_q} elements")
     if max_len is None:
         max_len = int(layer.host_lens.max())
-    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_kv_heads, max_len)
+    total = int(np.minimum(layer.host_lens, max_len).sum())
+    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_kv_heads, max_len, total)
     L = _lib.lib()
     need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
     ws = _workspace(ctx, need)

@@ -24,24 +24,35 @@ def test_version():
     assert _lib.lib().skv_version() == 100
 
 
-def _plan(B, Hkv, max_len, hint=0):
+def _plan(B, Hkv, max_len, hint=0, total=0):
     c, n = ctypes.c_int(), ctypes.c_int()
-    rc = _lib.lib().skv_decode_plan(B, Hkv, max_len, hint, ctypes.byref(c), ctypes.byref(n))
+    rc = _lib.lib().skv_decode_plan(B, Hkv, max_len, total, hint, ctypes.byref(c),
+                                    ctypes.byref(n))
     return rc, c.value, n.value
 
 
 @pytest.mark.parametrize("B,Hkv,L", [(4, 16, 32256), (8, 8, 2048), (64, 8, 8192), (1, 1, 1),
-                                     (16, 12, 1024), (1, 4, 256)])
+                                     (16, 12, 1024), (1, 4, 256), (2, 24, 100000)])
 def test_decode_plan_covers_every_length(B, Hkv, L):
     rc, chunk, n = _plan(B, Hkv, L)
     assert rc == 0
-    assert chunk % 256 == 0 and 256 <= chunk <= 2048
+    assert chunk % 32 == 0 and 64 <= chunk <= 8192
     assert n * chunk >= L > (n - 1) * chunk
+
+
+def test_decode_plan_c4_and_ragged_total():
+    # C4: 4 sequences x 16 kv heads (one head group) at 32256 -> 256-token
+    # chunks, 126 per sequence = 504 workgroups (two per CU)
+    assert _plan(4, 16, 32256) == (0, 256, 126)
+    # a ragged batch plans from its total fill, not from B * max_len
+    rc, chunk, n = _plan(64, 8, 8192, total=64 * 2000)
+    assert rc == 0 and chunk == 256 and n == 32
+    assert _plan(64, 8, 8192)[1] > chunk
 
 
 def test_decode_plan_hint_and_errors():
     rc, chunk, n = _plan(4, 16, 32768, hint=1000)
-    assert rc == 0 and chunk == 1024 and n == 32
+    assert rc == 0 and chunk == 1008 and n == 33
     assert _plan(0, 16, 100)[0] == _lib.SKV_E_INVALID
     assert _plan(4, 16, 0)[0] == _lib.SKV_E_INVALID
     assert b"dims must be > 0" in _lib.lib().skv_last_error()
@@ -73,7 +84,7 @@ def test_entry_points_reject_bad_arguments():
 
     assert dec(D=96) == _lib.SKV_E_UNSUPPORTED
     assert dec(Hq=6, Hkv=4) == _lib.SKV_E_INVALID
-    assert dec(chunk=100) == _lib.SKV_E_INVALID
+    assert dec(chunk=100) == _lib.SKV_E_INVALID  # not a multiple of 16
     assert dec(ws=ws - 1) == _lib.SKV_E_WORKSPACE
     ws48 = L.skv_decode_workspace_bytes(2, 48, 64, 1)
     assert dec(Hq=48, Hkv=3, ws=ws48) == _lib.SKV_E_UNSUPPORTED  # G = 16 has no kernel
