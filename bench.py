@@ -19,6 +19,9 @@ Output: one JSON line (rank 0) with
              bytes = sum_b 2*H_kv*L_b*D*2 (K and V rows read) + H_q*D*(4+4)
              (q read, out written); traffic = HBM bytes per call measured by
              rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/), or null
+  prefill    C4's one 512-token chunked prefill into the cache (MFMA path),
+             timed separately with HIP events: TFLOP/s of its QK^T + PV flops
+             against the 2.5 PFLOP/s dense bf16 peak
   cpu_baseline  the C restatement of the reference's decode attention
              (oracle/c/kv_attn_ref.c, OpenMP over (sequence, head)) plus the
              host append, timed on this box's cores over the first steps of
@@ -42,6 +45,8 @@ for _p in (ROOT, PKG):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
+PREFILL_C = 512  # C4's chunked prefill: 512 tokens from fill 32256 to 32768
 
 # C4 workload
 B, H, D, T_CAP, FILL = 4, 16, 128, 32768, 32000
@@ -55,6 +60,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU time budget of the cpu_baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-prefill", action="store_true",
+                   help="skip the separate timing of C4's 512-token MFMA chunked prefill")
     p.add_argument("--chunk-tokens", type=int, default=0,
                    help="split-K chunk size of decode attention (0: the library's plan)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -99,6 +106,50 @@ def measured_traffic():
     with open(path) as f:
         m = re.search(r"^traffic_bytes_per_call:\s*([0-9.eE+]+)", f.read(), flags=re.M)
     return float(m.group(1)) if m else None
+
+
+def prefill_flops(start, c=PREFILL_C, h_q=H, d=D, batch=B) -> float:
+    """QK^T and PV flops of a causal chunk after a prefix of `start` tokens."""
+    attended = c * start + c * (c + 1) // 2  # sum over the chunk's queries of their spans
+    return 4.0 * d * h_q * batch * attended
+
+
+def time_prefill(ctx, cache, reps: int):
+    """C4's 512-token chunked prefill (chunk append + MFMA causal attention over
+    prefix + chunk + fill advance), rewound to fill 32256 before each rep."""
+    import numpy as np
+    import torch
+
+    from simple_llm_amd.gpu import gpu
+
+    dev = ctx.device
+    start = T_CAP - PREFILL_C
+    g = torch.Generator(device=dev).manual_seed(1)
+    kn = torch.randn((B, PREFILL_C, H, D), generator=g, device=dev)
+    vn = torch.randn((B, PREFILL_C, H, D), generator=g, device=dev)
+    q = torch.randn((B, PREFILL_C, H, D), generator=g, device=dev)
+    out = torch.empty_like(q)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for i in range(reps + 2):
+        cache.current_len = start
+        if i >= 2:
+            evs[i - 2][0].record()
+        gpu.kv_cache_prefill(ctx, cache, 0, kn, vn, q, out)
+        if i >= 2:
+            evs[i - 2][1].record()
+    torch.cuda.synchronize()
+    ms = np.array([a.elapsed_time(b) for a, b in evs])
+    fl = prefill_flops(start)
+    mean_s = float(ms.mean()) * 1e-3
+    return {
+        "chunk_tokens": PREFILL_C, "start_fill": start, "reps": reps,
+        "mean_us": mean_s * 1e6, "tflops": fl / mean_s / 1e12,
+        "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+        "frac": fl / mean_s / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "flops": fl,
+        "includes": "chunk append + MFMA attention + split merge + fill advance",
+    }
 
 
 def cpu_baseline(args, k_dev, v_dev, q_all, k_all, v_all):
@@ -208,6 +259,7 @@ def main():
     assert cache.layers[0].lens.cpu().tolist() == [FILL + args.steps] * B
 
     chunk, n_chunks = gpu.decode_plan(ctx, B, H, max_len)
+    prefill = None if args.no_prefill else time_prefill(ctx, cache, reps=10)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args, layer.k_cache.buffer, layer.v_cache.buffer, q_all, k_all,
@@ -248,6 +300,7 @@ def main():
             "algorithmic_bytes_per_call": bytes_per_call,
         },
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(rec), flush=True)
 

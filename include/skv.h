@@ -135,6 +135,35 @@ int skv_decode_attn_paged(void* out, const void* q, const void* k_pool,
                           void* ws, size_t ws_bytes, int cache_dt, int q_dt,
                           int out_dt, skv_stream_t stream);
 
+/*
+ * Split count for skv_prefill_attn (host-only): about one workgroup per CU.
+ * max_kv_end = the largest start[b] + n_new[b] of the call.
+ */
+int skv_prefill_plan(int B, int C, int H_q, int H_kv, int max_kv_end, int* n_splits /* host */);
+
+/* Bytes of workspace skv_prefill_attn needs (0 when n_splits == 1). */
+size_t skv_prefill_workspace_bytes(int B, int C, int H_q, int D, int n_splits);
+
+/*
+ * Causal attention of a chunk of queries over the cache (chunked prefill).
+ * The reference's prefill analogue is flash_attention
+ * (simple-llm/src/gpu/gpu_pass_forward.py:497-588, kernel
+ * create_flash_attention_kernel simple-llm/src/gpu/gpu_kernels.py:499-770),
+ * causal over a sequence with no cache prefix; this adds the prefix offset:
+ *   out[b, i, h, :] = softmax(scale * q[b, i, h, :] . K[b, 0:start[b]+i+1, h/G, :]^T)
+ *                     . V[b, 0:start[b]+i+1, h/G, :]     for i < n_new[b],
+ * and zeros for i >= n_new[b]. The chunk's own K/V must already be in the
+ * cache at positions start[b] .. start[b]+n_new[b]-1 (skv_append_chunk).
+ * q, out: [B, C, H_q, D] of q_dt / out_dt; n_new may be NULL (C for all).
+ * Requires start[b] + n_new[b] <= T_cap. bf16 caches only: Q, K, V and the
+ * probabilities enter v_mfma_f32_32x32x16_bf16 as bf16, accumulation and
+ * softmax are fp32. D in {64, 128}; G = H_q / H_kv in {1, 2, 4, 8}.
+ */
+int skv_prefill_attn(void* out, const void* q, const void* k_cache, const void* v_cache,
+                     const int32_t* start, const int32_t* n_new, int B, int C, int H_q,
+                     int H_kv, int D, int T_cap, float scale, int n_splits, void* ws,
+                     size_t ws_bytes, int cache_dt, int q_dt, int out_dt, skv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,481 @@
+// Chunked prefill attention over the cache: MFMA flash attention on gfx950.
+//
+// Reference behaviour: flash_attention (simple-llm/src/gpu/gpu_pass_forward.py:497-588,
+// kernel create_flash_attention_kernel simple-llm/src/gpu/gpu_kernels.py:499-770):
+// causal FlashAttention-1, S = Q K^T / sqrt(D), mask kv_pos <= q_pos, online
+// softmax, O = sum_t p_t V[t] / l. The reference has no cache offset; here
+// query row i of sequence b sits at position start[b] + i and attends cache
+// positions [0, start[b] + i], so a chunk is prefilled after an existing
+// prefix (the chunk's own K/V must already be appended to the cache).
+//
+// Design (dense bf16 contraction, MFMA-bound: ~500 flop/byte at C4):
+//  * v_mfma_f32_32x32x16_bf16. The kernel computes S^T = K Q^T (K from LDS
+//    as operand A, Q held in registers as operand B) so that each lane's
+//    accumulator column is one query: the softmax statistics of a query live
+//    in one lane pair (lanes l and l^32), and the probabilities P^T come out
+//    of the accumulator in exactly the order operand B of the next product
+//    O^T += V^T P^T needs (accumulator slot r of rows 8kk..8kk+7 is slot j of
+//    k-block kk). Only V needs a transpose, done once per tile while staging
+//    it into LDS.
+//  * Workgroup = 4 wavefronts, 64 query rows each (2 blocks of 32), so every
+//    K/V operand read from LDS feeds two MFMAs. K/V tiles of 64 tokens are
+//    double buffered: the global loads of tile t+1 are in flight while tile t
+//    is computed. Grouped-query attention folds the G query heads of a kv
+//    head into the rows (row = query * G + head), so K/V are read once per
+//    group.
+//  * Long prefixes are split into n_splits token ranges (split-K, so that
+//    about one workgroup runs per CU); partials (m, l, o[D]) are merged by a
+//    second pass. The query tiles of one (sequence, kv head, split) are laid
+//    out 8 blocks apart so they land on the same XCD together and the second
+//    tile's K/V reads hit that XCD's L2.
+#include "skv_common.h"
+
+namespace skv {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWaves = 4;
+constexpr int kQB = 2;                      // 32-row query blocks per wavefront
+constexpr int kBM = kWaves * kQB * 32;      // query rows per workgroup (256)
+constexpr int kBN = 64;                     // tokens per K/V tile
+constexpr int kXCD = 8;                     // XCDs of an MI355X
+
+struct PrefillArgs {
+  const void* q;
+  void* out;
+  const uint16_t* k;
+  const uint16_t* v;
+  const int32_t* start;
+  const int32_t* n_new;
+  int C, Hq, Hkv, T_cap;
+  float qscale;  // softmax scale * log2(e)
+  int q_dt, out_dt;
+  int n_qt;      // query tiles per (sequence, kv head)
+  int n_splits;
+  int n_groups;  // B * Hkv * n_splits
+  float* ws_o;   // [n_splits][B][C][Hq][D]
+  float* ws_ml;  // [n_splits][B][C][Hq][2]
+  int B;
+};
+
+// K and V tiles live in LDS row-major, [kBN tokens][D] bf16, two stages
+// each. The 16-byte chunks of a row are XOR-swizzled (physical chunk =
+// chunk ^ (row mod chunks-per-row)) so that 16 consecutive rows read at the
+// same column hit 16 different bank groups.
+template <int D>
+struct alignas(16) Smem {
+  uint16_t k[2][kBN * D];
+  uint16_t v[2][kBN * D];
+};
+
+template <int D>
+__device__ __forceinline__ int swz(int row, int chunk) {  // element offset of a 16-B chunk
+  constexpr int CPR = D / 8;                               // chunks per row
+  return row * D + ((chunk ^ (row & (CPR - 1))) * 8);
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes from global memory straight into LDS (global_load_lds_dwordx4):
+// lane i of the wavefront writes lds_base + 16 * i. lds_base must be the
+// same for every lane of the wavefront.
+__device__ __forceinline__ void dma16(const uint16_t* src, const uint16_t* lds_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives as its slot j
+// the element i%4 of the four 16-bit values addressed by lane 4j + i/4.
+__device__ __forceinline__ i16x4 lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p));
+}
+
+// Waits until every memory operation this wavefront issued (including LDS
+// DMA writes) has completed.
+__device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+template <int D, int G>
+__global__ __launch_bounds__(256, 1) void k_prefill_mfma(PrefillArgs a) {
+  constexpr int KB = D / 16;  // k-blocks of the QK^T product
+  constexpr int DB = D / 32;  // 32-row d blocks of O^T
+  constexpr int KCH = kBN * D / 8 / 256;  // 16-byte K chunks per thread per tile
+  constexpr int VJ = (kBN / 2) * (D / 8) / 256;  // V jobs (2 tokens x 8 d) per thread
+  static_assert(KCH >= 1 && VJ >= 1, "tile too small for 256 threads");
+  __shared__ Smem<D> sm;
+
+  // ---- which (sequence, kv head, split, query tile) this workgroup is ----
+  const int w = blockIdx.x;
+  const int xcd = w % kXCD, rest = w / kXCD;
+  const int qt = rest % a.n_qt;
+  const int gi = (rest / a.n_qt) * kXCD + xcd;
+  if (gi >= a.n_groups) return;
+  const int split = gi % a.n_splits;
+  const int bh = gi / a.n_splits;
+  const int hk = bh % a.Hkv, b = bh / a.Hkv;
+
+  // Clamped so that no row outside the cache is ever addressed; the host
+  // rejects calls whose prefix plus chunk does not fit.
+  const int P = min(max(a.start[b], 0), a.T_cap);
+  const int n = max(0, min(a.n_new ? min(a.n_new[b], a.C) : a.C, a.T_cap - P));
+  const int R = n * G;                 // valid rows of this (b, hk)
+  const int row0 = qt * kBM;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lc = lane & 31, g = lane >> 5;
+
+  const int kv_end = P + n;  // tokens [0, kv_end) are in the cache
+  int span = (kv_end + a.n_splits - 1) / a.n_splits;
+  span = (span + kBN - 1) / kBN * kBN;
+  const int s0 = split * span;
+  // the last query of this tile bounds the tokens any of its rows attends;
+  // a tile past the valid rows has nothing to do
+  const int last_row = min(row0 + kBM, R) - 1;
+  const int s1 = row0 < R ? min(min(s0 + span, kv_end), P + last_row / G + 1) : s0;
+  const int first_q = row0 / G;  // smallest query index of the tile
+
+  // ---- queries of this wavefront's two row blocks, as MFMA operand B ----
+  bf16x8 qf[kQB][KB];
+  int qrow[kQB];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    const int r = row0 + wave * 64 + qb * 32 + lc;
+    qrow[qb] = r;
+    const bool ok = r < R;
+    const int i = r / G, h = hk * G + r % G;
+    const size_t qoff = (((size_t)b * a.C + i) * a.Hq + h) * D;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = ok ? load_elem(a.q, qoff + kb * 16 + g * 8 + j, a.q_dt) : 0.f;
+        qf[qb][kb][j] = (__bf16)x;
+      }
+    }
+  }
+
+  f32x16 o[kQB][DB];
+  float m[kQB], l[kQB];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    m[qb] = -INFINITY;
+    l[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[qb][db] = f32x16{};
+  }
+
+  const size_t row_stride = (size_t)a.Hkv * D;  // elements between consecutive tokens
+  const uint16_t* kbase = a.k + ((size_t)b * a.T_cap * a.Hkv + hk) * D;
+  const uint16_t* vbase = a.v + ((size_t)b * a.T_cap * a.Hkv + hk) * D;
+
+  // Tiles go from HBM straight into LDS (global_load_lds_dwordx4: each lane
+  // moves 16 bytes, a wavefront fills 1 KB of LDS in lane order), so no
+  // registers are spent on staging. A lane picks the global chunk that the
+  // swizzled layout stores at its LDS position. Token rows past kv_end are
+  // clamped to the last filled row (in bounds, masked later); the tile after
+  // the last one is fetched too and never read.
+  constexpr int RPK = 1024 / (D * 2);          // token rows per 1 KB
+  constexpr int KPT = kBN * D * 2 / 1024;      // 1 KB pieces per tile and tensor
+  static_assert(KPT % kWaves == 0, "tile pieces must split over the wavefronts");
+#define SKV_DMA_TILE(T0, ST)                                                                 \
+  {                                                                                          \
+    _Pragma("unroll") for (int c = 0; c < KPT / kWaves; ++c) {                               \
+      const int piece = wave * (KPT / kWaves) + c;                                           \
+      const int row = piece * RPK + lane / (D / 8);                                          \
+      const int pch = lane % (D / 8);                                                        \
+      const int lch = pch ^ (row & (D / 8 - 1));                                             \
+      const size_t gofs = (size_t)min((T0) + row, kv_end - 1) * row_stride + lch * 8;        \
+      dma16(kbase + gofs, &sm.k[(ST)][piece * 512]);                                         \
+      dma16(vbase + gofs, &sm.v[(ST)][piece * 512]);                                         \
+    }                                                                                        \
+  }
+
+  const int n_tiles = s1 > s0 ? (s1 - s0 + kBN - 1) / kBN : 0;
+  if (n_tiles > 0) SKV_DMA_TILE(s0, 0);
+  wait_all_memory();
+  __syncthreads();
+
+  for (int it = 0; it < n_tiles; ++it) {
+    const int st = it & 1;
+    const int t0 = s0 + it * kBN;
+    SKV_DMA_TILE(t0 + kBN, st ^ 1);
+
+    // The tile is consumed as two 32-token halves, each S^T -> online
+    // softmax -> PV, which keeps the live score registers to 2 x 16.
+    const bool need_mask = (t0 + kBN > s1) || (t0 + kBN - 1 > P + first_q);
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      // ---- S^T = K Q^T for 32 tokens x (2 x 32 queries) ----
+      f32x16 sc[kQB];
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) sc[qb] = f32x16{};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const bf16x8 ka =
+            *reinterpret_cast<const bf16x8*>(&sm.k[st][swz<D>(tb * 32 + lc, kb * 2 + g)]);
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb)
+          sc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[qb][kb], sc[qb], 0, 0, 0);
+      }
+      // Accumulator slot r holds token t0 + tb*32 + (r/4)*8 + 4g + r%4.
+      if (need_mask) {
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+          const int qpos = P + qrow[qb] / G;  // this lane's query position
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int t = t0 + tb * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+            sc[qb][r] = (t >= s1 || t > qpos) ? -INFINITY : sc[qb][r];
+          }
+        }
+      }
+      // ---- online softmax; P^T as operand B of the PV product ----
+      bf16x8 pf[kQB][2];
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) {
+        float tmax = sc[qb][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, sc[qb][r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        // Lazy rescaling: the running max m only moves when the block's max
+        // exceeds it by more than 8 (log2 units), so probabilities stay
+        // <= 2^8 (exact in fp32, in range for bf16) and O, l are rescaled
+        // on a few blocks instead of every one. O and l always refer to the
+        // same m.
+        const float tm = tmax * a.qscale;
+        const bool upd = tm > m[qb] + 8.f;  // also true on the first finite block
+        if (__ballot(upd) != 0ull) {        // wave-uniform branch
+          const float alpha = upd ? fast_exp2(m[qb] - tm) : 1.f;  // m = -inf: 0
+          if (upd) m[qb] = tm;
+          l[qb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
+        }
+        const float m_use = m[qb] == -INFINITY ? 0.f : m[qb];  // fully masked so far
+        float ls = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float p = fast_exp2(fmaf(sc[qb][kk * 8 + j], a.qscale, -m_use));
+            ls += p;
+            pf[qb][kk][j] = (__bf16)p;
+          }
+        l[qb] += ls;
+      }
+      // ---- O^T += V^T P^T ----
+      // Operand A of k-block kk needs, in lane (d = db*32 + lc, g), slot j =
+      // V[tb*32 + 16kk + 4g + j][d] for j < 4 and V[... + 8 + 4g + j - 4][d]
+      // for j >= 4 (the token order of pf). ds_read_b64_tr_b16 gives lane i
+      // of a 16-lane group the element i%4 of the 8 bytes addressed by lane
+      // 4j + i/4 as its slot j, so lane L of group gr addresses token
+      // T + 4g + L/4, elements d0 + 4(L%4) .. +3 with d0 = db*32 + (gr%2)*16.
+      {
+        const int gr = lane >> 4, L = lane & 15;
+        const int dq = (gr & 1) * 16 + 4 * (L & 3);  // d offset within the 32-row block
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const int d = db * 32 + dq;
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            const int r0 = tb * 32 + kk * 16 + 4 * g + (L >> 2);
+            const int r1 = r0 + 8;
+            const uint16_t* p0 = &sm.v[st][swz<D>(r0, d >> 3) + (d & 7)];
+            const uint16_t* p1 = &sm.v[st][swz<D>(r1, d >> 3) + (d & 7)];
+            const i16x4 lo = lds_read_tr16(p0);
+            const i16x4 hi = lds_read_tr16(p1);
+            const bf16x8 va = __builtin_bit_cast(
+                bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb)
+              o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[qb][kk], o[qb][db], 0,
+                                                                   0, 0);
+          }
+        }
+      }
+    }
+
+    // the next tile's DMA has landed in LDS before anyone reads it
+    wait_all_memory();
+    __syncthreads();
+  }
+#undef SKV_DMA_TILE
+
+  // ---- epilogue: this lane holds query column lc of each row block; the
+  // accumulator slot r of d block db is d = db*32 + (r/4)*8 + 4g + r%4 ----
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    const float lt = l[qb] + __shfl_xor(l[qb], 32);
+    const int r = qrow[qb];
+    if (r >= R) continue;
+    const int i = r / G, h = hk * G + r % G;
+    const size_t orow = ((size_t)b * a.C + i) * a.Hq + h;
+    if (a.n_splits == 1) {
+      const float inv = 1.f / lt;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            store_elem(a.out, orow * D + db * 32 + r4 * 8 + g * 4 + e, a.out_dt,
+                       o[qb][db][r4 * 4 + e] * inv);
+    } else {
+      const size_t prow = (size_t)split * a.B * a.C * a.Hq + orow;
+      float* dst = a.ws_o + prow * D;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          float4 x;
+          x.x = o[qb][db][r4 * 4 + 0];
+          x.y = o[qb][db][r4 * 4 + 1];
+          x.z = o[qb][db][r4 * 4 + 2];
+          x.w = o[qb][db][r4 * 4 + 3];
+          *reinterpret_cast<float4*>(dst + db * 32 + r4 * 8 + g * 4) = x;
+        }
+      if (g == 0) {
+        a.ws_ml[prow * 2 + 0] = m[qb];
+        a.ws_ml[prow * 2 + 1] = lt;
+      }
+    }
+  }
+}
+
+// Merge of the split partials: one thread per (row, d). Rows i >= n_new[b]
+// are zeros. Splits that saw no token of a row (m = -inf, l = 0) drop out.
+__global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a, int D) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t rows = (size_t)a.B * a.C * a.Hq;
+  if (idx >= rows * D) return;
+  const size_t row = idx / D;
+  const int d = (int)(idx % D);
+  const int b = (int)(row / ((size_t)a.C * a.Hq));
+  const int i = (int)((row / a.Hq) % a.C);
+  const int P = min(max(a.start[b], 0), a.T_cap);
+  const int n = max(0, min(a.n_new ? min(a.n_new[b], a.C) : a.C, a.T_cap - P));
+  if (i >= n) {
+    store_elem(a.out, idx, a.out_dt, 0.f);
+    return;
+  }
+  const size_t sstride = rows;
+  float M = -INFINITY;
+  for (int s = 0; s < a.n_splits; ++s) M = fmaxf(M, a.ws_ml[(s * sstride + row) * 2]);
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < a.n_splits; ++s) {
+    const size_t pr = s * sstride + row;
+    const float ms = a.ws_ml[pr * 2];
+    if (ms == -INFINITY) continue;
+    const float wgt = fast_exp2(ms - M);
+    L = fmaf(wgt, a.ws_ml[pr * 2 + 1], L);
+    O = fmaf(wgt, a.ws_o[pr * D + d], O);
+  }
+  store_elem(a.out, idx, a.out_dt, O / L);
+}
+
+// Zero-fill of rows i >= n_new[b] when there is no merge pass.
+__global__ __launch_bounds__(256) void k_prefill_zero_tail(PrefillArgs a, int D) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t rows = (size_t)a.B * a.C * a.Hq;
+  if (idx >= rows * D) return;
+  const size_t row = idx / D;
+  const int b = (int)(row / ((size_t)a.C * a.Hq));
+  const int i = (int)((row / a.Hq) % a.C);
+  const int P = min(max(a.start[b], 0), a.T_cap);
+  const int n = max(0, min(a.n_new ? min(a.n_new[b], a.C) : a.C, a.T_cap - P));
+  if (i >= n) store_elem(a.out, idx, a.out_dt, 0.f);
+}
+
+int n_query_tiles(int C, int G) { return (C * G + kBM - 1) / kBM; }
+
+bool dt_ok(int dt) { return dt == SKV_F32 || dt == SKV_BF16; }
+
+}  // namespace
+}  // namespace skv
+
+using namespace skv;
+
+extern "C" int skv_prefill_plan(int B, int C, int H_q, int H_kv, int max_kv_end, int* n_splits) {
+  SKV_REQUIRE(n_splits, SKV_E_INVALID, "skv_prefill_plan: null output");
+  SKV_REQUIRE(B > 0 && C > 0 && H_q > 0 && H_kv > 0 && max_kv_end > 0 && H_q % H_kv == 0,
+              SKV_E_INVALID, "skv_prefill_plan: bad dims (B=%d C=%d H_q=%d H_kv=%d len=%d)", B,
+              C, H_q, H_kv, max_kv_end);
+  // About one workgroup per CU (256 on MI355X), and splits of at least four
+  // 64-token tiles.
+  const long wg = (long)B * H_kv * n_query_tiles(C, H_q / H_kv);
+  long ns = (256 + wg - 1) / wg;
+  const long max_ns = (max_kv_end + 4 * kBN - 1) / (4 * kBN);
+  if (ns > max_ns) ns = max_ns;
+  if (ns > 32) ns = 32;
+  if (ns < 1) ns = 1;
+  *n_splits = (int)ns;
+  return SKV_OK;
+}
+
+extern "C" size_t skv_prefill_workspace_bytes(int B, int C, int H_q, int D, int n_splits) {
+  if (B <= 0 || C <= 0 || H_q <= 0 || D <= 0 || n_splits <= 1) return 0;
+  return (size_t)n_splits * B * C * H_q * (size_t)(D + 2) * sizeof(float);
+}
+
+extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
+                                const void* v_cache, const int32_t* start, const int32_t* n_new,
+                                int B, int C, int H_q, int H_kv, int D, int T_cap, float scale,
+                                int n_splits, void* ws, size_t ws_bytes, int cache_dt, int q_dt,
+                                int out_dt, skv_stream_t stream) {
+  const char* fn = "skv_prefill_attn";
+  SKV_REQUIRE(out && q && k_cache && v_cache && start, SKV_E_INVALID, "%s: null pointer argument",
+              fn);
+  SKV_REQUIRE(B > 0 && C > 0 && H_q > 0 && H_kv > 0 && T_cap > 0, SKV_E_INVALID,
+              "%s: dims must be > 0", fn);
+  SKV_REQUIRE(H_q % H_kv == 0, SKV_E_INVALID, "%s: H_q=%d not a multiple of H_kv=%d", fn, H_q,
+              H_kv);
+  SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(q_dt) && dt_ok(out_dt), SKV_E_INVALID, "%s: bad dtype",
+              fn);
+  SKV_REQUIRE(cache_dt == SKV_BF16, SKV_E_UNSUPPORTED,
+              "%s: the MFMA prefill reads bf16 caches (got fp32)", fn);
+  SKV_REQUIRE(D == 64 || D == 128, SKV_E_UNSUPPORTED, "%s: D=%d (supported: 64, 128)", fn, D);
+  const int G = H_q / H_kv;
+  SKV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, SKV_E_UNSUPPORTED,
+              "%s: no kernel for G=%d", fn, G);
+  SKV_REQUIRE(n_splits >= 1 && n_splits <= 32, SKV_E_INVALID, "%s: n_splits=%d out of range", fn,
+              n_splits);
+  SKV_REQUIRE(scale > 0.f, SKV_E_INVALID, "%s: scale must be > 0", fn);
+  if (n_splits > 1) {
+    const size_t need = skv_prefill_workspace_bytes(B, C, H_q, D, n_splits);
+    SKV_REQUIRE(ws && ws_bytes >= need, SKV_E_WORKSPACE, "%s: workspace %zu bytes < %zu required",
+                fn, ws_bytes, need);
+  }
+  PrefillArgs a;
+  a.q = q; a.out = out;
+  a.k = static_cast<const uint16_t*>(k_cache);
+  a.v = static_cast<const uint16_t*>(v_cache);
+  a.start = start; a.n_new = n_new;
+  a.C = C; a.Hq = H_q; a.Hkv = H_kv; a.T_cap = T_cap;
+  a.qscale = scale * LOG2E;
+  a.q_dt = q_dt; a.out_dt = out_dt;
+  a.n_qt = n_query_tiles(C, G);
+  a.n_splits = n_splits;
+  a.n_groups = B * H_kv * n_splits;
+  a.B = B;
+  a.ws_o = static_cast<float*>(ws);
+  a.ws_ml = n_splits > 1 ? a.ws_o + (size_t)n_splits * B * C * H_q * D : nullptr;
+  const long blocks = (long)((a.n_groups + kXCD - 1) / kXCD) * kXCD * a.n_qt;
+  SKV_REQUIRE(blocks < (1L << 31), SKV_E_UNSUPPORTED, "%s: grid too large", fn);
+  hipStream_t s = (hipStream_t)stream;
+#define SKV_PF(DD, GG)                                                                        \
+  if (D == DD && G == GG)                                                                     \
+    hipLaunchKernelGGL((k_prefill_mfma<DD, GG>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  SKV_PF(64, 1) SKV_PF(64, 2) SKV_PF(64, 4) SKV_PF(64, 8)
+  SKV_PF(128, 1) SKV_PF(128, 2) SKV_PF(128, 4) SKV_PF(128, 8)
+#undef SKV_PF
+  int rc = check_launch(fn);
+  if (rc) return rc;
+  const size_t elems = (size_t)B * C * H_q * D;
+  const unsigned mblocks = (unsigned)((elems + 255) / 256);
+  if (n_splits > 1)
+    hipLaunchKernelGGL(k_prefill_merge, dim3(mblocks), dim3(256), 0, s, a, D);
+  else if (n_new)
+    hipLaunchKernelGGL(k_prefill_zero_tail, dim3(mblocks), dim3(256), 0, s, a, D);
+  return check_launch(fn);
+}

@@ -38,6 +38,10 @@ _SIGNATURES = {
     "skv_decode_plan": (_I, [_I, _I, _I, ctypes.c_longlong, _I, ctypes.POINTER(_I),
                                  ctypes.POINTER(_I)]),
     "skv_decode_workspace_bytes": (_Z, [_I, _I, _I, _I]),
+    "skv_prefill_plan": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_I)]),
+    "skv_prefill_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
+    "skv_prefill_attn": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _Z,
+                              _I, _I, _I, _P]),
     "skv_decode_attn": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _Z,
                              _I, _I, _I, _P]),
     "skv_decode_attn_paged": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I,

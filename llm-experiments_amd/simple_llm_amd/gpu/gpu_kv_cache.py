@@ -311,3 +311,106 @@ def attention_with_kv_cache(ctx: GPUContext, cache: KVCache, layer_idx: int, q_n
     validate_buffer_shape_2d(output, (expected_q_rows, e_q), "output")
     batch_count(ctx)
     decode_attention(ctx, cache, layer_idx, q_new.buffer, output.buffer)
+
+
+# ============================================================================
+# CHUNKED PREFILL (extension; the reference appends one token per call)
+# ============================================================================
+
+
+def _prefill_workspace(ctx: GPUContext, nbytes: int) -> Optional[torch.Tensor]:
+    if nbytes == 0:
+        return None
+    ws = ctx.prefill_workspace
+    if ws is None or ws.numel() < nbytes or ws.device != ctx.device:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=ctx.device)
+        ctx.prefill_workspace = ws
+    return ws
+
+
+def kv_cache_prefill(ctx: GPUContext, cache: KVCache, layer_idx: int, new_k: torch.Tensor,
+                     new_v: torch.Tensor, q: Optional[torch.Tensor] = None,
+                     out: Optional[torch.Tensor] = None, n_new=None,
+                     scale: Optional[float] = None, n_splits: int = 0) -> np.ndarray:
+    """Append a chunk of up to C tokens per sequence to one layer and, if q is
+    given, attend the chunk's queries causally over prefix + chunk.
+
+    new_k, new_v: [batch_size, C, n_kv_heads, head_dim] device tensors (float32
+    or bfloat16). q, out: [batch_size, C, n_heads, head_dim]. n_new: optional
+    per-sequence token counts (<= C) for a ragged chunk; rows i >= n_new[b] of
+    out are zeros. Query row i of sequence b sits at position fill_b + i and
+    attends positions [0, fill_b + i] (the causal mask of the reference's
+    flash_attention, gpu/gpu_kernels.py:695-701, shifted by the cached
+    prefix). The layer's fills advance by n_new. Returns the new fills.
+
+    Raises ValueError (before any GPU work) on a bad layer, shapes, a chunk
+    that would overflow a sequence ("Cache is full"), a paged cache, or an
+    attention request on a float32 cache (the MFMA prefill reads bf16).
+    """
+    _check_layer(cache, layer_idx)
+    if cache.paged:
+        raise ValueError("kv_cache_prefill: paged caches take single-token appends only")
+    layer = cache.layers[layer_idx]
+    dev = layer.lens.device
+    B, Hq, Hkv, D, T = (cache.batch_size, cache.n_heads, cache.n_kv_heads, cache.head_dim,
+                        cache.max_seq_len)
+    for t, nm in ((new_k, "new_k"), (new_v, "new_v")):
+        _check_tensor(t, nm, dev)
+        if t.dim() != 4 or t.shape[0] != B or t.shape[2] != Hkv or t.shape[3] != D:
+            raise ValueError(f"{nm} must be [batch_size, C, n_kv_heads, head_dim] = "
+                             f"[{B}, C, {Hkv}, {D}], got {tuple(t.shape)}")
+    if new_k.shape != new_v.shape or new_k.dtype != new_v.dtype:
+        raise ValueError("new_k and new_v must share shape and dtype")
+    C = int(new_k.shape[1])
+    if C <= 0:
+        raise ValueError("the chunk must hold at least one token")
+    n_host = (np.full(B, C, np.int64) if n_new is None
+              else np.asarray(n_new, dtype=np.int64).reshape(B))
+    if (n_host < 0).any() or (n_host > C).any():
+        raise ValueError(f"n_new entries must lie in [0, {C}]")
+    start = layer.host_lens.copy()
+    if int((start + n_host).max()) > T:
+        raise ValueError(f"Cache is full: chunk of {int(n_host.max())} tokens after "
+                         f"current_len={int(start.max())}, max_seq_len={T}")
+    want_attn = q is not None
+    if want_attn:
+        if out is None:
+            raise ValueError("kv_cache_prefill: out is required with q")
+        for t, nm in ((q, "q"), (out, "output")):
+            _check_tensor(t, nm, dev)
+            if tuple(t.shape) != (B, C, Hq, D):
+                raise ValueError(f"{nm} must be [{B}, {C}, {Hq}, {D}], got {tuple(t.shape)}")
+        if cache.dtype != torch.bfloat16:
+            raise ValueError("kv_cache_prefill: attention over a float32 cache is not "
+                             "supported (the MFMA prefill reads bf16 caches)")
+    batch_count(ctx)
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    cdt, idt = _lib.dtype_code(cache.dtype), _lib.dtype_code(new_k.dtype)
+    n_dev = (None if n_new is None else
+             torch.from_numpy(n_host.astype(np.int32)).to(dev, non_blocking=False))
+    n_ptr = n_dev.data_ptr() if n_dev is not None else None
+    kc, vc = layer.k_cache.buffer, layer.v_cache.buffer
+    rc = L.skv_append_chunk(kc.data_ptr(), vc.data_ptr(), new_k.data_ptr(), new_v.data_ptr(),
+                            layer.lens.data_ptr(), n_ptr, B, C, Hkv, D, T, cdt, idt, stream)
+    _lib.check(rc, "skv_append_chunk")
+    if want_attn:
+        ns = ctypes.c_int()
+        if n_splits > 0:
+            ns.value = int(n_splits)
+        else:
+            _lib.check(L.skv_prefill_plan(B, C, Hq, Hkv, int((start + n_host).max()),
+                                          ctypes.byref(ns)), "skv_prefill_plan")
+        need = L.skv_prefill_workspace_bytes(B, C, Hq, D, ns.value)
+        ws = _prefill_workspace(ctx, need)
+        sc = float(scale) if scale is not None else 1.0 / float(np.sqrt(D))
+        rc = L.skv_prefill_attn(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                layer.lens.data_ptr(), n_ptr, B, C, Hq, Hkv, D, T, sc, ns.value,
+                                ws.data_ptr() if ws is not None else None,
+                                ws.numel() if ws is not None else 0, cdt,
+                                _lib.dtype_code(q.dtype), _lib.dtype_code(out.dtype), stream)
+        _lib.check(rc, "skv_prefill_attn")
+    rc = L.skv_advance(layer.lens.data_ptr(), n_ptr, C, B, T, stream)
+    _lib.check(rc, "skv_advance")
+    layer.host_lens = np.minimum(start + n_host, T)
+    return layer.host_lens.copy()

@@ -81,8 +81,9 @@ class GPUContext:
     batch_state: Optional[BatchState]
     pipeline_cache: PipelineCache
     reduction_workspace: Optional[GPUBuffer1D] = None
-    # split-K workspace for decode attention, grown on demand
+    # split-K workspaces of decode and prefill attention, grown on demand
     decode_workspace: Optional[torch.Tensor] = None
+    prefill_workspace: Optional[torch.Tensor] = None
 
 
 class KVCacheLayer:
