@@ -164,6 +164,46 @@ int skv_prefill_attn(void* out, const void* q, const void* k_cache, const void* 
                      int H_kv, int D, int T_cap, float scale, int n_splits, void* ws,
                      size_t ws_bytes, int cache_dt, int q_dt, int out_dt, skv_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Decode-step ops of the model around the cache (fp32). They replace the
+ * JAX model's per-token work (simple-llm/src/jax_backend.py:78-148) and the
+ * greedy pick of generate_text (simple-llm/src/generate.py:29-69,
+ * jax_backend.py:466-469), so a whole decode step runs on the GPU.
+ * ------------------------------------------------------------------------ */
+
+/* x[m, :] = embedding[ids[m], :] + pos_table[pos[m], :]
+ * (jax_backend.py:144). ids and pos are clamped into the tables. */
+int skv_embed(float* x, const int32_t* ids, const int32_t* pos, const float* embedding,
+              const float* pos_table, int M, int d, int vocab, int ctx, skv_stream_t stream);
+
+/* y[m, :] = (x[m, :] - mean) / sqrt(var + eps) * gamma + beta, population
+ * variance (jax_backend.py:78-82). d <= 4096; y may equal x. */
+int skv_layernorm(float* y, const float* x, const float* gamma, const float* beta, int M, int d,
+                  float eps, skv_stream_t stream);
+
+/* y = act(x . w_t^T + bias) + residual, x [M, K], w_t [N, K] (the
+ * transpose of the reference's [K, N] weight), y [M, N]. activation 0 =
+ * none, 1 = GELU, tanh form (jax.nn.gelu's default, jax_backend.py:127).
+ * bias and residual may be NULL; residual may equal y, x may not.
+ * split_cols > 0 writes column n to segment n / split_cols of a
+ * [N / split_cols][M][split_cols] output (q, k, v of a fused projection as
+ * three contiguous [M, d] blocks). K must be a multiple of 4. */
+int skv_linear(float* y, const float* x, const float* w_t, const float* bias,
+               const float* residual, int M, int N, int K, int activation, int split_cols,
+               skv_stream_t stream);
+
+/* out[m] = index of the largest x[m, :], the first on ties
+ * (jnp.argmax, jax_backend.py:469). */
+int skv_argmax(int32_t* out, const float* x, int M, int N, skv_stream_t stream);
+
+/* Next input token of each sequence (generate.py:29-69 with a cache):
+ * ids[b] = prompt[b, pos[b]] while pos[b] < prompt_len[b], else
+ * argmax_prev[b]; the token is also stored at seq[b, pos[b]] when
+ * pos[b] < seq_cap. pos is the sequence's current fill (layer 0's lens). */
+int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
+                    const int32_t* prompt, const int32_t* prompt_len, const int32_t* pos, int B,
+                    int max_prompt, int seq_cap, skv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,366 @@
+"""The reference model's decode path on the KV cache, on gfx950.
+
+Drop-in for the caller side of the hot path:
+  TransformerModelParams   simple-llm/src/common_backend.py:4-11
+  LayerParams field names  simple-llm/src/jax_backend.py:36-55
+  forward                  simple-llm/src/jax_backend.py:143-148 (logits of every
+                           position; here computed step by step on the cache)
+  generate_text            simple-llm/src/generate.py:8-71 (same signature)
+
+The model is the reference's JAX model (pre-LN blocks, bias-free attention
+projections, tanh GELU MLP, tied logits, positional table of
+jax_backend.py:25-33). One decode step runs every sequence's next token
+through all layers as HIP kernels of libskv.so: embedding + position,
+LayerNorm, fused q/k/v projection, the cache append (skv_append), decode
+attention (skv_decode_attn), output projection with residual, MLP with
+GELU and residual, tied logits and argmax. PyTorch only owns the memory.
+
+Differences from the reference's generate_text, both documented choices:
+  * tokens attend their cached prefix at their absolute positions; the
+    reference re-runs a left-padded window of context_size per token, which
+    shifts positions while the window is not full (its tokens are therefore
+    not a parity target; parity is checked on the logits of the final
+    sequence, teacher forced);
+  * sampling is greedy (temperature 0, the reference's jnp.argmax branch,
+    jax_backend.py:466-469); other sampling settings raise ValueError.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from .gpu import gpu
+from .gpu.gpu_types import GPUContext, KVCache
+
+LAYER_FIELDS = ("attn_wq", "attn_wk", "attn_wv", "attn_wo", "ff_w1", "ff_b1", "ff_w2",
+                "ff_b2", "ln_gamma1", "ln_beta1", "ln_gamma2", "ln_beta2")
+
+
+@dataclasses.dataclass
+class TransformerModelParams:
+    """Model shape record (reference: common_backend.py:4-11)."""
+
+    vocab_size: int
+    embedding_dim: int
+    context_size: int
+    n_heads: int
+    n_layers: int
+    epochs: list = dataclasses.field(default_factory=list)
+
+
+def positional_encoding(seq_len: int, dim: int) -> np.ndarray:
+    """The reference's positional table (jax_backend.py:25-33), float32:
+    sin of the even-index angles, then cos of the odd-index angles."""
+    pos = np.arange(seq_len, dtype=np.float64)[:, None]
+    i = np.arange(dim)[None, :]
+    ang = pos / (10000.0 ** (2 * (i // 2) / dim))
+    return np.concatenate([np.sin(ang[:, 0::2]), np.cos(ang[:, 1::2])], -1).astype(np.float32)
+
+
+def initialize_params(tm: TransformerModelParams, seed: int = 0, std: float = 0.02,
+                      mlp_dim: Optional[int] = None) -> dict:
+    """Seeded N(0, std) weights in the reference's layout ([in, out] float32
+    matrices, zero biases, LayerNorm gamma 1 / beta 0), drawn in the field
+    order of jax_backend.py:327-359 from numpy.random.default_rng(seed)."""
+    rng = np.random.default_rng(seed)
+    d, mlp = tm.embedding_dim, mlp_dim or 4 * tm.embedding_dim
+
+    def w(*shape):
+        return (rng.standard_normal(shape) * std).astype(np.float32)
+
+    layers = []
+    for _ in range(tm.n_layers):
+        layers.append({
+            "attn_wq": w(d, d), "attn_wk": w(d, d), "attn_wv": w(d, d), "attn_wo": w(d, d),
+            "ff_w1": w(d, mlp), "ff_b1": np.zeros(mlp, np.float32), "ff_w2": w(mlp, d),
+            "ff_b2": np.zeros(d, np.float32), "ln_gamma1": np.ones(d, np.float32),
+            "ln_beta1": np.zeros(d, np.float32), "ln_gamma2": np.ones(d, np.float32),
+            "ln_beta2": np.zeros(d, np.float32),
+        })
+    return {"embedding": w(tm.vocab_size, d),
+            "pos_encoding": positional_encoding(tm.context_size, d), "layers": layers}
+
+
+class _Buffers:
+    """Per-batch-size activations of one decode step (all device, fp32)."""
+
+    def __init__(self, dev, B, d, mlp, vocab):
+        self.B = B
+        self.ids = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.x = torch.zeros((B, d), device=dev)
+        self.h = torch.zeros((B, d), device=dev)
+        self.qkv = torch.zeros((3, B, d), device=dev)
+        self.attn = torch.zeros((B, d), device=dev)
+        self.ff = torch.zeros((B, mlp), device=dev)
+        self.logits = torch.zeros((B, vocab), device=dev)
+        self.argmax = torch.zeros(B, dtype=torch.int32, device=dev)
+
+
+class TransformerModel:
+    """The reference model's weights on the device, laid out for the decode
+    kernels: every matrix transposed to [out, in] (rows read contiguously by
+    skv_linear) and the q/k/v projections fused into one [3d, d] matrix."""
+
+    def __init__(self, ctx: GPUContext, tm_params: TransformerModelParams,
+                 params: Optional[dict] = None, kv_dtype: torch.dtype = torch.float32):
+        self.ctx = ctx
+        self.tm_params = tm_params
+        self.kv_dtype = kv_dtype
+        d = tm_params.embedding_dim
+        if d % tm_params.n_heads:
+            raise ValueError("embedding_dim must be a multiple of n_heads")
+        self.head_dim = d // tm_params.n_heads
+        params = params if params is not None else initialize_params(tm_params)
+        self.params = params
+        dev = ctx.device
+
+        def t(a, transpose=False):
+            a = np.asarray(a, np.float32)
+            return torch.from_numpy(np.ascontiguousarray(a.T if transpose else a)).to(dev)
+
+        self.emb = t(params["embedding"])
+        if tuple(self.emb.shape) != (tm_params.vocab_size, d):
+            raise ValueError(f"embedding must be [{tm_params.vocab_size}, {d}]")
+        self.pe = t(params["pos_encoding"])
+        if self.pe.shape[0] < tm_params.context_size:
+            raise ValueError("pos_encoding has fewer rows than context_size")
+        self.layers = []
+        for lp in params["layers"][:tm_params.n_layers]:
+            wqkv = np.concatenate([np.asarray(lp[k], np.float32).T
+                                   for k in ("attn_wq", "attn_wk", "attn_wv")], 0)
+            self.layers.append({
+                "wqkv_t": t(wqkv), "wo_t": t(lp["attn_wo"], True),
+                "w1_t": t(lp["ff_w1"], True), "b1": t(lp["ff_b1"]),
+                "w2_t": t(lp["ff_w2"], True), "b2": t(lp["ff_b2"]),
+                "g1": t(lp["ln_gamma1"]), "be1": t(lp["ln_beta1"]),
+                "g2": t(lp["ln_gamma2"]), "be2": t(lp["ln_beta2"]),
+            })
+        if len(self.layers) != tm_params.n_layers:
+            raise ValueError("params hold fewer layers than n_layers")
+        self.mlp_dim = self.layers[0]["w1_t"].shape[0]
+        self._bufs = {}
+
+    # -- cache and buffers ---------------------------------------------------
+
+    def new_cache(self, batch_size: int) -> KVCache:
+        tm = self.tm_params
+        return gpu.kv_cache_create(self.ctx, gpu.KVCacheConfig(
+            batch_size=batch_size, max_seq_len=tm.context_size, n_layers=tm.n_layers,
+            n_heads=tm.n_heads, head_dim=self.head_dim, dtype=self.kv_dtype))
+
+    def buffers(self, B: int) -> _Buffers:
+        if B not in self._bufs:
+            tm = self.tm_params
+            self._bufs[B] = _Buffers(self.ctx.device, B, tm.embedding_dim, self.mlp_dim,
+                                     tm.vocab_size)
+        return self._bufs[B]
+
+    # -- one decode step -----------------------------------------------------
+
+    def forward_step(self, cache: KVCache, ids: torch.Tensor) -> torch.Tensor:
+        """Run token ids[b] of every sequence at its current fill through all
+        layers, appending its K/V to the cache; returns logits [B, V] (a
+        buffer reused by the next call). ids: int32 device tensor [B].
+        Sequences whose cache is full are not appended to (their logits are
+        not meaningful)."""
+        B = cache.batch_size
+        if cache.n_kv_heads != cache.n_heads or cache.paged:
+            raise ValueError("the model path uses a contiguous multi-head cache")
+        bf = self.buffers(B)
+        if ids.data_ptr() != bf.ids.data_ptr():
+            bf.ids.copy_(ids)
+        self._launch_step(cache, bf)
+        # host mirror: every layer appended where the sequence had room
+        for layer in cache.layers:
+            layer.host_lens = np.minimum(layer.host_lens + 1, cache.max_seq_len)
+        return bf.logits
+
+    def _decode_plan(self, cache: KVCache):
+        key = ("plan", cache.batch_size)
+        if key not in self._bufs:
+            T = cache.max_seq_len
+            chunk, n = gpu.decode_plan(self.ctx, cache.batch_size, cache.n_kv_heads, T,
+                                       cache.batch_size * T)
+            L = _lib.lib()
+            need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, n)
+            ws = torch.empty(max(need, 1), dtype=torch.uint8, device=self.ctx.device)
+            self._bufs[key] = (chunk, n, ws)
+        return self._bufs[key]
+
+    def _launch_step(self, cache: KVCache, bf: _Buffers) -> None:
+        L = _lib.lib()
+        tm = self.tm_params
+        B, d, H, D, T = cache.batch_size, tm.embedding_dim, tm.n_heads, self.head_dim, \
+            cache.max_seq_len
+        s = _lib.stream_handle(self.ctx.device)
+        chk = _lib.check
+        cdt = _lib.dtype_code(cache.dtype)
+        chunk, n_chunks, ws = self._decode_plan(cache)
+        scale = 1.0 / float(np.sqrt(D))
+        x, h, qkv, attn, ff = bf.x.data_ptr(), bf.h.data_ptr(), bf.qkv.data_ptr(), \
+            bf.attn.data_ptr(), bf.ff.data_ptr()
+        q_ptr, k_ptr, v_ptr = qkv, qkv + B * d * 4, qkv + 2 * B * d * 4
+        lens0 = cache.layers[0].lens.data_ptr()
+        chk(L.skv_embed(x, bf.ids.data_ptr(), lens0, self.emb.data_ptr(), self.pe.data_ptr(), B, d,
+                        tm.vocab_size, self.pe.shape[0], s), "skv_embed")
+        for lw, layer in zip(self.layers, cache.layers):
+            kc, vc = layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr()
+            chk(L.skv_layernorm(h, x, lw["g1"].data_ptr(), lw["be1"].data_ptr(), B, d, 1e-5, s),
+                "skv_layernorm")
+            chk(L.skv_linear(qkv, h, lw["wqkv_t"].data_ptr(), None, None, B, 3 * d, d, 0, d, s),
+                "skv_linear")
+            chk(L.skv_append(kc, vc, k_ptr, v_ptr, layer.lens.data_ptr(), B, H, D, T, cdt,
+                             _lib.F32, s), "skv_append")
+            chk(L.skv_decode_attn(attn, q_ptr, kc, vc, layer.lens.data_ptr(), B, H, H, D, T, scale,
+                                  chunk, n_chunks, ws.data_ptr(), ws.numel(), cdt, _lib.F32,
+                                  _lib.F32, s), "skv_decode_attn")
+            chk(L.skv_linear(x, attn, lw["wo_t"].data_ptr(), None, x, B, d, d, 0, 0, s),
+                "skv_linear")
+            chk(L.skv_layernorm(h, x, lw["g2"].data_ptr(), lw["be2"].data_ptr(), B, d, 1e-5, s),
+                "skv_layernorm")
+            chk(L.skv_linear(ff, h, lw["w1_t"].data_ptr(), lw["b1"].data_ptr(), None, B,
+                             self.mlp_dim, d, 1, 0, s), "skv_linear")
+            chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, B, d,
+                             self.mlp_dim, 0, 0, s), "skv_linear")
+        chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, B,
+                         tm.vocab_size, d, 0, 0, s), "skv_linear")
+
+    # -- many steps ----------------------------------------------------------
+
+    def forward(self, tokens: np.ndarray) -> np.ndarray:
+        """Logits of every position of [B, T] token ids (T <= context_size),
+        computed step by step on a fresh cache: row t equals the reference's
+        forward (jax_backend.py:143-148) at position t. Returns float32 host
+        array [B, T, V]."""
+        tokens = np.asarray(tokens, np.int32)
+        B, T = tokens.shape
+        if T > self.tm_params.context_size:
+            raise ValueError("sequence longer than context_size")
+        cache = self.new_cache(B)
+        out = np.zeros((B, T, self.tm_params.vocab_size), np.float32)
+        ids = torch.from_numpy(tokens).to(self.ctx.device)
+        for t in range(T):
+            out[:, t] = self.forward_step(cache, ids[:, t].contiguous()).cpu().numpy()
+        return out
+
+
+class Generator:
+    """Greedy generation of a batch of (possibly ragged) prompts on the device.
+
+    Every step feeds each sequence its next prompt token while it is inside
+    its prompt and its previous argmax afterwards (skv_next_tokens), so the
+    loop never waits for the host. With use_graph the step is captured once
+    into a HIP graph (torch.cuda.CUDAGraph over the library's launches) and
+    replayed.
+    """
+
+    def __init__(self, model: TransformerModel, prompts: Sequence[Sequence[int]],
+                 total_len: Sequence[int] | int, use_graph: bool = False):
+        tm = model.tm_params
+        self.model = model
+        B = len(prompts)
+        if B == 0:
+            raise ValueError("no prompts")
+        plen = np.array([len(p) for p in prompts], np.int32)
+        if (plen <= 0).any():
+            raise ValueError("every prompt needs at least one token")
+        tot = np.broadcast_to(np.asarray(total_len, np.int64), (B,)).astype(np.int64)
+        if (tot < plen).any():
+            raise ValueError("total_len shorter than a prompt")
+        if int(tot.max()) > tm.context_size:
+            raise ValueError(f"total length {int(tot.max())} exceeds context_size "
+                             f"{tm.context_size} (the cache does not slide)")
+        for p in prompts:
+            if min(p) < 0 or max(p) >= tm.vocab_size:
+                raise ValueError("prompt token out of the vocabulary")
+        dev = model.ctx.device
+        self.B, self.plen, self.tot = B, plen, tot
+        Pm = int(plen.max())
+        pr = np.zeros((B, Pm), np.int32)
+        for b, p in enumerate(prompts):
+            pr[b, :len(p)] = p
+        self.prompt = torch.from_numpy(pr).to(dev)
+        self.prompt_len = torch.from_numpy(plen).to(dev)
+        self.seq = torch.zeros((B, tm.context_size), dtype=torch.int32, device=dev)
+        self.cache = model.new_cache(B)
+        self.bufs = model.buffers(B)
+        self.steps = int(tot.max()) - 1  # position p's step produces token p + 1
+        self.use_graph = use_graph
+        self.graph = None
+
+    def _one_step(self):
+        L = _lib.lib()
+        m, c, bf = self.model, self.cache, self.bufs
+        s = _lib.stream_handle(m.ctx.device)
+        _lib.check(L.skv_next_tokens(bf.ids.data_ptr(), self.seq.data_ptr(), bf.argmax.data_ptr(),
+                                     self.prompt.data_ptr(), self.prompt_len.data_ptr(),
+                                     c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
+                                     self.seq.shape[1], s), "skv_next_tokens")
+        m._launch_step(c, bf)
+        _lib.check(L.skv_argmax(bf.argmax.data_ptr(), bf.logits.data_ptr(), self.B,
+                                m.tm_params.vocab_size, s), "skv_argmax")
+
+    def run(self) -> List[List[int]]:
+        """Run all steps; returns every sequence's tokens (prompt + output)."""
+        steps = self.steps
+        if steps > 0:
+            if self.use_graph:
+                self._one_step()  # eager first step: workspaces exist before capture
+                torch.cuda.synchronize()
+                if self.graph is None and steps > 1:
+                    # stream capture records the launches without running them
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g):
+                        self._one_step()
+                    self.graph = g
+                for _ in range(steps - 1):
+                    self.graph.replay()
+            else:
+                for _ in range(steps):
+                    self._one_step()
+        # record the last argmax at its position (the final token)
+        L = _lib.lib()
+        s = _lib.stream_handle(self.model.ctx.device)
+        _lib.check(L.skv_next_tokens(self.bufs.ids.data_ptr(), self.seq.data_ptr(),
+                                     self.bufs.argmax.data_ptr(), self.prompt.data_ptr(),
+                                     self.prompt_len.data_ptr(),
+                                     self.cache.layers[0].lens.data_ptr(), self.B,
+                                     self.prompt.shape[1], self.seq.shape[1], s),
+                   "skv_next_tokens")
+        for layer in self.cache.layers:
+            layer.host_lens = layer.lens.cpu().numpy().astype(np.int64)
+        seq = self.seq.cpu().numpy()
+        return [seq[b, :int(self.tot[b])].tolist() for b in range(self.B)]
+
+
+def generate_text(model: TransformerModel, prompt_tokens, max_tokens=100, temperature=1.0,
+                  top_k=0, top_p=1.0, min_p=0.0, repetition_penalty=1.0, repetition_window=64,
+                  use_graph: bool = True):
+    """Generate max_tokens tokens after prompt_tokens (generate.py:8-71's
+    signature); returns prompt + generated tokens as a list of ints.
+
+    Greedy only: temperature must be 0 (and the other filters at their
+    neutral values); anything else raises ValueError. The prompt plus the
+    output must fit in context_size."""
+    if temperature != 0.0:
+        raise ValueError("only greedy decoding (temperature=0) runs on the device; "
+                         "sampling with temperature/top-k/top-p/min-p is not built")
+    if repetition_penalty != 1.0:
+        raise ValueError("repetition_penalty is not supported by the device decoder")
+    prompt = [int(t) for t in prompt_tokens]
+    if max_tokens <= 0:
+        return prompt
+    g = Generator(model, [prompt], len(prompt) + int(max_tokens), use_graph=use_graph)
+    return g.run()[0]
+
+
+def generate_batch(model: TransformerModel, prompts: Sequence[Sequence[int]], total_len,
+                   use_graph: bool = True) -> List[List[int]]:
+    """Greedy generation of a ragged batch until each sequence holds
+    total_len tokens (an int or one per sequence)."""
+    return Generator(model, prompts, total_len, use_graph=use_graph).run()
