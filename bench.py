@@ -55,6 +55,10 @@ B, H, D, T_CAP, FILL = 4, 16, 128, 32768, 32000
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--workload", choices=["c4", "c1", "c2", "c3", "c5"], default="c4",
+                   help="BASELINE config: c4 (default, the headline line), c1 tiny LM "
+                        "generate, c2 fp32 KV microbench, c3 GPT-2-small ragged batch, "
+                        "c5 GQA paged ragged decode")
     p.add_argument("--steps", type=int, default=256)
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -188,6 +192,310 @@ def cpu_baseline(args, k_dev, v_dev, q_all, k_all, v_all):
     }
 
 
+def _record(metric, value, unit, steps, warmup, ms_per_step, dtype, config, roofline, cpu,
+            **extra):
+    rec = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps,
+           "warmup": warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic",
+           "config": config, "roofline": roofline, "cpu_baseline": cpu}
+    rec.update(extra)
+    return rec
+
+
+def _time_reference_generate(params, prompt, n_heads, context, budget_s, max_tokens):
+    """The reference's generate loop (generate.py:29-69, greedy): a full
+    float32 torch CPU forward over the left-padded window per token."""
+    import torch
+
+    from oracle import model_oracle as mo
+
+    fwd = lambda p, ids: mo.torch_forward_fp32(p, ids, n_heads).numpy()  # noqa: E731
+    with torch.no_grad():
+        mo.reference_generate(params, prompt, 1, n_heads, context, forward_fn=fwd)  # warm-up
+        n, t0 = 0, time.perf_counter()
+        while n < max_tokens and time.perf_counter() - t0 < budget_s:
+            mo.reference_generate(params, prompt + [0] * n, 1, n_heads, context, forward_fn=fwd)
+            n += 1
+        dt = time.perf_counter() - t0
+    return n, dt
+
+
+def _model_workload(args, ctx, tm, prompts, total_len, label, kv_dtypes):
+    """Greedy generation of `prompts` to `total_len` tokens with HIP-graph
+    replay; per KV dtype, the mean of 3 timed runs after a warm-up run."""
+    import numpy as np
+    import torch
+
+    from simple_llm_amd import model as M
+
+    params = M.initialize_params(tm, seed=0, std=0.02)
+    model = M.TransformerModel(ctx, tm, params)
+    runs = {}
+    for kvd in kv_dtypes:
+        model.kv_dtype = kvd
+        g = M.Generator(model, prompts, total_len, use_graph=True)
+        out = g.run()  # warm-up: eager first step, graph capture, replays
+        times = []
+        for _ in range(3):
+            g.reset()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out2 = g.run()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        assert out2 == out, "graph replays must reproduce the first run"
+        gen = sum(total_len - len(p) for p in prompts)
+        runs[str(kvd).replace("torch.", "")] = {
+            "run_s": float(np.mean(times)), "steps": g.steps,
+            "generated_tokens": gen, "tokens_per_s": gen / float(np.mean(times)),
+            "step_us": float(np.mean(times)) / g.steps * 1e6}
+    d, L, V = tm.embedding_dim, tm.n_layers, tm.vocab_size
+    weight_bytes = 4 * (V * d + L * (4 * d * d + 2 * d * model.mlp_dim + model.mlp_dim + 7 * d))
+    return params, model, runs, weight_bytes
+
+
+def run_c1(args, ctx):
+    """tiny LM (4 layers, d 256, 4 x 64, MLP 1024, vocab
+    256, context 256, fp32, N(0, 0.02) weights from seed 0), 64-token prompt
+    drawn from seed 1, greedy decode of 192 tokens, batch 1."""
+    import numpy as np
+    import torch
+
+    from simple_llm_amd import model as M
+
+    tm = M.TransformerModelParams(256, 256, 256, 4, 4)
+    prompt = np.random.default_rng(1).integers(0, 256, 64).tolist()
+    params, model, runs, wbytes = _model_workload(args, ctx, tm, [prompt], 256, "c1",
+                                                  [torch.float32])
+    r = runs["float32"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        n, dt = _time_reference_generate(params, prompt, 4, 256, args.cpu_seconds, 192)
+        cpu = {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"{n} greedy tokens of the reference's generate loop (full float32 "
+                         f"forward over the 256-token left-padded window per token, torch CPU), "
+                         f"{dt:.1f} s"}
+    return _record(
+        "decode tokens/sec", r["tokens_per_s"], "tokens/s", r["steps"], 1, r["step_us"] / 1e3,
+        "fp32",
+        {"workload": "C1 tiny LM: 4 layers, d 256, 4 heads x 64, MLP 1024, vocab 256, context "
+                     "256, fp32 weights and KV, 64-token prompt + 192 greedy tokens, batch 1; "
+                     "prompt fed token by token through the same cached step (HIP graph)",
+         "batch": 1, "prompt": 64, "generated": 192},
+        {"bound": "launch latency", "note": "12.8 MB of weights per token; ~40 launches per "
+                                            "step replayed from one HIP graph",
+         "achieved": wbytes / (r["step_us"] * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": wbytes / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, "traffic": None},
+        cpu, runs=runs)
+
+
+def run_c3(args, ctx):
+    """GPT-2-small shape (12 layers, d 768, 12 x 64,
+    vocab 50304, context 1024), batch 16, prompt lengths U[32, 512] (ragged),
+    greedy decode to 1024 tokens each; KV in fp32 and in bf16."""
+    import numpy as np
+    import torch
+
+    from simple_llm_amd import model as M
+
+    tm = M.TransformerModelParams(50304, 768, 1024, 12, 12)
+    r = np.random.default_rng(1)
+    plen = r.integers(32, 513, 16)
+    prompts = [r.integers(0, 50304, int(n)).tolist() for n in plen]
+    params, model, runs, wbytes = _model_workload(args, ctx, tm, prompts, 1024, "c3",
+                                                  [torch.float32, torch.bfloat16])
+    # per step: all weights + every sequence's K and V prefix (mean fill over the run)
+    mean_fill = 1024 / 2
+    kv = {"float32": 4, "bfloat16": 2}
+    roof = {}
+    for k, run in runs.items():
+        by = wbytes + 16 * 12 * 2 * mean_fill * 768 * kv[k]
+        roof[k] = by / (run["step_us"] * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        n, dt = _time_reference_generate(params, prompts[0], 12, 1024, args.cpu_seconds, 4)
+        cpu = {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"{n} greedy tokens of one sequence through the reference's generate "
+                         f"loop (full float32 forward over the 1024-token window per token, "
+                         f"~292 GFLOP each, torch CPU), {dt:.1f} s; the reference runs batch 1"}
+    r32 = runs["float32"]
+    return _record(
+        "decode tokens/sec", r32["tokens_per_s"], "tokens/s", r32["steps"], 1,
+        r32["step_us"] / 1e3, "fp32",
+        {"workload": "C3 GPT-2-small shape: 12 layers, d 768, 12 heads x 64, vocab 50304, "
+                     "context 1024, batch 16, prompts U[32,512], greedy to 1024 tokens, fp32 "
+                     "weights; value = generated tokens/s with the fp32 KV cache (bf16 KV in "
+                     "runs)", "batch": 16, "prompt_lens": plen.tolist()},
+        {"bound": "hbm", "achieved": roof["float32"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": roof["float32"] / HBM_PEAK_GBS, "traffic": None,
+         "note": "per step: all weights + mean K/V prefix of 16 sequences, over step time",
+         "achieved_bf16_kv": roof["bfloat16"]},
+        cpu, runs=runs)
+
+
+def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt, label):
+    """Timed loop of append + decode attention on one prepared cache layer."""
+    import numpy as np
+    import torch
+
+    from simple_llm_amd.gpu import gpu
+
+    dev = ctx.device
+    B = cache.batch_size
+    g = torch.Generator(device=dev).manual_seed(2)
+    n_in = args.warmup + steps
+    q_all = torch.randn((n_in, B, Hq, Dh), generator=g, device=dev)
+    k_all = torch.randn((n_in, B, Hkv, Dh), generator=g, device=dev)
+    v_all = torch.randn((n_in, B, Hkv, Dh), generator=g, device=dev)
+    out = torch.empty((B, Hq, Dh), device=dev)
+    cap = (cache.block_table.shape[1] * cache.block_size) if cache.paged else cache.max_seq_len
+    max_len = int(min(lens0.max() + steps, cap))
+    layer = cache.layers[0]
+
+    def set_lens(v):
+        layer.lens.copy_(torch.from_numpy(v.astype(np.int32)))
+        layer.host_lens = v.astype(np.int64).copy()
+
+    def step(i, ev=None):
+        gpu.kv_cache_append(ctx, cache, 0, k_all[i], v_all[i])
+        if ev is not None:
+            ev[0].record()
+        gpu.decode_attention(ctx, cache, 0, q_all[i], out, max_len=max_len)
+        if ev is not None:
+            ev[1].record()
+
+    set_lens(lens0)
+    for i in range(args.warmup):
+        step(steps + i)
+    torch.cuda.synchronize()
+    set_lens(lens0)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = np.array([a.elapsed_time(b) for a, b in evs])
+    # fills at each call: lens after the append (full sequences stay put)
+    fills, active = [], 0
+    cur = lens0.astype(np.int64).copy()
+    for _ in range(steps):
+        act = cur < cap
+        active += int(act.sum())
+        cur = np.where(act, cur + 1, cur)
+        fills.append(cur.copy())
+    byts = float(np.mean([algorithmic_bytes(f, h_q=Hq, h_kv=Hkv, d=Dh, s_kv=s_kv, s_q=4, s_o=4)
+                          for f in fills]))
+    mean_s = float(ms.mean()) * 1e-3
+    chunk, n_chunks = gpu.decode_plan(ctx, B, Hkv, max_len, int(lens0.sum()))
+    roof = {"kernel": "decode attention (k_decode_partial + k_decode_merge)", "bound": "hbm",
+            "achieved": byts / mean_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": byts / mean_s / 1e9 / HBM_PEAK_GBS, "traffic": None,
+            "mean_call_us": mean_s * 1e6, "algorithmic_bytes_per_call": byts,
+            "split_k": {"chunk_tokens": chunk, "n_chunks": n_chunks}}
+    return wall, active, roof, (q_all, k_all, v_all)
+
+
+def run_c5(args, ctx):
+    """64 sequences, 32 query heads over 8 kv heads,
+    head_dim 128, bf16, lognormal lengths (median 1500, sigma 0.8, clipped to
+    [16, 8192]), 16-token pages with a seeded random page table, 128 steps of
+    append + decode attention."""
+    import numpy as np
+    import torch
+
+    from simple_llm_amd.gpu import gpu
+
+    B, Hq, Hkv, Dh, bs, steps = 64, 32, 8, 128, 16, 128
+    r = np.random.default_rng(0)
+    lens0 = np.clip(np.exp(r.normal(np.log(1500), 0.8, B)), 16, 8192).astype(np.int64)
+    max_seq = 8192 + steps
+    max_blocks = -(-max_seq // bs)
+    need = -(-(lens0 + steps) // bs)
+    n_blocks = int(need.sum())
+    cache = gpu.kv_cache_create(ctx, gpu.KVCacheConfig(B, max_seq, 1, Hq, Dh, n_kv_heads=Hkv,
+                                                       dtype=torch.bfloat16, block_size=bs,
+                                                       n_blocks=n_blocks))
+    perm = r.permutation(n_blocks).astype(np.int32)
+    table = np.zeros((B, max_blocks), np.int32)
+    o = 0
+    for b in range(B):
+        table[b, :need[b]] = perm[o:o + need[b]]
+        o += need[b]
+    gpu.kv_cache_set_block_table(cache, torch.from_numpy(table))
+    layer = cache.layers[0]
+    g = torch.Generator(device=ctx.device).manual_seed(0)
+    for buf in (layer.k_cache.buffer, layer.v_cache.buffer):
+        for i in range(0, buf.shape[0], 1 << 16):
+            chunk = buf[i:i + (1 << 16)]
+            chunk.copy_(torch.randn(chunk.shape, generator=g, device=ctx.device))
+    wall, active, roof, _ = _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, 2,
+                                                0, "c5")
+    return _record(
+        "decode tokens/sec", active / wall, "tokens/s", steps, args.warmup, wall / steps * 1e3,
+        "bf16",
+        {"workload": "C5 batched ragged GQA decode: 64 seqs, 32 q heads over 8 kv heads, "
+                     "head_dim 128, bf16 paged cache (16-token pages, random page table), "
+                     "lognormal lengths median 1500 sigma 0.8 in [16, 8192], 128 steps of "
+                     "append + decode attention",
+         "batch": B, "mean_len": float(lens0.mean()), "pages": n_blocks},
+        roof, None)
+
+
+def run_c2(args, ctx):
+    """fp32 cache [B=8, H=8, T=2048, D=64], start lengths
+    U[1, 2047], 256 steps of append at pos_b + attention over [0, pos_b];
+    sequences that reach 2048 retire (no append, not counted)."""
+    import numpy as np
+    import torch
+
+    from simple_llm_amd.gpu import gpu
+
+    B, H, T, Dh, steps = 8, 8, 2048, 64, 256
+    lens0 = np.random.default_rng(0).integers(1, 2048, B).astype(np.int64)
+    cache = gpu.kv_cache_create(ctx, gpu.KVCacheConfig(B, T, 1, H, Dh))
+    layer = cache.layers[0]
+    g = torch.Generator(device=ctx.device).manual_seed(0)
+    layer.k_cache.buffer.copy_(torch.randn(layer.k_cache.buffer.shape, generator=g,
+                                           device=ctx.device))
+    layer.v_cache.buffer.copy_(torch.randn(layer.v_cache.buffer.shape, generator=g,
+                                           device=ctx.device))
+    wall, active, roof, (q_all, k_all, v_all) = _attention_workload(
+        args, ctx, cache, lens0, steps, H, H, Dh, 4, 0, "c2")
+    roof["note"] = "the 67 MB cache fits in the 256 MB Infinity Cache: not an HBM figure"
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import c_oracle
+
+        kc = layer.k_cache.buffer.cpu().numpy().reshape(B, T, H, Dh).copy()
+        vc = layer.v_cache.buffer.cpu().numpy().reshape(B, T, H, Dh).copy()
+        qs, ks, vs = q_all.cpu().numpy(), k_all.cpu().numpy(), v_all.cpu().numpy()
+        lens = lens0.astype(np.int32).copy()
+        n, tok, t0 = 0, 0, time.perf_counter()
+        while n < steps and time.perf_counter() - t0 < args.cpu_seconds:
+            for b in range(B):
+                if lens[b] < T:
+                    kc[b, lens[b]], vc[b, lens[b]] = ks[n, b], vs[n, b]
+                    lens[b] += 1
+                    tok += 1
+            c_oracle.decode_attn(qs[n], kc, vc, lens, cache_bf16=False)
+            n += 1
+        dt = time.perf_counter() - t0
+        cpu = {"value": tok / dt, "unit": "tokens/s", "cores": c_oracle.threads(),
+               "kind": "port", "sample": f"first {n} of the {steps} C2 steps, "
+                                         f"oracle/c/kv_attn_ref.c with OpenMP, {dt:.1f} s"}
+    return _record(
+        "decode tokens/sec", active / wall, "tokens/s", steps, args.warmup, wall / steps * 1e3,
+        "fp32",
+        {"workload": "C2 KV microbench fp32: cache [8, 8, 2048, 64], start lengths U[1,2047], "
+                     "256 steps of append + attention, full sequences retire", "batch": B},
+        roof, cpu)
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -198,6 +506,14 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.workload != "c4":
+        from simple_llm_amd.gpu import gpu
+
+        ctx = gpu.context_create()
+        ctx.config.decode_chunk_tokens = args.chunk_tokens
+        rec = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c5": run_c5}[args.workload](args, ctx)
+        print(json.dumps(rec), flush=True)
         return
     if FILL + args.steps > T_CAP or args.steps < 1 or args.warmup < 0:
         print(f"bench.py: --steps must lie in [1, {T_CAP - FILL}]", file=sys.stderr)

@@ -293,6 +293,13 @@ class Generator:
         self.use_graph = use_graph
         self.graph = None
 
+    def reset(self) -> None:
+        """Rewind to before the first step (empty cache, no tokens), keeping
+        the captured graph, so run() can be repeated."""
+        self.cache.current_len = 0
+        self.seq.zero_()
+        self.bufs.argmax.zero_()
+
     def _one_step(self):
         L = _lib.lib()
         m, c, bf = self.model, self.cache, self.bufs

@@ -29,9 +29,10 @@ How each function is pinned (tests/test_model_oracle.py):
                         with is_causal) on the same weights; causality
   decode_step           equals forward's rows (a different algorithm: the
                         per-token cached recurrence the GPU path uses)
-  reference_generate    the left-padding rule of generate.py:31-36 on a
-                        case where the window is not full, and equality with
-                        greedy_generate once prompt + output fit the window
+  reference_generate    the left-padding rule of generate.py:31-36 observed
+                        through a spy forward, while the window is not full
+                        and once the sequence is longer than the window
+  torch_forward_fp32    equals forward to float32 accuracy
 """
 from __future__ import annotations
 
@@ -195,3 +196,44 @@ def init_params(vocab: int, dim: int, n_layers: int, context: int, mlp: int | No
     return {"embedding": w(vocab, dim),
             "pos_encoding": positional_encoding(context, dim).astype(np.float32),
             "layers": layers}
+
+
+def torch_forward_fp32(params: dict, tokens, n_heads: int):
+    """The same forward in float32 torch on the CPU (jax_backend.py:143-148
+    with its float32 dtypes): the timed CPU restatement of the reference's
+    JAX CPU path in bench.py's cpu_baseline legs. Returns a float32 tensor
+    [B, T, V]. Weights are converted on each call's first use and cached."""
+    import torch
+
+    cache = params.setdefault("_torch_fp32", {})
+    if not cache:
+        cache["E"] = torch.from_numpy(np.asarray(params["embedding"], np.float32))
+        cache["PE"] = torch.from_numpy(np.asarray(params["pos_encoding"], np.float32))
+        cache["L"] = [{k: torch.from_numpy(np.asarray(lp[k], np.float32)) for k in LAYER_FIELDS}
+                      for lp in params["layers"]]
+    E, PE = cache["E"], cache["PE"]
+    ids = torch.as_tensor(np.asarray(tokens), dtype=torch.long)
+    B, T = ids.shape
+    d = E.shape[1]
+    D = d // n_heads
+    x = E[ids] + PE[:T]
+    mask = torch.triu(torch.ones(T, T), diagonal=1) * -1e9
+
+    def ln(y, g, b):
+        mu = y.mean(-1, keepdim=True)
+        var = ((y - mu) ** 2).mean(-1, keepdim=True)
+        return (y - mu) / torch.sqrt(var + 1e-5) * g + b
+
+    for lp in cache["L"]:
+        h = ln(x, lp["ln_gamma1"], lp["ln_beta1"])
+        q = (h @ lp["attn_wq"]).reshape(B, T, n_heads, D).transpose(1, 2)
+        k = (h @ lp["attn_wk"]).reshape(B, T, n_heads, D).transpose(1, 2)
+        v = (h @ lp["attn_wv"]).reshape(B, T, n_heads, D).transpose(1, 2)
+        s = q @ k.transpose(-1, -2) / (D ** 0.5) + mask
+        a = torch.softmax(s, -1) @ v
+        x = x + a.transpose(1, 2).reshape(B, T, d) @ lp["attn_wo"]
+        h = ln(x, lp["ln_gamma2"], lp["ln_beta2"])
+        f = h @ lp["ff_w1"] + lp["ff_b1"]
+        f = 0.5 * f * (1 + torch.tanh(0.7978845608028654 * (f + 0.044715 * f ** 3)))
+        x = x + f @ lp["ff_w2"] + lp["ff_b2"]
+    return x @ E.T

@@ -159,3 +159,14 @@ def test_reference_generate_left_pads_window():
     out2 = mo.reference_generate(p, list(range(1, 11)), 2, 4, context_size=8, forward_fn=spy)
     assert seen[-2] == list(range(3, 11))
     assert out2[:10] == list(range(1, 11))
+
+
+def test_torch_fp32_forward_matches_oracle():
+    """The CPU-baseline forward (float32 torch) agrees with the float64
+    oracle to float32 accuracy."""
+    p = small_params(seed=11, std=0.1)
+    toks = rng.integers(0, 37, (2, 24))
+    got = mo.torch_forward_fp32(p, toks, 4).numpy()
+    want = mo.forward(p, toks, 4)
+    err = np.linalg.norm(got - want, axis=-1) / np.linalg.norm(want, axis=-1)
+    assert err.max() < 1e-4
