@@ -181,20 +181,29 @@ int skv_embed(float* x, const int32_t* ids, const int32_t* pos, const float* emb
 int skv_layernorm(float* y, const float* x, const float* gamma, const float* beta, int M, int d,
                   float eps, skv_stream_t stream);
 
-/* y = act(x . w_t^T + bias) + residual, x [M, K], w_t [N, K] (the
+/* y = act(LN(x) . w_t^T + bias) + residual, x [M, K], w_t [N, K] (the
  * transpose of the reference's [K, N] weight), y [M, N]. activation 0 =
  * none, 1 = GELU, tanh form (jax.nn.gelu's default, jax_backend.py:127).
+ * LN is the row LayerNorm with ln_gamma, ln_beta, ln_eps (both NULL: x as
+ * is), folded into the reads of x (jax_backend.py:135, 138 put a LayerNorm
+ * in front of the attention and MLP projections).
  * bias and residual may be NULL; residual may equal y, x may not.
  * split_cols > 0 writes column n to segment n / split_cols of a
  * [N / split_cols][M][split_cols] output (q, k, v of a fused projection as
- * three contiguous [M, d] blocks). K must be a multiple of 4. */
+ * three contiguous [M, d] blocks). K must be a multiple of 4. Sums run in a
+ * fixed order, so results are reproducible run to run. */
 int skv_linear(float* y, const float* x, const float* w_t, const float* bias,
-               const float* residual, int M, int N, int K, int activation, int split_cols,
-               skv_stream_t stream);
+               const float* residual, const float* ln_gamma, const float* ln_beta, float ln_eps,
+               int M, int N, int K, int activation, int split_cols, skv_stream_t stream);
+
+/* Workspace of skv_argmax (per-slice candidates and counters); zero it
+ * once before its first use; not shared by concurrent calls. */
+size_t skv_argmax_workspace_bytes(int M, int N);
 
 /* out[m] = index of the largest x[m, :], the first on ties
  * (jnp.argmax, jax_backend.py:469). */
-int skv_argmax(int32_t* out, const float* x, int M, int N, skv_stream_t stream);
+int skv_argmax(int32_t* out, const float* x, int M, int N, void* ws, size_t ws_bytes,
+               skv_stream_t stream);
 
 /* Next input token of each sequence (generate.py:29-69 with a cache):
  * ids[b] = prompt[b, pos[b]] while pos[b] < prompt_len[b], else

@@ -397,7 +397,7 @@ extern "C" int skv_decode_plan(int B, int H_kv, int max_len, long long total_len
     // fastest: 1 or 2 workgroups on every CU stream at the same rate, while
     // grids that leave some CUs one workgroup more than others (e.g. 336
     // workgroups) or that use more, shorter chunks were 5-15% slower. Chunks
-    // are 64 to 8192 tokens, sized from the filled tokens of the whole batch
+    // are 32 to 8192 tokens, sized from the filled tokens of the whole batch
     // so a ragged batch gets as many workgroups as a uniform one of the same
     // total.
     const long long tot = total_len > 0 ? total_len : (long long)B * max_len;
@@ -405,7 +405,7 @@ extern "C" int skv_decode_plan(int B, int H_kv, int max_len, long long total_len
     const long long target = 2 * kNumCUs;
     long long per = (tot * groups + target - 1) / target;
     per = (per + 31) / 32 * 32;
-    if (per < 64) per = 64;
+    if (per < 32) per = 32;
     if (per > 8192) per = 8192;
     chunk = (int)per;
   }

@@ -11,9 +11,10 @@ The model is the reference's JAX model (pre-LN blocks, bias-free attention
 projections, tanh GELU MLP, tied logits, positional table of
 jax_backend.py:25-33). One decode step runs every sequence's next token
 through all layers as HIP kernels of libskv.so: embedding + position,
-LayerNorm, fused q/k/v projection, the cache append (skv_append), decode
-attention (skv_decode_attn), output projection with residual, MLP with
-GELU and residual, tied logits and argmax. PyTorch only owns the memory.
+fused q/k/v projection (the LayerNorm before it folded into its reads), the
+cache append (skv_append), decode attention (skv_decode_attn), output
+projection with residual, MLP (LayerNorm folded in, GELU, residual), tied
+logits and argmax. PyTorch only owns the memory.
 
 Differences from the reference's generate_text, both documented choices:
   * tokens attend their cached prefix at their absolute positions; the
@@ -99,6 +100,11 @@ class _Buffers:
         self.ff = torch.zeros((B, mlp), device=dev)
         self.logits = torch.zeros((B, vocab), device=dev)
         self.argmax = torch.zeros(B, dtype=torch.int32, device=dev)
+        # split-argmax workspace: zero-filled once, its arrival counters
+        # return to zero after every call
+        L = _lib.lib()
+        arg = L.skv_argmax_workspace_bytes(B, vocab)
+        self.arg_ws = torch.zeros(max(arg, 4), dtype=torch.uint8, device=dev)
 
 
 class TransformerModel:
@@ -210,25 +216,25 @@ class TransformerModel:
                         tm.vocab_size, self.pe.shape[0], s), "skv_embed")
         for lw, layer in zip(self.layers, cache.layers):
             kc, vc = layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr()
-            chk(L.skv_layernorm(h, x, lw["g1"].data_ptr(), lw["be1"].data_ptr(), B, d, 1e-5, s),
-                "skv_layernorm")
-            chk(L.skv_linear(qkv, h, lw["wqkv_t"].data_ptr(), None, None, B, 3 * d, d, 0, d, s),
-                "skv_linear")
+            # q, k, v = LN1(x) . [Wq Wk Wv] (LayerNorm folded into the projection)
+            chk(L.skv_linear(qkv, x, lw["wqkv_t"].data_ptr(), None, None, lw["g1"].data_ptr(),
+                             lw["be1"].data_ptr(), 1e-5, B, 3 * d, d, 0, d, s), "skv_linear")
             chk(L.skv_append(kc, vc, k_ptr, v_ptr, layer.lens.data_ptr(), B, H, D, T, cdt,
                              _lib.F32, s), "skv_append")
             chk(L.skv_decode_attn(attn, q_ptr, kc, vc, layer.lens.data_ptr(), B, H, H, D, T, scale,
                                   chunk, n_chunks, ws.data_ptr(), ws.numel(), cdt, _lib.F32,
                                   _lib.F32, s), "skv_decode_attn")
-            chk(L.skv_linear(x, attn, lw["wo_t"].data_ptr(), None, x, B, d, d, 0, 0, s),
-                "skv_linear")
-            chk(L.skv_layernorm(h, x, lw["g2"].data_ptr(), lw["be2"].data_ptr(), B, d, 1e-5, s),
-                "skv_layernorm")
-            chk(L.skv_linear(ff, h, lw["w1_t"].data_ptr(), lw["b1"].data_ptr(), None, B,
-                             self.mlp_dim, d, 1, 0, s), "skv_linear")
-            chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, B, d,
-                             self.mlp_dim, 0, 0, s), "skv_linear")
-        chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, B,
-                         tm.vocab_size, d, 0, 0, s), "skv_linear")
+            # x += attn . Wo
+            chk(L.skv_linear(x, attn, lw["wo_t"].data_ptr(), None, x, None, None, 0.0, B, d, d, 0,
+                             0, s), "skv_linear")
+            # ff = gelu(LN2(x) . W1 + b1); x += ff . W2 + b2
+            chk(L.skv_linear(ff, x, lw["w1_t"].data_ptr(), lw["b1"].data_ptr(), None,
+                             lw["g2"].data_ptr(), lw["be2"].data_ptr(), 1e-5, B, self.mlp_dim, d,
+                             1, 0, s), "skv_linear")
+            chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, None, None, 0.0,
+                             B, d, self.mlp_dim, 0, 0, s), "skv_linear")
+        chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, None, None,
+                         0.0, B, tm.vocab_size, d, 0, 0, s), "skv_linear")
 
     # -- many steps ----------------------------------------------------------
 
@@ -310,7 +316,8 @@ class Generator:
                                      self.seq.shape[1], s), "skv_next_tokens")
         m._launch_step(c, bf)
         _lib.check(L.skv_argmax(bf.argmax.data_ptr(), bf.logits.data_ptr(), self.B,
-                                m.tm_params.vocab_size, s), "skv_argmax")
+                                m.tm_params.vocab_size, bf.arg_ws.data_ptr(), bf.arg_ws.numel(),
+                                s), "skv_argmax")
 
     def run(self) -> List[List[int]]:
         """Run all steps; returns every sequence's tokens (prompt + output)."""

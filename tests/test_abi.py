@@ -36,7 +36,7 @@ def _plan(B, Hkv, max_len, hint=0, total=0):
 def test_decode_plan_covers_every_length(B, Hkv, L):
     rc, chunk, n = _plan(B, Hkv, L)
     assert rc == 0
-    assert chunk % 32 == 0 and 64 <= chunk <= 8192
+    assert chunk % 32 == 0 and 32 <= chunk <= 8192
     assert n * chunk >= L > (n - 1) * chunk
 
 

@@ -46,7 +46,7 @@ def lib():
 @pytest.mark.parametrize("M,N,K", [(1, 256, 256), (5, 100, 260), (16, 768, 768),
                                    (17, 3072, 768), (64, 48, 3072), (100, 1024, 64),
                                    (3, 50304, 768)])
-@pytest.mark.parametrize("epi", ["plain", "bias_gelu", "bias_res", "split"])
+@pytest.mark.parametrize("epi", ["plain", "bias_gelu", "bias_res", "split", "ln_gelu"])
 def test_linear_matches_numpy(gpu_ctx, M, N, K, epi):
     banner(f"linear M={M} N={N} K={K} {epi}")
     if epi == "split" and N % 3:
@@ -73,13 +73,29 @@ def test_linear_matches_numpy(gpu_ctx, M, N, K, epi):
         residual = y
     if epi == "split":
         split = N // 3
+    g = ln_g = ln_b = None
+    if epi == "ln_gelu":  # LayerNorm folded into the reads of x, then bias + GELU
+        g = (1 + 0.1 * r.standard_normal(K)).astype(np.float32)
+        beta = (0.1 * r.standard_normal(K)).astype(np.float32)
+        want = mo.gelu_tanh(mo.layer_norm(x, g, beta) @ w.astype(np.float64) + b)
+        bias, act, ln_g, ln_b = dev(b), 1, dev(g), dev(beta)
     xd, wtd = dev(x), dev(np.ascontiguousarray(w.T))
-    rc = _lib.lib().skv_linear(y.data_ptr(), xd.data_ptr(), wtd.data_ptr(),
-                               bias.data_ptr() if bias is not None else None,
-                               residual.data_ptr() if residual is not None else None,
-                               M, N, K, act or 0, split, _lib.stream_handle())
-    _lib.check(rc, "skv_linear")
-    got = y.cpu().numpy()
+    L = _lib.lib()
+    res0 = y.clone()
+    for rep in range(2):  # a second call gives the same bits
+        if rep:
+            y.copy_(res0)
+        rc = L.skv_linear(y.data_ptr(), xd.data_ptr(), wtd.data_ptr(),
+                          bias.data_ptr() if bias is not None else None,
+                          residual.data_ptr() if residual is not None else None,
+                          ln_g.data_ptr() if ln_g is not None else None,
+                          ln_b.data_ptr() if ln_b is not None else None, 1e-5,
+                          M, N, K, act or 0, split, _lib.stream_handle())
+        _lib.check(rc, "skv_linear")
+        got_rep = y.cpu().numpy()
+        if rep:
+            np.testing.assert_array_equal(got_rep, got)  # bitwise reproducible
+        got = got_rep
     if split:  # [3][M][N/3] -> [M, N]
         got = got.reshape(3, M, split).transpose(1, 0, 2).reshape(M, N)
     assert rel_rows(got, want) < FP32_TOL
@@ -127,9 +143,19 @@ def test_argmax_first_index_on_ties(gpu_ctx):
     x[4, 12345] = np.inf
     out = torch.empty(6, dtype=torch.int32, device="cuda")
     xd = dev(x)
-    _lib.check(_lib.lib().skv_argmax(out.data_ptr(), xd.data_ptr(), 6, 50304,
-                                     _lib.stream_handle()), "argmax")
-    np.testing.assert_array_equal(out.cpu().numpy(), np.argmax(x, axis=1))
+    L = _lib.lib()
+    ws = torch.zeros(L.skv_argmax_workspace_bytes(6, 50304), dtype=torch.uint8, device="cuda")
+    for _ in range(2):
+        _lib.check(L.skv_argmax(out.data_ptr(), xd.data_ptr(), 6, 50304, ws.data_ptr(),
+                                ws.numel(), _lib.stream_handle()), "argmax")
+        np.testing.assert_array_equal(out.cpu().numpy(), np.argmax(x, axis=1))
+    assert not ws[:6 * 4].any()  # counters reset
+    # a row narrower than one slice
+    small = torch.zeros(3, dtype=torch.int32, device="cuda")
+    xs = dev(x[:3, :100])
+    _lib.check(L.skv_argmax(small.data_ptr(), xs.data_ptr(), 3, 100, ws.data_ptr(), ws.numel(),
+                            _lib.stream_handle()), "argmax")
+    np.testing.assert_array_equal(small.cpu().numpy(), np.argmax(x[:3, :100], axis=1))
 
 
 def test_next_tokens(gpu_ctx):
