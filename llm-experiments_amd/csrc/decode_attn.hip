@@ -95,8 +95,18 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const size_t qoff = ((size_t)b * a.Hq + hk * G + h) * D + e0;
+    if constexpr (EPL == 8) {
+      load8_f32(a.q, qoff, a.q_dt, q[h]);
+    } else {  // EPL == 4 (D = 64)
+      float v[8];
+      // the lane's 4 elements sit in an 8-element group, first or second half
+      load8_f32(a.q, qoff & ~(size_t)7, a.q_dt, v);
+      const int off = (int)(qoff & 7);
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) q[h][e] = load_elem(a.q, qoff + e, a.q_dt) * a.qscale;
+      for (int e = 0; e < EPL; ++e) q[h][e] = off ? v[4 + e] : v[e];
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) q[h][e] *= a.qscale;
   }
 
   float m[G], l[G], acc[G][EPL];

@@ -145,13 +145,13 @@ __global__ __launch_bounds__(256, 1) void k_prefill_mfma(PrefillArgs a) {
     const bool ok = r < R;
     const int i = r / G, h = hk * G + r % G;
     const size_t qoff = (((size_t)b * a.C + i) * a.Hq + h) * D;
+    const size_t qsafe = ok ? qoff : 0;  // rows past the chunk read row 0 and are zeroed
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
+      float v[8];
+      load8_f32(a.q, qsafe + kb * 16 + g * 8, a.q_dt, v);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float x = ok ? load_elem(a.q, qoff + kb * 16 + g * 8 + j, a.q_dt) : 0.f;
-        qf[qb][kb][j] = (__bf16)x;
-      }
+      for (int j = 0; j < 8; ++j) qf[qb][kb][j] = (__bf16)(ok ? v[j] : 0.f);
     }
   }
 

@@ -96,6 +96,27 @@ struct Frag<uint16_t, EPL> {
   }
 };
 
+// Eight consecutive elements of a runtime-dtype row, as fp32, with one branch
+// and vector loads (p + i must be 16-byte aligned for fp32, 8 elements
+// aligned for bf16). A per-element load behind a dtype branch makes the
+// compiler wait for each load on its own.
+__device__ __forceinline__ void load8_f32(const void* p, size_t i, int dt, float* out) {
+  if (dt == SKV_BF16) {
+    const uint4 x = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      out[2 * j] = bf16w_lo(w[j]);
+      out[2 * j + 1] = bf16w_hi(w[j]);
+    }
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i + 4);
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+  }
+}
+
 // Element loads/stores with runtime dtype (used off the hot loops).
 __device__ __forceinline__ float load_elem(const void* p, size_t i, int dt) {
   return dt == SKV_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i])
