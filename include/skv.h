@@ -97,14 +97,19 @@ int skv_advance(int32_t* lens, const int32_t* n_new, int n_const, int B, int T_c
  * Split-K sizing for decode attention (host-only, no device work).
  * Given the longest sequence the call may see (max_len) and the filled
  * tokens of the whole batch (total_len; <= 0 means B * max_len), picks
- * chunk_tokens (tokens per workgroup) for about 1024 workgroups per call and
- * n_chunks_max = ceil(max_len / chunk_tokens).
+ * chunk_tokens (tokens of the flat token stream -- every sequence's filled
+ * tokens end to end -- per workgroup) for about 512 busy workgroups per call,
+ * and n_chunks_max = ceil(max_len / chunk_tokens) + 1 partial slots per
+ * sequence: B * (n_chunks_max - 1) workgroups cover B * max_len tokens, and
+ * the spare slot holds the piece of a sequence that starts inside a
+ * workgroup's range.
  * chunk_hint > 0 forces that chunk size (rounded up to a multiple of 16).
  */
 int skv_decode_plan(int B, int H_kv, int max_len, long long total_len, int chunk_hint,
                     int* chunk_tokens /* host */, int* n_chunks_max /* host */);
 
-/* Bytes of workspace skv_decode_attn needs for this plan. */
+/* Bytes of workspace skv_decode_attn needs for this plan: fp32 partials
+ * (o[D], m, l) per (query head, slot), then B + 1 int64 prefix sums. */
 size_t skv_decode_workspace_bytes(int B, int H_q, int D, int n_chunks_max);
 
 /*
@@ -116,9 +121,11 @@ size_t skv_decode_workspace_bytes(int B, int H_q, int D, int n_chunks_max);
  *                  . V[b, 0:lens[b], h/G, :],           G = H_q / H_kv.
  * No length cap (the reference caps lens at 256). lens[b] == 0 gives zeros.
  * q, out: [B, H_q, D] of q_dt / out_dt. D in {64, 128}; G in {1, 2, 4, 8}.
- * Split-K: pass 1 writes per-chunk (max, sum, unnormalised o) partials into
- * ws; pass 2 merges them. Requires lens[b] <= n_chunks_max * chunk_tokens
- * (violations produce NaN outputs, never out-of-bounds reads).
+ * Split-K: pass 1 writes per-piece (max, sum, unnormalised o) partials into
+ * ws; pass 2 merges them. n_chunks_max >= 2. A sequence whose tokens lie
+ * past the first B * (n_chunks_max - 1) * chunk_tokens tokens of the flat
+ * stream (possible only when some lens[b] > max_len of the plan) gets NaN
+ * outputs, never out-of-bounds reads.
  */
 int skv_decode_attn(void* out, const void* q, const void* k_cache,
                     const void* v_cache, const int32_t* lens, int B, int H_q,

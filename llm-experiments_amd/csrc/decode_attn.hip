@@ -7,9 +7,12 @@
 // o = sum_t p_t V[t]. One workgroup per (b, h) and len <= 256 there.
 //
 // Design (HBM-bound GEMV, no MFMA):
-//  * Pass 1, grid (chunk, kv-head group, seq). A workgroup owns a token range
-//    [c*chunk, (c+1)*chunk) of one sequence for a group of HW kv heads, and
-//    is made of 16-lane DPP rows: row r serves kv head r % HW of the group
+//  * Pass 1, grid (workgroup, kv-head group). The sequences' filled tokens,
+//    laid end to end, form one flat stream; workgroup w owns its tokens
+//    [w*chunk, (w+1)*chunk), cut into pieces at sequence boundaries, for a
+//    group of HW kv heads. Equal ranges keep a ragged batch as evenly spread
+//    over the CUs as a uniform one. A workgroup is made of 16-lane DPP rows:
+//    row r serves kv head r % HW of the group
 //    and token substream r / HW (S substreams, HW*S <= 16). Lane i of a row
 //    owns elements [i*D/16, (i+1)*D/16) of each K and V row it reads, as
 //    16-byte (or 8-byte) vector loads. Because the cache is [B, T, H_kv, D],
@@ -24,11 +27,12 @@
 //    traffic. Scores are in log2 units (log2(e) is folded into the query
 //    scale) so each exp is a single v_exp_f32. GQA: a row serves all
 //    G = H_q/H_kv query heads of its kv head, so each K/V byte is read once.
-//  * Each (seq, query head, chunk) gets one partial (m, l, o[D]) in the
+//  * Each (piece, query head) gets one partial (m, l, o[D]) in the
 //    workspace. With S > 1 the S substreams of a head merge through LDS
 //    first.
-//  * Pass 2, grid (q_head, seq), 256 threads: log-sum-exp merge of the chunk
-//    partials, 8 chunk streams in parallel, then across the streams in LDS.
+//  * Pass 2, grid (q_head, seq), 256 threads: log-sum-exp merge of the
+//    sequence's piece partials, 8 streams in parallel, then across the
+//    streams in LDS.
 // No atomics anywhere: results are bitwise reproducible run to run.
 #include "skv_common.h"
 
@@ -46,17 +50,25 @@ struct DecodeArgs {
   const int32_t* block_table;
   int max_blocks;
   int bs_shift;
-  int Hq, Hkv, T_cap;
+  int B, Hq, Hkv, T_cap;
   int cap;       // tokens a sequence can hold: T_cap, or max_blocks * block_size
   float qscale;  // softmax scale * log2(e)
-  int chunk;
-  int n_chunks_max;
+  int chunk;     // tokens of the flat token stream per pass-1 workgroup
+  int n_wg;      // pass-1 workgroups along the token stream
+  int n_slots;   // partial slots per query head (>= n_wg + B - 1)
   int q_dt;
   int hw;        // kv heads per workgroup
   int S;         // token substreams per kv head
-  float* ws_o;   // [B][Hq][n_chunks_max][D]
-  float* ws_ml;  // [B][Hq][n_chunks_max][2]  (m in log2 units, l)
+  long long* cum;  // [B + 1] exclusive prefix sums of the clamped lengths
+  float* ws_o;   // [Hq][n_slots][D]
+  float* ws_ml;  // [Hq][n_slots][2]  (m in log2 units, l)
 };
+
+// Lengths outside [0, cap] are clamped so no row outside the cache (or block
+// table entry outside the table) is ever addressed.
+__device__ __forceinline__ int clamped_len(const DecodeArgs& a, int b) {
+  return min(max(a.lens[b], 0), a.cap);
+}
 
 template <typename TC, int D, bool PAGED>
 __device__ __forceinline__ const TC* row_ptr(const TC* base, const DecodeArgs& a, int b, int t,
@@ -71,17 +83,62 @@ __device__ __forceinline__ const TC* row_ptr(const TC* base, const DecodeArgs& a
   return base + (row * a.Hkv + hk) * D;
 }
 
-template <typename TC, int D, int G, int TPG, bool PAGED>
-__global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
-  constexpr int EPL = D / 16;
-  const int c = blockIdx.x, hg = blockIdx.y, b = blockIdx.z;
-  // Lengths beyond the capacity are clamped so no row outside the cache (or
-  // block table entry outside the table) is ever addressed.
-  const int len = min(a.lens[b], a.cap);
-  const int start = c * a.chunk;
-  if (start >= len) return;  // uniform over the workgroup
-  const int end = min(start + a.chunk, len);
+// Position `first` of the flat token stream (the sequences' filled tokens
+// laid end to end) -> (sequence, offset in it), or sequence -1 past the end.
+// Rounds of blockDim sequences: an inclusive scan of the clamped lengths
+// within each wavefront (shuffles, no barrier), then across the wavefronts
+// through LDS. The workgroup with write_cum also stores the exclusive prefix
+// sums (and the total at [B]) for the merge pass.
+__device__ void locate(const DecodeArgs& a, long long first, bool write_cum, int* b_out,
+                       int* off_out) {
+  __shared__ long long s_wave[4];  // wavefront totals of one round (blockDim <= 256)
+  __shared__ int s_b, s_off;
+  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wv = tid >> 6;
+  const int nwaves = (nt + 63) >> 6;
+  if (tid == 0) s_b = -1;
+  long long carry = 0;
+  for (int base = 0; base < a.B; base += nt) {
+    const int bb = base + tid;
+    const long long L = bb < a.B ? clamped_len(a, bb) : 0;
+    long long x = L;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {  // lanes below are active, also in a partial wavefront
+      const long long y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63 || tid == nt - 1) s_wave[wv] = x;
+    __syncthreads();
+    long long incl = carry + x, round_total = 0;
+    for (int w2 = 0; w2 < nwaves; ++w2) {
+      const long long t = s_wave[w2];
+      if (w2 < wv) incl += t;
+      round_total += t;
+    }
+    const long long excl = incl - L;
+    if (bb < a.B) {
+      if (write_cum) a.cum[bb] = excl;
+      if (L > 0 && excl <= first && first < incl) {  // exactly one thread
+        s_b = bb;
+        s_off = (int)(first - excl);
+      }
+    }
+    carry += round_total;
+    __syncthreads();
+    if (!write_cum && s_b >= 0) break;  // uniform: read after the barrier
+  }
+  if (write_cum && tid == 0) a.cum[a.B] = carry;
+  // Uniform values from LDS: readfirstlane keeps them (and the addresses
+  // derived from them) in scalar registers.
+  *b_out = __builtin_amdgcn_readfirstlane(s_b);
+  *off_out = __builtin_amdgcn_readfirstlane(s_off);
+}
 
+// Tokens [start, end) of sequence b for the workgroup's kv heads -> one
+// partial per query head at `slot`.
+template <typename TC, int D, int G, int TPG, bool PAGED>
+__device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b, int start,
+                                             int end, int slot) {
+  constexpr int EPL = D / 16;
   const int tid = threadIdx.x;
   const int rid = tid >> 4;  // DPP row
   const int li = tid & 15;   // lane within the row
@@ -95,16 +152,10 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const size_t qoff = ((size_t)b * a.Hq + hk * G + h) * D + e0;
-    if constexpr (EPL == 8) {
+    if constexpr (EPL == 8)
       load8_f32(a.q, qoff, a.q_dt, q[h]);
-    } else {  // EPL == 4 (D = 64)
-      float v[8];
-      // the lane's 4 elements sit in an 8-element group, first or second half
-      load8_f32(a.q, qoff & ~(size_t)7, a.q_dt, v);
-      const int off = (int)(qoff & 7);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) q[h][e] = off ? v[4 + e] : v[e];
-    }
+    else  // D = 64
+      load4_f32(a.q, qoff, a.q_dt, q[h]);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) q[h][e] *= a.qscale;
   }
@@ -163,13 +214,13 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
     }
   }
 
-  const size_t pbase = ((size_t)b * a.Hq + hk * G) * a.n_chunks_max + c;
   if (S == 1) {
-    // One row per head: it holds the whole chunk's partial. A row that saw no
-    // token (only possible if chunk < TPG) keeps m = -inf, l = 0, o = 0.
+    // One row per head: it holds the whole piece's partial. A row that saw no
+    // token (only possible if the piece is shorter than TPG) keeps m = -inf,
+    // l = 0, o = 0.
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const size_t pidx = pbase + (size_t)h * a.n_chunks_max;
+      const size_t pidx = (size_t)(hk * G + h) * a.n_slots + slot;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) a.ws_o[pidx * D + e0 + e] = acc[h][e];
       if (li == 0) {
@@ -205,8 +256,7 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
         L = fmaf(w, sm_ml[r][1], L);
         O = fmaf(w, sm_o[r][d], O);
       }
-      const size_t pidx =
-          ((size_t)b * a.Hq + (hg * a.hw + hh) * G + h) * a.n_chunks_max + c;
+      const size_t pidx = (size_t)((hg * a.hw + hh) * G + h) * a.n_slots + slot;
       a.ws_o[pidx * D + d] = O;
       if (d == 0) {
         a.ws_ml[pidx * 2 + 0] = M;
@@ -217,36 +267,66 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
   }
 }
 
-// Pass 2: grid (Hq, B), 256 threads = 8 chunk streams x 32 lanes; lane i of a
-// stream owns elements [i*D/32, (i+1)*D/32). Each stream merges chunks
-// n = stream, stream + 8, ... online; the 8 streams merge in LDS.
+// Pass 1: grid (n_wg, kv-head groups). Workgroup w owns the flat token
+// range [w*chunk, (w+1)*chunk) of the sequences laid end to end, so every
+// workgroup but the last has the same number of tokens however ragged the
+// lengths are, and the busy workgroups are the first ones dispatched. The
+// range is cut at sequence boundaries into pieces; the piece of sequence b
+// in workgroup w gets partial slot w + b (unique: along the stream, each
+// boundary of either kind moves w or b on by at least one).
+template <typename TC, int D, int G, int TPG, bool PAGED>
+__global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
+  const int w = blockIdx.x, hg = blockIdx.y;
+  int b, off;
+  locate(a, (long long)w * a.chunk, w == 0 && hg == 0, &b, &off);
+  if (b < 0) return;  // uniform over the workgroup
+  int budget = a.chunk;
+  while (true) {
+    const int n = min(clamped_len(a, b) - off, budget);
+    decode_piece<TC, D, G, TPG, PAGED>(a, hg, b, off, off + n, w + b);
+    budget -= n;
+    if (budget == 0) break;
+    do {
+      ++b;
+    } while (b < a.B && clamped_len(a, b) == 0);
+    if (b >= a.B) break;
+    off = 0;
+  }
+}
+
+// Pass 2: grid (Hq, B), 256 threads = 8 piece streams x 32 lanes; lane i of a
+// stream owns elements [i*D/32, (i+1)*D/32). Sequence b's pieces are the
+// slots w + b for the workgroups w its token range [cum[b], cum[b+1])
+// overlaps. Each stream merges pieces n = stream, stream + 8, ... online;
+// the 8 streams merge in LDS.
 template <int D>
 __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, int out_dt,
-                                                      const int32_t* __restrict__ lens,
+                                                      const long long* __restrict__ cum,
                                                       const float* __restrict__ ws_o,
                                                       const float* __restrict__ ws_ml, int Hq,
-                                                      int chunk, int n_chunks_max, int cap) {
+                                                      int chunk, int n_wg, int n_slots) {
   constexpr int NS = 8;
   constexpr int EPL = D / 32;
   const int hq = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int st = tid >> 5, li = tid & 31;
   const size_t obase = ((size_t)b * Hq + hq) * D;
-  const int len = min(lens[b], cap);
-  if (len <= 0) {
+  const long long c0 = cum[b], c1 = cum[b + 1];
+  if (c1 <= c0) {
     if (tid < D) store_elem(out, obase + tid, out_dt, 0.f);
     return;
   }
-  const int nc = (len + chunk - 1) / chunk;
-  if (nc > n_chunks_max) {  // plan too small for this length: flag, never read past it
+  if (c1 > (long long)n_wg * chunk) {  // plan too small for these lengths: flag, never read past it
     if (tid < D) store_elem(out, obase + tid, out_dt, __builtin_nanf(""));
     return;
   }
-  const size_t base = ((size_t)b * Hq + hq) * n_chunks_max;
+  const long long wf = c0 / chunk;
+  const int np = (int)((c1 - 1) / chunk - wf + 1);
+  const size_t base = (size_t)hq * n_slots + wf + b;
   float M = -INFINITY, L = 0.f, O[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) O[e] = 0.f;
 #pragma unroll 4
-  for (int n = st; n < nc; n += NS) {
+  for (int n = st; n < np; n += NS) {
     const float mn = ws_ml[(base + n) * 2];
     const float ln = ws_ml[(base + n) * 2 + 1];
     float on[EPL];
@@ -258,7 +338,7 @@ __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, in
 #pragma unroll
       for (int e = 0; e < EPL; ++e) on[e] = src[e];
     }
-    // every chunk n < nc holds at least one token, so mn is finite
+    // every piece holds at least one token, so mn is finite
     const float Mn = fmaxf(M, mn);
     const float wa = fast_exp2(M - Mn), wb = fast_exp2(mn - Mn);
     L = L * wa + ln * wb;
@@ -282,7 +362,7 @@ __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, in
     float LL = 0.f, OO = 0.f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const float w = fast_exp2(sm_ml[s][0] - MM);  // streams with no chunk: w = 0
+      const float w = fast_exp2(sm_ml[s][0] - MM);  // streams with no piece: w = 0
       LL = fmaf(w, sm_ml[s][1], LL);
       OO = fmaf(w, sm_o[s][tid], OO);
     }
@@ -298,20 +378,20 @@ int heads_per_group(int Hkv) {
 }
 
 template <typename TC, int D, int G, bool PAGED>
-void launch_partial(const DecodeArgs& a, int B, hipStream_t s) {
+void launch_partial(const DecodeArgs& a, hipStream_t s) {
   // Tokens per row per iteration: 8 x 16 B (or 8 x 8 B for bf16 D=64) in
   // flight per lane for K and as many for V; 4 x 32 B for fp32 D=128.
   constexpr int TPG = (sizeof(TC) == 4 && D == 128) ? 4 : 8;
-  dim3 grid(a.n_chunks_max, a.Hkv / a.hw, B);
+  dim3 grid(a.n_wg, a.Hkv / a.hw);
   hipLaunchKernelGGL((k_decode_partial<TC, D, G, TPG, PAGED>), grid, dim3(16 * a.hw * a.S), 0, s,
                      a);
 }
 
 template <typename TC, bool PAGED>
-int dispatch_partial(const DecodeArgs& a, int B, int D, int G, hipStream_t s) {
+int dispatch_partial(const DecodeArgs& a, int D, int G, hipStream_t s) {
 #define SKV_DEC(DD, GG)                                    \
   if (D == DD && G == GG) {                                \
-    launch_partial<TC, DD, GG, PAGED>(a, B, s);            \
+    launch_partial<TC, DD, GG, PAGED>(a, s);               \
     return 0;                                              \
   }
   SKV_DEC(64, 1) SKV_DEC(64, 2) SKV_DEC(64, 4) SKV_DEC(64, 8)
@@ -346,8 +426,11 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
               fn);
   SKV_REQUIRE(chunk > 0 && chunk % 16 == 0, SKV_E_INVALID,
               "%s: chunk_tokens=%d must be a positive multiple of 16", fn, chunk);
-  SKV_REQUIRE(n_chunks_max > 0 && n_chunks_max <= (1 << 20), SKV_E_INVALID,
-              "%s: n_chunks_max=%d out of range", fn, n_chunks_max);
+  SKV_REQUIRE(n_chunks_max >= 2 && n_chunks_max <= (1 << 20), SKV_E_INVALID,
+              "%s: n_chunks_max=%d out of range [2, 2^20]", fn, n_chunks_max);
+  const long long n_slots = (long long)B * n_chunks_max;
+  SKV_REQUIRE(n_slots <= (1LL << 31) - 1, SKV_E_UNSUPPORTED,
+              "%s: B * n_chunks_max = %lld exceeds the grid limit", fn, n_slots);
   const size_t need = skv_decode_workspace_bytes(B, Hq, D, n_chunks_max);
   SKV_REQUIRE(ws_bytes >= need, SKV_E_WORKSPACE, "%s: workspace %zu bytes < %zu required", fn,
               ws_bytes, need);
@@ -362,29 +445,33 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   DecodeArgs a;
   a.q = q; a.k = k; a.v = v; a.lens = lens; a.block_table = bt;
   a.max_blocks = max_blocks; a.bs_shift = shift;
-  a.Hq = Hq; a.Hkv = Hkv; a.T_cap = T_cap;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_cap = T_cap;
   a.cap = PAGED ? (max_blocks << shift) : T_cap;
   a.qscale = scale * LOG2E;
-  a.chunk = chunk; a.n_chunks_max = n_chunks_max; a.q_dt = q_dt;
+  a.chunk = chunk; a.q_dt = q_dt;
+  // B pieces more than workgroups: a sequence can start inside a workgroup.
+  a.n_slots = (int)n_slots;
+  a.n_wg = (int)(n_slots - B);
   a.hw = heads_per_group(Hkv);
   a.S = kMaxRows / a.hw;
   SKV_REQUIRE(Hkv / a.hw <= 65535, SKV_E_UNSUPPORTED, "%s: H_kv=%d exceeds the grid limit", fn,
               Hkv);
-  const size_t o_elems = (size_t)B * Hq * n_chunks_max * D;
+  const size_t parts = (size_t)Hq * a.n_slots;
   a.ws_o = static_cast<float*>(ws);
-  a.ws_ml = a.ws_o + o_elems;
+  a.ws_ml = a.ws_o + parts * D;
+  a.cum = reinterpret_cast<long long*>(a.ws_ml + parts * 2);
   const int G = Hq / Hkv;
-  int rc = cache_dt == SKV_BF16 ? dispatch_partial<uint16_t, PAGED>(a, B, D, G, s)
-                                : dispatch_partial<float, PAGED>(a, B, D, G, s);
+  int rc = cache_dt == SKV_BF16 ? dispatch_partial<uint16_t, PAGED>(a, D, G, s)
+                                : dispatch_partial<float, PAGED>(a, D, G, s);
   if (rc) return rc;
   rc = check_launch(fn);
   if (rc) return rc;
   if (D == 64)
-    hipLaunchKernelGGL(k_decode_merge<64>, dim3(Hq, B), dim3(256), 0, s, out, out_dt, lens,
-                       a.ws_o, a.ws_ml, Hq, chunk, n_chunks_max, a.cap);
+    hipLaunchKernelGGL(k_decode_merge<64>, dim3(Hq, B), dim3(256), 0, s, out, out_dt, a.cum,
+                       a.ws_o, a.ws_ml, Hq, chunk, a.n_wg, a.n_slots);
   else
-    hipLaunchKernelGGL(k_decode_merge<128>, dim3(Hq, B), dim3(256), 0, s, out, out_dt, lens,
-                       a.ws_o, a.ws_ml, Hq, chunk, n_chunks_max, a.cap);
+    hipLaunchKernelGGL(k_decode_merge<128>, dim3(Hq, B), dim3(256), 0, s, out, out_dt, a.cum,
+                       a.ws_o, a.ws_ml, Hq, chunk, a.n_wg, a.n_slots);
   return check_launch(fn);
 }
 
@@ -402,14 +489,14 @@ extern "C" int skv_decode_plan(int B, int H_kv, int max_len, long long total_len
   if (chunk_hint > 0) {
     chunk = (int)(((long)chunk_hint + 15) / 16 * 16);
   } else {
-    // At most about 512 workgroups per call: two per CU on MI355X's 256 CUs,
-    // as evenly as the lengths allow. On C4 (4 x 32K tokens) this measured
-    // fastest: 1 or 2 workgroups on every CU stream at the same rate, while
-    // grids that leave some CUs one workgroup more than others (e.g. 336
-    // workgroups) or that use more, shorter chunks were 5-15% slower. Chunks
-    // are 32 to 8192 tokens, sized from the filled tokens of the whole batch
-    // so a ragged batch gets as many workgroups as a uniform one of the same
-    // total.
+    // About 512 busy workgroups per call: two per CU on MI355X's 256 CUs.
+    // On C4 (4 x 32K tokens) this measured fastest: 1 or 2 workgroups on
+    // every CU stream at the same rate, while grids that leave some CUs one
+    // workgroup more than others (e.g. 336 workgroups) or that use more,
+    // shorter chunks were 5-15% slower. A workgroup owns chunk tokens of the
+    // flat token stream (every sequence's filled tokens end to end), so the
+    // chunk follows the batch's total fill and a ragged batch splits as
+    // evenly as a uniform one. Chunks are 32 to 8192 tokens.
     const long long tot = total_len > 0 ? total_len : (long long)B * max_len;
     const long long groups = H_kv / heads_per_group(H_kv);
     const long long target = 2 * kNumCUs;
@@ -419,7 +506,10 @@ extern "C" int skv_decode_plan(int B, int H_kv, int max_len, long long total_len
     if (per > 8192) per = 8192;
     chunk = (int)per;
   }
-  const long n = ((long)max_len + chunk - 1) / chunk;
+  // ceil(max_len / chunk) workgroups per sequence cover B * max_len tokens;
+  // one more slot per sequence holds the piece of a sequence that starts
+  // inside a workgroup's range.
+  const long n = ((long)max_len + chunk - 1) / chunk + 1;
   SKV_REQUIRE(n <= (1 << 20), SKV_E_UNSUPPORTED,
               "skv_decode_plan: %ld chunks exceed the grid limit", n);
   *chunk_tokens = chunk;
@@ -430,7 +520,8 @@ extern "C" int skv_decode_plan(int B, int H_kv, int max_len, long long total_len
 extern "C" size_t skv_decode_workspace_bytes(int B, int H_q, int D, int n_chunks_max) {
   if (B <= 0 || H_q <= 0 || D <= 0 || n_chunks_max <= 0) return 0;
   const size_t parts = (size_t)B * H_q * n_chunks_max;
-  return parts * (size_t)(D + 2) * sizeof(float);
+  // partials (o[D], m, l) per (query head, slot), then B + 1 int64 prefix sums
+  return parts * (size_t)(D + 2) * sizeof(float) + (size_t)(B + 1) * sizeof(long long);
 }
 
 extern "C" int skv_decode_attn(void* out, const void* q, const void* k_cache, const void* v_cache,

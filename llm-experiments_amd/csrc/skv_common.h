@@ -117,6 +117,21 @@ __device__ __forceinline__ void load8_f32(const void* p, size_t i, int dt, float
   }
 }
 
+// Four consecutive elements, as load8_f32 (p + i 16-byte aligned for fp32,
+// 8-byte aligned for bf16).
+__device__ __forceinline__ void load4_f32(const void* p, size_t i, int dt, float* out) {
+  if (dt == SKV_BF16) {
+    const uint2 x = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    out[0] = bf16w_lo(x.x);
+    out[1] = bf16w_hi(x.x);
+    out[2] = bf16w_lo(x.y);
+    out[3] = bf16w_hi(x.y);
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  }
+}
+
 // Element loads/stores with runtime dtype (used off the hot loops).
 __device__ __forceinline__ float load_elem(const void* p, size_t i, int dt) {
   return dt == SKV_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i])

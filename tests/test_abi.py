@@ -37,22 +37,24 @@ def test_decode_plan_covers_every_length(B, Hkv, L):
     rc, chunk, n = _plan(B, Hkv, L)
     assert rc == 0
     assert chunk % 32 == 0 and 32 <= chunk <= 8192
-    assert n * chunk >= L > (n - 1) * chunk
+    # one workgroup range per chunk of every sequence, plus one spare slot
+    # per sequence for the piece that starts inside a workgroup's range
+    assert (n - 1) * chunk >= L > (n - 2) * chunk
 
 
 def test_decode_plan_c4_and_ragged_total():
     # C4: 4 sequences x 16 kv heads (one head group) at 32256 -> 256-token
-    # chunks, 126 per sequence = 504 workgroups (two per CU)
-    assert _plan(4, 16, 32256) == (0, 256, 126)
+    # chunks, 4 * 126 = 504 workgroups (two per CU), 127 slots per sequence
+    assert _plan(4, 16, 32256) == (0, 256, 127)
     # a ragged batch plans from its total fill, not from B * max_len
     rc, chunk, n = _plan(64, 8, 8192, total=64 * 2000)
-    assert rc == 0 and chunk == 256 and n == 32
+    assert rc == 0 and chunk == 256 and n == 33
     assert _plan(64, 8, 8192)[1] > chunk
 
 
 def test_decode_plan_hint_and_errors():
     rc, chunk, n = _plan(4, 16, 32768, hint=1000)
-    assert rc == 0 and chunk == 1008 and n == 33
+    assert rc == 0 and chunk == 1008 and n == 34
     assert _plan(0, 16, 100)[0] == _lib.SKV_E_INVALID
     assert _plan(4, 16, 0)[0] == _lib.SKV_E_INVALID
     assert b"dims must be > 0" in _lib.lib().skv_last_error()
@@ -60,7 +62,8 @@ def test_decode_plan_hint_and_errors():
 
 def test_workspace_bytes():
     L = _lib.lib()
-    assert L.skv_decode_workspace_bytes(4, 16, 128, 32) == 4 * 16 * 32 * (128 + 2) * 4
+    # partials (o, m, l) per (query head, slot), then B + 1 int64 prefix sums
+    assert L.skv_decode_workspace_bytes(4, 16, 128, 32) == 4 * 16 * 32 * (128 + 2) * 4 + 5 * 8
     assert L.skv_decode_workspace_bytes(0, 16, 128, 32) == 0
 
 
@@ -73,8 +76,8 @@ def test_entry_points_reject_bad_arguments():
     assert rc == _lib.SKV_E_INVALID and b"dtype" in L.skv_last_error()
     rc = L.skv_append_paged(fake, fake, fake, fake, fake, fake, 4, 12, 2, 4, 64, 0, 0, None)
     assert rc == _lib.SKV_E_INVALID and b"power of two" in L.skv_last_error()
-    ws = L.skv_decode_workspace_bytes(2, 4, 64, 1)
-    args = dict(B=2, Hq=4, Hkv=4, D=64, T=128, scale=0.125, chunk=256, n=1)
+    ws = L.skv_decode_workspace_bytes(2, 4, 64, 2)
+    args = dict(B=2, Hq=4, Hkv=4, D=64, T=128, scale=0.125, chunk=256, n=2)
 
     def dec(**kw):
         a = {**args, **kw}
@@ -86,7 +89,8 @@ def test_entry_points_reject_bad_arguments():
     assert dec(Hq=6, Hkv=4) == _lib.SKV_E_INVALID
     assert dec(chunk=100) == _lib.SKV_E_INVALID  # not a multiple of 16
     assert dec(ws=ws - 1) == _lib.SKV_E_WORKSPACE
-    ws48 = L.skv_decode_workspace_bytes(2, 48, 64, 1)
+    assert dec(n=1) == _lib.SKV_E_INVALID  # no spare slot per sequence
+    ws48 = L.skv_decode_workspace_bytes(2, 48, 64, 2)
     assert dec(Hq=48, Hkv=3, ws=ws48) == _lib.SKV_E_UNSUPPORTED  # G = 16 has no kernel
     rc = L.skv_append_chunk(fake, fake, fake, fake, fake, None, 2, 0, 4, 64, 128, 0, 0, None)
     assert rc == _lib.SKV_E_INVALID
