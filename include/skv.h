@@ -198,10 +198,19 @@ int skv_layernorm(float* y, const float* x, const float* gamma, const float* bet
  * split_cols > 0 writes column n to segment n / split_cols of a
  * [N / split_cols][M][split_cols] output (q, k, v of a fused projection as
  * three contiguous [M, d] blocks). K must be a multiple of 4. Sums run in a
- * fixed order, so results are reproducible run to run. */
+ * fixed order, so results are reproducible run to run.
+ * ws (may be NULL) of skv_linear_workspace_bytes(M, N, K) bytes lets a
+ * narrow projection (few 16-column tiles) split K over more workgroups and
+ * finish in a second kernel; the split sums in a different fixed order, so
+ * its bits differ from the unsplit result within fp32 rounding. Calls that
+ * share ws must be stream ordered. */
 int skv_linear(float* y, const float* x, const float* w_t, const float* bias,
                const float* residual, const float* ln_gamma, const float* ln_beta, float ln_eps,
-               int M, int N, int K, int activation, int split_cols, skv_stream_t stream);
+               int M, int N, int K, int activation, int split_cols, void* ws, size_t ws_bytes,
+               skv_stream_t stream);
+
+/* Workspace skv_linear can use for these sizes (0: it never splits them). */
+size_t skv_linear_workspace_bytes(int M, int N, int K);
 
 /* Workspace of skv_argmax (per-slice candidates and counters); zero it
  * once before its first use; not shared by concurrent calls. */

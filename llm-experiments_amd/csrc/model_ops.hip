@@ -137,6 +137,8 @@ struct LinArgs {
   int M, N, K;
   int act;      // 0 none, 1 gelu (tanh form)
   int split;    // > 0: column n goes to segment n / split of a [N/split][M][split] output
+  int kz;       // K range of one workgroup along grid z (a multiple of 16; K when unsplit)
+  float* part;  // split K: raw partial sums [grid z][M][N]; the reduce pass finishes them
 };
 
 // Lane layout of v_mfma_f32_16x16x4_f32: operand A lane l holds
@@ -146,17 +148,22 @@ struct LinArgs {
 // the same 16-byte load of x and of Wt (a consistent permutation of k).
 //
 // The W wavefronts of a workgroup (W = blockDim / 64) split K in contiguous
-// ranges, each keeping U weight loads in flight, and sum their tiles through
-// LDS; no workgroup waits on another. Measured on MI355X (M = 16): a CU
-// streams ~15-20 GB/s of weights whatever W and U are, so narrow layers
-// (few 16-column tiles, one CU each) want many short-range wavefronts
-// (W = 16, U = 2) and wide layers (the 50304-column logits) few long ones
-// (W = 2, U = 8); a masked deep unroll costs extra time on small K. With ln_g set, each x row is layer-normalized as it is read
-// (mean and 1/std of the workgroup's rows are computed first), which takes
-// the LayerNorm launch out of the step.
-template <int TILES, int U>
+// ranges of STEPS 16-wide steps and sum their tiles through LDS; no
+// workgroup waits on another. Each wavefront issues every load it needs --
+// its weights, its x values, gamma and beta, and for the epilogue threads the
+// bias and residual -- before it uses any of them, so a projection costs one
+// HBM round trip for the weights, overlapped with the LayerNorm statistics,
+// instead of one per unrolled round: at these sizes (M <= 64 rows, a few MB
+// of weights) a CU's weight stream is latency-bound, so the number of
+// dependent round trips sets the time. K beyond W * STEPS * 16 (K > 3072 for
+// 16 wavefronts of 12 steps) runs in further passes.
+//
+// With LN, each x row is layer-normalized as it is read: the mean and 1/std
+// of the workgroup's rows are computed first (one pass over values shifted by
+// the row's first element, var = E[(x-c)^2] - E[x-c]^2), which takes the
+// LayerNorm launch out of the step.
+template <int TILES, int STEPS, bool LN>
 __global__ __launch_bounds__(kLinMaxWaves * 64) void k_linear(LinArgs a) {
-  constexpr int kLinUnroll = U;
   extern __shared__ float red[];  // [W][TILES][64][4] partial tiles
   __shared__ float stat[kLinRowsPerBlock][2];
   const int NW = blockDim.x >> 6;
@@ -165,120 +172,178 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void k_linear(LinArgs a) {
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int lr = l & 15, lk = l >> 4;
   const int rows = min(TILES * 16, a.M - m0);
-  const bool ln = a.ln_g != nullptr;
+  const int n = n0 + lr;
+  const bool n_ok = n < a.N;
+  const float* wrow = a.wt + (size_t)(n_ok ? n : 0) * a.K;
+  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  // Loads read a clamped, in-bounds address and select zero afterwards: a
+  // load inside a condition cannot be hoisted, and the compiler then splits
+  // it into four guarded 4-byte loads. K % 4 == 0, so K - 4 starts a float4.
+  const int klast = a.K - 4;
+  auto load4 = [](const float* p, bool ok, float4 z) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    return ok ? v : z;
+  };
 
-  if (ln) {
-    // Row statistics, one wavefront per row, in a single pass over values
-    // shifted by the row's first element c (var = E[(x-c)^2] - E[x-c]^2 stays
-    // well conditioned when |mean| >> std), so all loads are in flight at once.
-    for (int r = wave; r < rows; r += NW) {
-      const float* xr = a.x + (size_t)(m0 + r) * a.K;
-      const float c = xr[0];
-      float sum = 0.f, sq = 0.f;
-      for (int j = l; j < a.K; j += 64) {
-        const float v = xr[j] - c;
-        sum += v;
-        sq += v * v;
+  // Epilogue thread (t, ll) = (wave, lane) of the first TILES wavefronts:
+  // its bias and residual values are loaded now, with everything else.
+  const bool epi = wave < TILES && wave * 16 < rows && n0 + (l & 15) < a.N;
+  const bool partial = a.part != nullptr;  // split K: raw sums, no epilogue here
+  const int nn = n0 + (l & 15);
+  float bias_v = 0.f, resv[4] = {0.f, 0.f, 0.f, 0.f};
+  size_t oidx[4] = {0, 0, 0, 0};
+  if (epi && !partial) {
+    if (a.bias) bias_v = a.bias[nn];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + wave * 16 + 4 * (l >> 4) + i;
+      if (m >= a.M) continue;
+      if (a.split > 0) {
+        const int seg = nn / a.split;
+        oidx[i] = ((size_t)seg * a.M + m) * a.split + (nn - seg * a.split);
+      } else {
+        oidx[i] = (size_t)m * a.N + nn;
       }
-      const float ms = wave_sum(sum) / a.K;
-      const float mean = c + ms;
-      const float rstd = 1.f / sqrtf(fmaxf(wave_sum(sq) / a.K - ms * ms, 0.f) + a.ln_eps);
-      if (l == 0) {
-        stat[r][0] = mean;
-        stat[r][1] = rstd;
-      }
+      if (a.res) resv[i] = a.res[oidx[i]];
     }
-    __syncthreads();
   }
-
-  // K range of this wavefront, in steps of 16
-  const int steps = (a.K + 15) / 16;
-  const int per = (steps + NW - 1) / NW;
-  const int k_begin = wave * per * 16;
-  const int k_end = min(a.K, (wave + 1) * per * 16);
 
   f32x4 acc[TILES];
 #pragma unroll
   for (int t = 0; t < TILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int n = n0 + lr;
-  const bool n_ok = n < a.N;
-  const float* wrow = a.wt + (size_t)(n_ok ? n : 0) * a.K;
 
-  auto load_w = [&](int kk) {
-    return (n_ok && kk < a.K) ? *reinterpret_cast<const float4*>(wrow + kk)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
-  };
-  auto fma_step = [&](int kk, const float4& w) {
-    float4 g = make_float4(1.f, 1.f, 1.f, 1.f), bb = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (ln && kk < a.K) {
-      g = *reinterpret_cast<const float4*>(a.ln_g + kk);
-      bb = *reinterpret_cast<const float4*>(a.ln_b + kk);
+  const int pass_k = NW * STEPS * 16;
+  const int kz0 = blockIdx.z * a.kz;
+  const int kz1 = min(a.K, kz0 + a.kz);
+  for (int kp = kz0; kp < kz1; kp += pass_k) {
+    const int kb = kp + wave * STEPS * 16 + 4 * lk;
+    float4 w[STEPS], xv[TILES][STEPS], g[LN ? STEPS : 1], be[LN ? STEPS : 1];
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+      const int kk = kb + 16 * st;
+      w[st] = load4(wrow + min(kk, klast), n_ok && kk < kz1, zero4);
     }
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-      const int r = t * 16 + lr;
-      float4 xv = (r < rows && kk < a.K)
-                      ? *reinterpret_cast<const float4*>(a.x + (size_t)(m0 + r) * a.K + kk)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-      if (ln && r < rows && kk < a.K) {
-        const float mu = stat[r][0], rs = stat[r][1];
-        xv.x = (xv.x - mu) * rs * g.x + bb.x;
-        xv.y = (xv.y - mu) * rs * g.y + bb.y;
-        xv.z = (xv.z - mu) * rs * g.z + bb.z;
-        xv.w = (xv.w - mu) * rs * g.w + bb.w;
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) {
+        const int r = t * 16 + lr, kk = kb + 16 * st;
+        xv[t][st] = load4(a.x + (size_t)(m0 + min(r, rows - 1)) * a.K + min(kk, klast),
+                          r < rows && kk < kz1, zero4);
       }
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, w.x, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, w.y, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, w.z, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, w.w, acc[t], 0, 0, 0);
-    }
-  };
-  // All (up to kLinUnroll) steps of a round issue their loads before any
-  // MFMA; steps past this wavefront's range are masked to zero, so a short
-  // range costs one round trip. K % 4 == 0: a 16-byte group at kk is either
-  // wholly inside the range or past it.
-  for (int k = k_begin; k < k_end; k += 16 * kLinUnroll) {
-    float4 w[kLinUnroll];
+    if constexpr (LN) {
 #pragma unroll
-    for (int u = 0; u < kLinUnroll; ++u) {
-      const int kk = k + u * 16 + 4 * lk;
-      w[u] = kk < k_end ? load_w(kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int st = 0; st < STEPS; ++st) {
+        const int kk = kb + 16 * st;
+        g[st] = load4(a.ln_g + min(kk, klast), kk < kz1, zero4);
+        be[st] = load4(a.ln_b + min(kk, klast), kk < kz1, zero4);
+      }
+    }
+    // keep every load above issued before the first use below
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (LN) {
+      if (kp == kz0) {
+        // row statistics over the whole row, one wavefront per row
+        for (int r = wave; r < rows; r += NW) {
+          const float* xr = a.x + (size_t)(m0 + r) * a.K;
+          const float c = xr[0];
+          float sum = 0.f, sq = 0.f;
+          for (int j = l; j < a.K; j += 64) {
+            const float v = xr[j] - c;
+            sum += v;
+            sq += v * v;
+          }
+          const float ms = wave_sum(sum) / a.K;
+          const float mean = c + ms;
+          const float rstd = 1.f / sqrtf(fmaxf(wave_sum(sq) / a.K - ms * ms, 0.f) + a.ln_eps);
+          if (l == 0) {
+            stat[r][0] = mean;
+            stat[r][1] = rstd;
+          }
+        }
+        __syncthreads();
+      }
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        const int r = t * 16 + lr;
+        if (r >= rows) continue;  // those x values are zero already
+        const float mu = stat[r][0], rs = stat[r][1];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+          if (kb + 16 * st >= kz1) continue;
+          float4& v = xv[t][st];
+          v.x = (v.x - mu) * rs * g[st].x + be[st].x;
+          v.y = (v.y - mu) * rs * g[st].y + be[st].y;
+          v.z = (v.z - mu) * rs * g[st].z + be[st].z;
+          v.w = (v.w - mu) * rs * g[st].w + be[st].w;
+        }
+      }
     }
 #pragma unroll
-    for (int u = 0; u < kLinUnroll; ++u) {
-      const int kk = k + u * 16 + 4 * lk;
-      fma_step(kk < k_end ? kk : a.K, w[u]);  // kk = K marks a masked step
-    }
+    for (int st = 0; st < STEPS; ++st)
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t][st].x, w[st].x, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t][st].y, w[st].y, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t][st].z, w[st].z, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t][st].w, w[st].w, acc[t], 0, 0, 0);
+      }
   }
 #pragma unroll
   for (int t = 0; t < TILES; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[((wave * TILES + t) * 64 + l) * 4 + i] = acc[t][i];
   __syncthreads();
-  // thread -> (row tile t, lane ll): sums the wavefronts' partial tiles
-  if (threadIdx.x >= TILES * 64) return;
-  const int t = threadIdx.x >> 6, ll = threadIdx.x & 63;
-  if (t * 16 >= rows) return;
-  const int nn = n0 + (ll & 15);
-  if (nn >= a.N) return;
-  const float b = a.bias ? a.bias[nn] : 0.f;
+  // thread -> (row tile t = wave, lane l): sums the wavefronts' partial tiles
+  if (!epi) return;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int m = m0 + t * 16 + 4 * (ll >> 4) + i;
+    const int m = m0 + wave * 16 + 4 * (l >> 4) + i;
     if (m >= a.M) continue;
-    float v = b;
-    for (int wv = 0; wv < NW; ++wv) v += red[((wv * TILES + t) * 64 + ll) * 4 + i];
-    if (a.act == 1) v = gelu_tanh(v);
-    size_t o;
-    if (a.split > 0) {
-      const int seg = nn / a.split;
-      o = ((size_t)seg * a.M + m) * a.split + (nn - seg * a.split);
-    } else {
-      o = (size_t)m * a.N + nn;
+    float v = bias_v;
+    for (int wv = 0; wv < NW; ++wv) v += red[((wv * TILES + wave) * 64 + l) * 4 + i];
+    if (partial) {
+      a.part[((size_t)blockIdx.z * a.M + m) * a.N + nn] = v;
+      continue;
     }
-    if (a.res) v += a.res[o];
-    a.y[o] = v;
+    if (a.act == 1) v = gelu_tanh(v);
+    a.y[oidx[i]] = v + resv[i];
   }
+}
+
+// Split-K finish: y = act(bias + sum of the S partials, in order) + res, one
+// thread per output element.
+__global__ __launch_bounds__(256) void k_linear_reduce(LinArgs a, int S) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)a.M * a.N) return;
+  const int m = (int)(i / a.N), nn = (int)(i - (size_t)m * a.N);
+  float v = a.bias ? a.bias[nn] : 0.f;
+  for (int z = 0; z < S; ++z) v += a.part[((size_t)z * a.M + m) * a.N + nn];
+  if (a.act == 1) v = gelu_tanh(v);
+  size_t o = i;
+  if (a.split > 0) {
+    const int seg = nn / a.split;
+    o = ((size_t)seg * a.M + m) * a.split + (nn - seg * a.split);
+  }
+  if (a.res) v += a.res[o];
+  a.y[o] = v;
+}
+
+// Split count along K for a projection: narrow ones (fewer than ~160
+// workgroups of 16 columns x 64 rows) leave most CUs idle, and a CU's weight
+// stream is capped (~15-20 GB/s measured), so K is split until about 256
+// workgroups run, keeping at least 16 steps (256 k) per split. Only long K
+// (>= 2048) gains: measured on MI355X, the 16 x 768 x 3072 projection went
+// from 13.5 to 10.3 us, while at K = 768 or 1024 the reduce launch costs more
+// than the split saves.
+int linear_splits(int M, int N, int K) {
+  const long wgs = (long)((N + 15) / 16) * ((M + kLinRowsPerBlock - 1) / kLinRowsPerBlock);
+  const int ksteps = (K + 15) / 16;
+  if (wgs >= 160 || ksteps < 128) return 1;
+  int S = (int)((256 + wgs - 1) / wgs);
+  if (S > ksteps / 16) S = ksteps / 16;
+  const int kz = (ksteps + S - 1) / S;  // steps per split; drop empty splits
+  return (ksteps + kz - 1) / kz;
 }
 
 // ---------------------------------------------------------------------------
@@ -382,10 +447,16 @@ extern "C" int skv_layernorm(float* y, const float* x, const float* gamma, const
   return check_launch("skv_layernorm");
 }
 
+extern "C" size_t skv_linear_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const int S = linear_splits(M, N, K);
+  return S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+}
+
 extern "C" int skv_linear(float* y, const float* x, const float* w_t, const float* bias,
                           const float* residual, const float* ln_gamma, const float* ln_beta,
                           float ln_eps, int M, int N, int K, int activation, int split_cols,
-                          skv_stream_t stream) {
+                          void* ws, size_t ws_bytes, skv_stream_t stream) {
   SKV_REQUIRE(y && x && w_t, SKV_E_INVALID, "skv_linear: null pointer argument");
   SKV_REQUIRE(M > 0 && N > 0 && K > 0, SKV_E_INVALID, "skv_linear: dims must be > 0");
   SKV_REQUIRE(K % 4 == 0, SKV_E_UNSUPPORTED, "skv_linear: K=%d must be a multiple of 4", K);
@@ -396,26 +467,55 @@ extern "C" int skv_linear(float* y, const float* x, const float* w_t, const floa
               "skv_linear: LayerNorm needs both gamma and beta");
   SKV_REQUIRE((M + kLinRowsPerBlock - 1) / kLinRowsPerBlock <= 65535, SKV_E_UNSUPPORTED,
               "skv_linear: M=%d too large", M);
+  const int ksteps = (K + 15) / 16;
+  // split K when the caller gave room for the partials
+  int S = linear_splits(M, N, K);
+  if (S > 1 && (ws == nullptr || ws_bytes < (size_t)S * M * N * sizeof(float))) S = 1;
+  const int kz_steps = (ksteps + S - 1) / S;
   LinArgs a{y, x, w_t, bias, residual, ln_gamma, ln_beta, ln_eps, M, N, K, activation,
-            split_cols};
+            split_cols, S > 1 ? kz_steps * 16 : K, S > 1 ? static_cast<float*>(ws) : nullptr};
   const int col_tiles = (N + 15) / 16;
-  // enough wavefronts per tile that narrow layers still fill the machine
-  const bool wide = col_tiles >= 1024;
-  const int nw = wide ? 2 : 16;
   const int tiles = M >= kLinRowsPerBlock ? 4 : (M + 15) / 16;
-  dim3 grid(col_tiles, (M + kLinRowsPerBlock - 1) / kLinRowsPerBlock);
+  // Wavefronts per workgroup: narrow layers (few 16-column tiles, one CU
+  // each) split their K range over 16 wavefronts; the wide logits use 8,
+  // since every CU holds several of their workgroups.
+  const bool wide = col_tiles >= 1024;
+  int nw = wide ? 8 : (kz_steps < kLinMaxWaves ? kz_steps : kLinMaxWaves);
+  nw = nw < tiles ? tiles : nw;  // wavefront t writes row tile t in the epilogue
+  const bool ln = ln_gamma != nullptr;
+  // Steps per pass: at most 4 (measured on MI355X: deeper passes gain
+  // nothing on narrow layers, since a CU's weight stream is capped, and on the
+  // wide logits 3 beat 4 and 12 by keeping more workgroups resident), and no
+  // more than fit the registers without spilling (checked with the
+  // compiler's resource report: per step, w and x take (1 + TILES) * 4
+  // registers and LN's gamma and beta 8 more).
+  const int max_steps = wide ? 3 : ln ? (tiles == 1 ? 4 : tiles == 2 ? 3 : 2) : 4;
+  int steps = (kz_steps + nw - 1) / nw;
+  steps = steps > max_steps ? max_steps : steps;
+  dim3 grid(col_tiles, (M + kLinRowsPerBlock - 1) / kLinRowsPerBlock, S);
   const size_t lds = (size_t)nw * tiles * 64 * 4 * sizeof(float);
   hipStream_t s = (hipStream_t)stream;
-#define SKV_LIN(T)                                                                           \
-  if (wide) hipLaunchKernelGGL((k_linear<T, 8>), grid, dim3(nw * 64), lds, s, a);           \
-  else hipLaunchKernelGGL((k_linear<T, 2>), grid, dim3(nw * 64), lds, s, a);
-  switch (tiles) {
-    case 1: SKV_LIN(1) break;
-    case 2: SKV_LIN(2) break;
-    case 3: SKV_LIN(3) break;
-    default: SKV_LIN(4) break;
+  bool launched = false;
+#define SKV_LIN(T, S_, L)                                                                 \
+  if (!launched && tiles == T && steps == S_ && ln == L) {                                \
+    hipLaunchKernelGGL((k_linear<T, S_, L>), grid, dim3(nw * 64), lds, s, a);             \
+    launched = true;                                                                      \
   }
+#define SKV_LIN2(T, S_) SKV_LIN(T, S_, false) SKV_LIN(T, S_, true)
+  SKV_LIN2(1, 1) SKV_LIN2(1, 2) SKV_LIN2(1, 3) SKV_LIN2(1, 4)
+  SKV_LIN2(2, 1) SKV_LIN2(2, 2) SKV_LIN2(2, 3) SKV_LIN(2, 4, false)
+  SKV_LIN2(3, 1) SKV_LIN2(3, 2) SKV_LIN(3, 3, false) SKV_LIN(3, 4, false)
+  SKV_LIN2(4, 1) SKV_LIN2(4, 2) SKV_LIN(4, 3, false) SKV_LIN(4, 4, false)
+#undef SKV_LIN2
 #undef SKV_LIN
+  if (!launched)
+    return set_error(SKV_E_UNSUPPORTED, "skv_linear: no kernel for %d row tiles x %d steps",
+                     tiles, steps);
+  int rc = check_launch("skv_linear");
+  if (rc || S == 1) return rc;
+  const size_t n_out = (size_t)M * N;
+  hipLaunchKernelGGL(k_linear_reduce, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s, a,
+                     S);
   return check_launch("skv_linear");
 }
 

@@ -44,7 +44,8 @@ _SIGNATURES = {
                               _I, _I, _I, _P]),
     "skv_embed": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "skv_layernorm": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
-    "skv_linear": (_I, [_P, _P, _P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P]),
+    "skv_linear": (_I, [_P, _P, _P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _Z, _P]),
+    "skv_linear_workspace_bytes": (_Z, [_I, _I, _I]),
     "skv_argmax_workspace_bytes": (_Z, [_I, _I]),
     "skv_argmax": (_I, [_P, _P, _I, _I, _P, _Z, _P]),
     "skv_next_tokens": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),

@@ -105,6 +105,11 @@ class _Buffers:
         L = _lib.lib()
         arg = L.skv_argmax_workspace_bytes(B, vocab)
         self.arg_ws = torch.zeros(max(arg, 4), dtype=torch.uint8, device=dev)
+        # split-K partials of the narrow projections, shared by the step's
+        # linears (stream ordered)
+        lin = max(L.skv_linear_workspace_bytes(B, n, k)
+                  for n, k in ((3 * d, d), (d, d), (mlp, d), (d, mlp), (vocab, d)))
+        self.lin_ws = torch.empty(max(lin, 4), dtype=torch.uint8, device=dev)
 
 
 class TransformerModel:
@@ -211,6 +216,7 @@ class TransformerModel:
         x, h, qkv, attn, ff = bf.x.data_ptr(), bf.h.data_ptr(), bf.qkv.data_ptr(), \
             bf.attn.data_ptr(), bf.ff.data_ptr()
         q_ptr, k_ptr, v_ptr = qkv, qkv + B * d * 4, qkv + 2 * B * d * 4
+        lw_ws, lw_n = bf.lin_ws.data_ptr(), bf.lin_ws.numel()
         lens0 = cache.layers[0].lens.data_ptr()
         chk(L.skv_embed(x, bf.ids.data_ptr(), lens0, self.emb.data_ptr(), self.pe.data_ptr(), B, d,
                         tm.vocab_size, self.pe.shape[0], s), "skv_embed")
@@ -218,7 +224,8 @@ class TransformerModel:
             kc, vc = layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr()
             # q, k, v = LN1(x) . [Wq Wk Wv] (LayerNorm folded into the projection)
             chk(L.skv_linear(qkv, x, lw["wqkv_t"].data_ptr(), None, None, lw["g1"].data_ptr(),
-                             lw["be1"].data_ptr(), 1e-5, B, 3 * d, d, 0, d, s), "skv_linear")
+                             lw["be1"].data_ptr(), 1e-5, B, 3 * d, d, 0, d, lw_ws, lw_n, s),
+                "skv_linear")
             chk(L.skv_append(kc, vc, k_ptr, v_ptr, layer.lens.data_ptr(), B, H, D, T, cdt,
                              _lib.F32, s), "skv_append")
             chk(L.skv_decode_attn(attn, q_ptr, kc, vc, layer.lens.data_ptr(), B, H, H, D, T, scale,
@@ -226,15 +233,15 @@ class TransformerModel:
                                   _lib.F32, s), "skv_decode_attn")
             # x += attn . Wo
             chk(L.skv_linear(x, attn, lw["wo_t"].data_ptr(), None, x, None, None, 0.0, B, d, d, 0,
-                             0, s), "skv_linear")
+                             0, lw_ws, lw_n, s), "skv_linear")
             # ff = gelu(LN2(x) . W1 + b1); x += ff . W2 + b2
             chk(L.skv_linear(ff, x, lw["w1_t"].data_ptr(), lw["b1"].data_ptr(), None,
                              lw["g2"].data_ptr(), lw["be2"].data_ptr(), 1e-5, B, self.mlp_dim, d,
-                             1, 0, s), "skv_linear")
+                             1, 0, lw_ws, lw_n, s), "skv_linear")
             chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, None, None, 0.0,
-                             B, d, self.mlp_dim, 0, 0, s), "skv_linear")
+                             B, d, self.mlp_dim, 0, 0, lw_ws, lw_n, s), "skv_linear")
         chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, None, None,
-                         0.0, B, tm.vocab_size, d, 0, 0, s), "skv_linear")
+                         0.0, B, tm.vocab_size, d, 0, 0, lw_ws, lw_n, s), "skv_linear")
 
     # -- many steps ----------------------------------------------------------
 

@@ -45,7 +45,8 @@ def lib():
 
 @pytest.mark.parametrize("M,N,K", [(1, 256, 256), (5, 100, 260), (16, 768, 768),
                                    (17, 3072, 768), (64, 48, 3072), (100, 1024, 64),
-                                   (3, 50304, 768)])
+                                   (3, 50304, 768), (2, 80, 4100), (16, 768, 3072),
+                                   (1, 256, 1024)])
 @pytest.mark.parametrize("epi", ["plain", "bias_gelu", "bias_res", "split", "ln_gelu"])
 def test_linear_matches_numpy(gpu_ctx, M, N, K, epi):
     banner(f"linear M={M} N={N} K={K} {epi}")
@@ -82,23 +83,29 @@ def test_linear_matches_numpy(gpu_ctx, M, N, K, epi):
     xd, wtd = dev(x), dev(np.ascontiguousarray(w.T))
     L = _lib.lib()
     res0 = y.clone()
-    for rep in range(2):  # a second call gives the same bits
-        if rep:
+    # without a workspace: one kernel; with one: narrow shapes split K over
+    # more workgroups and finish in a reduce kernel
+    wsb = L.skv_linear_workspace_bytes(M, N, K)
+    ws = torch.full((max(wsb, 4) // 4,), float("nan"), device="cuda")  # stale partials
+    for use_ws in ([False, True] if wsb else [False]):
+        for rep in range(2):  # a second call gives the same bits
             y.copy_(res0)
-        rc = L.skv_linear(y.data_ptr(), xd.data_ptr(), wtd.data_ptr(),
-                          bias.data_ptr() if bias is not None else None,
-                          residual.data_ptr() if residual is not None else None,
-                          ln_g.data_ptr() if ln_g is not None else None,
-                          ln_b.data_ptr() if ln_b is not None else None, 1e-5,
-                          M, N, K, act or 0, split, _lib.stream_handle())
-        _lib.check(rc, "skv_linear")
-        got_rep = y.cpu().numpy()
-        if rep:
-            np.testing.assert_array_equal(got_rep, got)  # bitwise reproducible
-        got = got_rep
-    if split:  # [3][M][N/3] -> [M, N]
-        got = got.reshape(3, M, split).transpose(1, 0, 2).reshape(M, N)
-    assert rel_rows(got, want) < FP32_TOL
+            rc = L.skv_linear(y.data_ptr(), xd.data_ptr(), wtd.data_ptr(),
+                              bias.data_ptr() if bias is not None else None,
+                              residual.data_ptr() if residual is not None else None,
+                              ln_g.data_ptr() if ln_g is not None else None,
+                              ln_b.data_ptr() if ln_b is not None else None, 1e-5,
+                              M, N, K, act or 0, split, ws.data_ptr() if use_ws else None,
+                              wsb if use_ws else 0, _lib.stream_handle())
+            _lib.check(rc, "skv_linear")
+            got_rep = y.cpu().numpy()
+            if rep:
+                np.testing.assert_array_equal(got_rep, got)  # bitwise reproducible
+            got = got_rep
+        if split:  # [3][M][N/3] -> [M, N]
+            got = got.reshape(3, M, split).transpose(1, 0, 2).reshape(M, N)
+        print(f"use_ws={use_ws} rel_err={rel_rows(got, want):.3e}")
+        assert rel_rows(got, want) < FP32_TOL
 
 
 def test_layernorm_and_embed(gpu_ctx):
