@@ -17,10 +17,14 @@
 //    O^T += V^T P^T needs (accumulator slot r of rows 8kk..8kk+7 is slot j of
 //    k-block kk). Only V needs a transpose, done once per tile while staging
 //    it into LDS.
-//  * Workgroup = 4 wavefronts, 64 query rows each (2 blocks of 32), so every
-//    K/V operand read from LDS feeds two MFMAs. K/V tiles of 64 tokens are
-//    double buffered: the global loads of tile t+1 are in flight while tile t
-//    is computed. Grouped-query attention folds the G query heads of a kv
+//  * Workgroup = 8 wavefronts of 32 query rows (256 rows). A wavefront needs
+//    ~206 registers at D = 128, so two run on each SIMD and the softmax of
+//    one overlaps the MFMAs of the other. (With 4 wavefronts of 64 rows, each
+//    K/V operand fed two MFMAs, but ~460 registers were live and the
+//    compiler shuttled values between AGPRs and VGPRs on every tile: 11%
+//    slower, measured on MI355X.) K/V tiles of 64 tokens are double
+//    buffered: the global loads of tile t+1 are in flight while tile t is
+//    computed. Grouped-query attention folds the G query heads of a kv
 //    head into the rows (row = query * G + head), so K/V are read once per
 //    group.
 //  * Long prefixes are split into n_splits token ranges (split-K, so that
@@ -37,8 +41,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kWaves = 4;
-constexpr int kQB = 2;                      // 32-row query blocks per wavefront
+constexpr int kWaves = 8;
+constexpr int kQB = 1;                      // 32-row query blocks per wavefront
 constexpr int kBM = kWaves * kQB * 32;      // query rows per workgroup (256)
 constexpr int kBN = 64;                     // tokens per K/V tile
 constexpr int kXCD = 8;                     // XCDs of an MI355X
@@ -98,12 +102,9 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const uint16_t* p) {
 __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
 template <int D, int G>
-__global__ __launch_bounds__(256, 1) void k_prefill_mfma(PrefillArgs a) {
+__global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) {
   constexpr int KB = D / 16;  // k-blocks of the QK^T product
   constexpr int DB = D / 32;  // 32-row d blocks of O^T
-  constexpr int KCH = kBN * D / 8 / 256;  // 16-byte K chunks per thread per tile
-  constexpr int VJ = (kBN / 2) * (D / 8) / 256;  // V jobs (2 tokens x 8 d) per thread
-  static_assert(KCH >= 1 && VJ >= 1, "tile too small for 256 threads");
   __shared__ Smem<D> sm;
 
   // ---- which (sequence, kv head, split, query tile) this workgroup is ----
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256, 1) void k_prefill_mfma(PrefillArgs a) {
   int qrow[kQB];
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
-    const int r = row0 + wave * 64 + qb * 32 + lc;
+    const int r = row0 + (wave * kQB + qb) * 32 + lc;
     qrow[qb] = r;
     const bool ok = r < R;
     const int i = r / G, h = hk * G + r % G;
@@ -201,79 +202,89 @@ __global__ __launch_bounds__(256, 1) void k_prefill_mfma(PrefillArgs a) {
     const int t0 = s0 + it * kBN;
     SKV_DMA_TILE(t0 + kBN, st ^ 1);
 
-    // The tile is consumed as two 32-token halves, each S^T -> online
-    // softmax -> PV, which keeps the live score registers to 2 x 16.
+    // S^T for the whole 64-token tile first (two independent accumulator
+    // chains per query block), then one online-softmax update, then PV.
     const bool need_mask = (t0 + kBN > s1) || (t0 + kBN - 1 > P + first_q);
+    f32x16 sc[2][kQB];
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      // ---- S^T = K Q^T for 32 tokens x (2 x 32 queries) ----
-      f32x16 sc[kQB];
+    for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) sc[qb] = f32x16{};
+      for (int qb = 0; qb < kQB; ++qb) sc[tb][qb] = f32x16{};
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
         const bf16x8 ka =
             *reinterpret_cast<const bf16x8*>(&sm.k[st][swz<D>(tb * 32 + lc, kb * 2 + g)]);
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb)
-          sc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[qb][kb], sc[qb], 0, 0, 0);
+          sc[tb][qb] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[qb][kb], sc[tb][qb], 0, 0, 0);
       }
-      // Accumulator slot r holds token t0 + tb*32 + (r/4)*8 + 4g + r%4.
-      if (need_mask) {
+    // Accumulator slot r of half tb holds token t0 + tb*32 + (r/4)*8 + 4g + r%4.
+    if (need_mask) {
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
-          const int qpos = P + qrow[qb] / G;  // this lane's query position
+      for (int qb = 0; qb < kQB; ++qb) {
+        const int qpos = P + qrow[qb] / G;  // this lane's query position
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int t = t0 + tb * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
-            sc[qb][r] = (t >= s1 || t > qpos) ? -INFINITY : sc[qb][r];
+            sc[tb][qb][r] = (t >= s1 || t > qpos) ? -INFINITY : sc[tb][qb][r];
           }
-        }
       }
-      // ---- online softmax; P^T as operand B of the PV product ----
-      bf16x8 pf[kQB][2];
+    }
+    // ---- online softmax; P^T as operand B of the PV product ----
+    bf16x8 pf[kQB][4];  // [qb][tb * 2 + kk]
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) {
-        float tmax = sc[qb][0];
+    for (int qb = 0; qb < kQB; ++qb) {
+      float tmax = sc[0][qb][0];
 #pragma unroll
-        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, sc[qb][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        // Lazy rescaling: the running max m only moves when the block's max
-        // exceeds it by more than 8 (log2 units), so probabilities stay
-        // <= 2^8 (exact in fp32, in range for bf16) and O, l are rescaled
-        // on a few blocks instead of every one. O and l always refer to the
-        // same m.
-        const float tm = tmax * a.qscale;
-        const bool upd = tm > m[qb] + 8.f;  // also true on the first finite block
-        if (__ballot(upd) != 0ull) {        // wave-uniform branch
-          const float alpha = upd ? fast_exp2(m[qb] - tm) : 1.f;  // m = -inf: 0
-          if (upd) m[qb] = tm;
-          l[qb] *= alpha;
+      for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-          for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
-        }
-        const float m_use = m[qb] == -INFINITY ? 0.f : m[qb];  // fully masked so far
-        float ls = 0.f;
+        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[tb][qb][r]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      // Lazy rescaling: the running max m only moves when the tile's max
+      // exceeds it by more than 8 (log2 units), so probabilities stay
+      // <= 2^8 (exact in fp32, in range for bf16) and O, l are rescaled
+      // on a few tiles instead of every one. O and l always refer to the
+      // same m.
+      const float tm = tmax * a.qscale;
+      const bool upd = tm > m[qb] + 8.f;  // also true on the first finite tile
+      if (__ballot(upd) != 0ull) {        // wave-uniform branch
+        const float alpha = upd ? fast_exp2(m[qb] - tm) : 1.f;  // m = -inf: 0
+        if (upd) m[qb] = tm;
+        l[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
+      }
+      const float m_use = m[qb] == -INFINITY ? 0.f : m[qb];  // fully masked so far
+      float ls = 0.f;
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const float p = fast_exp2(fmaf(sc[qb][kk * 8 + j], a.qscale, -m_use));
+            const float p = fast_exp2(fmaf(sc[tb][qb][kk * 8 + j], a.qscale, -m_use));
             ls += p;
-            pf[qb][kk][j] = (__bf16)p;
+            pf[qb][tb * 2 + kk][j] = (__bf16)p;
           }
-        l[qb] += ls;
-      }
-      // ---- O^T += V^T P^T ----
-      // Operand A of k-block kk needs, in lane (d = db*32 + lc, g), slot j =
-      // V[tb*32 + 16kk + 4g + j][d] for j < 4 and V[... + 8 + 4g + j - 4][d]
-      // for j >= 4 (the token order of pf). ds_read_b64_tr_b16 gives lane i
-      // of a 16-lane group the element i%4 of the 8 bytes addressed by lane
-      // 4j + i/4 as its slot j, so lane L of group gr addresses token
-      // T + 4g + L/4, elements d0 + 4(L%4) .. +3 with d0 = db*32 + (gr%2)*16.
-      {
-        const int gr = lane >> 4, L = lane & 15;
-        const int dq = (gr & 1) * 16 + 4 * (L & 3);  // d offset within the 32-row block
+      l[qb] += ls;
+    }
+    // ---- O^T += V^T P^T ----
+    // Operand A of k-block kk needs, in lane (d = db*32 + lc, g), slot j =
+    // V[tb*32 + 16kk + 4g + j][d] for j < 4 and V[... + 8 + 4g + j - 4][d]
+    // for j >= 4 (the token order of pf). ds_read_b64_tr_b16 gives lane i
+    // of a 16-lane group the element i%4 of the 8 bytes addressed by lane
+    // 4j + i/4 as its slot j, so lane L of group gr addresses token
+    // T + 4g + L/4, elements d0 + 4(L%4) .. +3 with d0 = db*32 + (gr%2)*16.
+    {
+      const int gr = lane >> 4, L = lane & 15;
+      const int dq = (gr & 1) * 16 + 4 * (L & 3);  // d offset within the 32-row block
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const int d = db * 32 + dq;
@@ -289,11 +300,10 @@ __global__ __launch_bounds__(256, 1) void k_prefill_mfma(PrefillArgs a) {
                 bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb)
-              o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[qb][kk], o[qb][db], 0,
-                                                                   0, 0);
+              o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[qb][tb * 2 + kk],
+                                                                   o[qb][db], 0, 0, 0);
           }
         }
-      }
     }
 
     // the next tile's DMA has landed in LDS before anyone reads it
@@ -465,7 +475,8 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
   hipStream_t s = (hipStream_t)stream;
 #define SKV_PF(DD, GG)                                                                        \
   if (D == DD && G == GG)                                                                     \
-    hipLaunchKernelGGL((k_prefill_mfma<DD, GG>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((k_prefill_mfma<DD, GG>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, \
+                       s, a);
   SKV_PF(64, 1) SKV_PF(64, 2) SKV_PF(64, 4) SKV_PF(64, 8)
   SKV_PF(128, 1) SKV_PF(128, 2) SKV_PF(128, 4) SKV_PF(128, 8)
 #undef SKV_PF
