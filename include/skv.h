@@ -221,6 +221,31 @@ size_t skv_argmax_workspace_bytes(int M, int N);
 int skv_argmax(int32_t* out, const float* x, int M, int N, void* ws, size_t ws_bytes,
                skv_stream_t stream);
 
+/*
+ * Next token of each row drawn from its logits, as sample_token
+ * (simple-llm/src/jax_backend.py:413-515) filters them:
+ *  - repetition_penalty divides, once per distinct token, the logits of the
+ *    tokens in seq[m, max(0, L - repetition_window) : L], L = lens[m];
+ *  - temperature == 0: out[m] = first index of the maximum (greedy);
+ *  - else p = softmax(logits / temperature); then, when enabled, min_p
+ *    (p < min_p * max p -> 0), top_k (the top_k largest; of equal
+ *    probabilities the larger index ranks higher) and top_p (the longest
+ *    prefix of the descending order whose sum stays <= top_p, at least one
+ *    entry), renormalising after each filter;
+ *  - out[m] = the first index, in index order, where the running sum of p
+ *    exceeds u * sum(p), u = splitmix64(seed, m, L) in [0, 1). The
+ *    reference's jax.random stream is not reproduced; a call is bitwise
+ *    reproducible for the same inputs.
+ * logits [M, V] fp32 (not modified), V <= 65536; seq [M, seq_stride] int32;
+ * probs_out (may be NULL): [M, V] fp32, the filtered distribution the draw
+ * used (one-hot for greedy). Disabled filters: top_k = 0, top_p >= 1,
+ * min_p = 0, repetition_penalty = 1.
+ */
+int skv_sample(int32_t* out, float* probs_out, const float* logits, const int32_t* seq,
+               int seq_stride, const int32_t* lens, int M, int V, float temperature, int top_k,
+               float top_p, float min_p, float repetition_penalty, int repetition_window,
+               unsigned long long seed, skv_stream_t stream);
+
 /* Next input token of each sequence (generate.py:29-69 with a cache):
  * ids[b] = prompt[b, pos[b]] while pos[b] < prompt_len[b], else
  * argmax_prev[b]; the token is also stored at seq[b, pos[b]] when

@@ -14,7 +14,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(HERE, "libskv.so")
 
-SOURCES = ["skv_api.hip", "append.hip", "decode_attn.hip", "prefill_attn.hip", "model_ops.hip"]
+SOURCES = ["skv_api.hip", "append.hip", "decode_attn.hip", "prefill_attn.hip", "model_ops.hip",
+           "sample.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -273,7 +273,10 @@ class Generator:
     """
 
     def __init__(self, model: TransformerModel, prompts: Sequence[Sequence[int]],
-                 total_len: Sequence[int] | int, use_graph: bool = False):
+                 total_len: Sequence[int] | int, use_graph: bool = False,
+                 temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
+                 min_p: float = 0.0, repetition_penalty: float = 1.0,
+                 repetition_window: int = 64, seed: int = 42):
         tm = model.tm_params
         self.model = model
         B = len(prompts)
@@ -305,6 +308,16 @@ class Generator:
         self.steps = int(tot.max()) - 1  # position p's step produces token p + 1
         self.use_graph = use_graph
         self.graph = None
+        if temperature < 0 or top_k < 0 or min_p < 0 or repetition_penalty <= 0 \
+                or repetition_window < 0:
+            raise ValueError("bad sampling parameters")
+        if tm.vocab_size > 65536 and (temperature != 0.0 or repetition_penalty != 1.0):
+            raise ValueError("device sampling supports vocab_size <= 65536")
+        self.sampling = (float(temperature), int(top_k), float(top_p), float(min_p),
+                         float(repetition_penalty), int(repetition_window))
+        self.seed = int(seed) & ((1 << 64) - 1)
+        # greedy without a penalty takes the multi-workgroup argmax
+        self.greedy = temperature == 0.0 and repetition_penalty == 1.0
 
     def reset(self) -> None:
         """Rewind to before the first step (empty cache, no tokens), keeping
@@ -322,9 +335,20 @@ class Generator:
                                      c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
                                      self.seq.shape[1], s), "skv_next_tokens")
         m._launch_step(c, bf)
-        _lib.check(L.skv_argmax(bf.argmax.data_ptr(), bf.logits.data_ptr(), self.B,
-                                m.tm_params.vocab_size, bf.arg_ws.data_ptr(), bf.arg_ws.numel(),
-                                s), "skv_argmax")
+        if self.greedy:
+            _lib.check(L.skv_argmax(bf.argmax.data_ptr(), bf.logits.data_ptr(), self.B,
+                                    m.tm_params.vocab_size, bf.arg_ws.data_ptr(),
+                                    bf.arg_ws.numel(), s), "skv_argmax")
+        else:
+            # sample_token (jax_backend.py:413-515) over the sequence's tokens so
+            # far (seq[b, :lens[b]], the prompt included); the draw is keyed by
+            # (seed, sequence, position)
+            T, k, p, mp, pen, win = self.sampling
+            _lib.check(L.skv_sample(bf.argmax.data_ptr(), None, bf.logits.data_ptr(),
+                                    self.seq.data_ptr(), self.seq.shape[1],
+                                    c.layers[0].lens.data_ptr(), self.B,
+                                    m.tm_params.vocab_size, T, k, p, mp, pen, win, self.seed,
+                                    s), "skv_sample")
 
     def run(self) -> List[List[int]]:
         """Run all steps; returns every sequence's tokens (prompt + output)."""
@@ -361,27 +385,28 @@ class Generator:
 
 def generate_text(model: TransformerModel, prompt_tokens, max_tokens=100, temperature=1.0,
                   top_k=0, top_p=1.0, min_p=0.0, repetition_penalty=1.0, repetition_window=64,
-                  use_graph: bool = True):
+                  use_graph: bool = True, seed: int = 42):
     """Generate max_tokens tokens after prompt_tokens (generate.py:8-71's
-    signature); returns prompt + generated tokens as a list of ints.
-
-    Greedy only: temperature must be 0 (and the other filters at their
-    neutral values); anything else raises ValueError. The prompt plus the
-    output must fit in context_size."""
-    if temperature != 0.0:
-        raise ValueError("only greedy decoding (temperature=0) runs on the device; "
-                         "sampling with temperature/top-k/top-p/min-p is not built")
-    if repetition_penalty != 1.0:
-        raise ValueError("repetition_penalty is not supported by the device decoder")
+    signature and defaults); returns prompt + generated tokens as a list of
+    ints. temperature = 0 is greedy; otherwise each token is drawn on the
+    device from sample_token's filtered distribution (jax_backend.py:413-515)
+    with a uniform keyed by (seed, position) -- the reference's jax.random
+    stream itself is not reproduced. The prompt plus the output must fit in
+    context_size (the cache does not slide)."""
     prompt = [int(t) for t in prompt_tokens]
     if max_tokens <= 0:
         return prompt
-    g = Generator(model, [prompt], len(prompt) + int(max_tokens), use_graph=use_graph)
+    g = Generator(model, [prompt], len(prompt) + int(max_tokens), use_graph=use_graph,
+                  temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p,
+                  repetition_penalty=repetition_penalty, repetition_window=repetition_window,
+                  seed=seed)
     return g.run()[0]
 
 
 def generate_batch(model: TransformerModel, prompts: Sequence[Sequence[int]], total_len,
-                   use_graph: bool = True) -> List[List[int]]:
-    """Greedy generation of a ragged batch until each sequence holds
-    total_len tokens (an int or one per sequence)."""
-    return Generator(model, prompts, total_len, use_graph=use_graph).run()
+                   use_graph: bool = True, **sampling) -> List[List[int]]:
+    """Generation of a ragged batch until each sequence holds total_len
+    tokens (an int or one per sequence); greedy unless sampling parameters
+    (temperature, top_k, top_p, min_p, repetition_penalty, repetition_window,
+    seed) are given."""
+    return Generator(model, prompts, total_len, use_graph=use_graph, **sampling).run()

@@ -97,6 +97,24 @@ def test_entry_points_reject_bad_arguments():
     assert L.skv_advance(None, None, 1, 2, 128, None) == _lib.SKV_E_INVALID
 
 
+def test_sample_rejects_bad_arguments():
+    L = _lib.lib()
+    fake = 4096  # never dereferenced: each call below fails validation first
+    args = [fake, None, fake, fake, 8, fake, 2, 100, 1.0, 0, 1.0, 0.0, 1.0, 64, 42, None]
+
+    def call(**kw):
+        a = list(args)
+        for k, v in kw.items():
+            a[{"V": 7, "T": 8, "top_k": 9, "pen": 12, "M": 6}[k]] = v
+        return L.skv_sample(*a)
+
+    assert call(V=70000) == _lib.SKV_E_UNSUPPORTED
+    assert call(T=-1.0) == _lib.SKV_E_INVALID
+    assert call(top_k=-3) == _lib.SKV_E_INVALID
+    assert call(pen=0.0) == _lib.SKV_E_INVALID
+    assert call(M=0) == _lib.SKV_E_INVALID
+
+
 def test_check_maps_status_to_exceptions():
     L = _lib.lib()
     L.skv_append(None, None, None, None, None, 1, 1, 64, 1, 0, 0, None)

@@ -261,9 +261,45 @@ def test_generate_rejects_unsupported(gpu_ctx):
     banner("generate argument checks")
     from simple_llm_amd import model as M
     m, _ = make_model(gpu_ctx, 61, 128, 2, 1, 32)
-    with pytest.raises(ValueError, match="greedy"):
-        M.generate_text(m, [1, 2], 5, temperature=1.0)
+    with pytest.raises(ValueError, match="sampling parameters"):
+        M.generate_text(m, [1, 2], 5, temperature=-1.0)
     with pytest.raises(ValueError, match="context_size"):
         M.generate_text(m, [1, 2], 40, temperature=0.0)
     with pytest.raises(ValueError, match="vocabulary"):
         M.generate_text(m, [1, 99], 4, temperature=0.0)
+
+
+def test_sampled_generate_matches_oracle_draws(gpu_ctx):
+    """generate_text with temperature / top-k / top-p / min-p / repetition
+    penalty: every token is the oracle's draw (sample_token's filtered
+    distribution over the teacher-forced float64 logits, u keyed by the
+    position) until a legitimate fp32 divergence (a near-boundary draw)."""
+    banner("sampled generate vs oracle draws")
+    from oracle import sample_oracle as so
+    from simple_llm_amd import model as M
+    m, params = make_model(gpu_ctx, 97, 128, 2, 2, 96, seed=8, std=0.3)
+    prompt = [3, 14, 15, 92, 65, 35]
+    kw = dict(temperature=0.8, top_k=20, top_p=0.9, min_p=0.01, repetition_penalty=1.3,
+              repetition_window=16)
+    out = M.generate_text(m, prompt, max_tokens=60, use_graph=True, seed=99, **kw)
+    again = M.generate_text(m, prompt, max_tokens=60, use_graph=False, seed=99, **kw)
+    assert out == again and out[:len(prompt)] == prompt and len(out) == 66
+    # the seed matters where the distribution is not one-hot after the filters
+    hot = [M.generate_text(m, prompt, max_tokens=60, use_graph=True, seed=sd, temperature=2.0)
+           for sd in (99, 100)]
+    assert hot[0] != hot[1]
+    full = mo.forward(params, np.array([out]), 2)[0]
+    checked = 0
+    for pos in range(len(prompt) - 1, len(out) - 1):
+        L = pos + 1  # tokens so far
+        recent = out[max(0, L - 16):L]
+        probs = so.sample_filter(full[pos], 0.8, 20, 0.9, 0.01, 1.3, recent)
+        u = so.splitmix_uniform(99, 0, L)
+        c = np.cumsum(probs)
+        want = so.sample_draw(probs, u)
+        if out[L] != want:
+            # only a draw within float rounding of a step may differ
+            assert np.abs(c - u * c[-1]).min() < 1e-4, (pos, out[L], want)
+            break
+        checked += 1
+    assert checked >= 20
