@@ -254,6 +254,26 @@ int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                     const int32_t* prompt, const int32_t* prompt_len, const int32_t* pos, int B,
                     int max_prompt, int seq_cap, skv_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Byte-level BPE tokenizer (host code, no device work), replacing the
+ * reference's C tokenizer (simple-llm/src/common/bpe_tokenizer.c) that
+ * common/bpe_tokenizer.py runs as a subprocess.
+ * ------------------------------------------------------------------------ */
+
+/* Training (bpe_tokenizer.c:155-243): merges of the corpus bytes, as
+ * (p1, p2, new_id) triples in order, new_id = 256 + i; at most
+ * min(vocab_size, 50000) - 256 merges, fewer if the pairs run out. Ties take
+ * the first pair of the reference's hash-table order. merges holds
+ * max_merges triples (>= vocab_size - 256). */
+int skv_bpe_train(const uint8_t* corpus, size_t n, int vocab_size, int32_t* merges,
+                  int max_merges, int* n_merges);
+
+/* Encoding (bpe_tokenizer.c:246-355): one pass; a pair of raw bytes that is
+ * a merge becomes the first such merge's id, any other byte stays. ids holds
+ * n entries; *n_ids gets the count. */
+int skv_bpe_encode(const uint8_t* text, size_t n, const int32_t* merges, int n_merges,
+                   int32_t* ids, size_t* n_ids);
+
 #ifdef __cplusplus
 }
 #endif
