@@ -14,7 +14,10 @@ through all layers as HIP kernels of libskv.so: embedding + position,
 fused q/k/v projection (the LayerNorm before it folded into its reads), the
 cache append (skv_append), decode attention (skv_decode_attn), output
 projection with residual, MLP (LayerNorm folded in, GELU, residual), tied
-logits and argmax. PyTorch only owns the memory.
+logits and the next token: skv_argmax when greedy (temperature 0, the
+reference's jnp.argmax branch, jax_backend.py:466-469), otherwise skv_sample
+(repetition penalty, temperature, min-p, top-k, top-p, then a draw).
+PyTorch only owns the memory.
 
 Differences from the reference's generate_text, both documented choices:
   * tokens attend their cached prefix at their absolute positions; the
@@ -22,8 +25,9 @@ Differences from the reference's generate_text, both documented choices:
     shifts positions while the window is not full (its tokens are therefore
     not a parity target; parity is checked on the logits of the final
     sequence, teacher forced);
-  * sampling is greedy (temperature 0, the reference's jnp.argmax branch,
-    jax_backend.py:466-469); other sampling settings raise ValueError.
+  * the draw's uniform comes from splitmix64 of (seed, row, position), so a
+    captured step replays deterministically; the reference's jax.random
+    stream is not reproduced, only its filtered distribution.
 """
 from __future__ import annotations
 

@@ -303,3 +303,18 @@ def test_sampled_generate_matches_oracle_draws(gpu_ctx):
             break
         checked += 1
     assert checked >= 20
+
+
+def test_model_loaded_from_checkpoint_dir(gpu_ctx, tmp_path):
+    """A model directory written by checkpoint.save_model loads through
+    checkpoint.load_model (the reference's load_model arguments) into a model
+    whose logits are bit-identical to the one built from the same weights."""
+    banner("model from model.flax.zst")
+    from simple_llm_amd import checkpoint
+    m, params = make_model(gpu_ctx, 97, 128, 2, 2, 48, seed=5, std=0.1)
+    checkpoint.save_model(m, str(tmp_path))
+    m2 = checkpoint.load_model(None, 0, str(tmp_path), ctx=gpu_ctx)
+    toks = np.random.default_rng(6).integers(0, 97, (2, 30))
+    got, want = m2.forward(toks), m.forward(toks)
+    assert np.array_equal(got, want)
+    assert rel_rows(got, mo.forward(params, toks, 2)) < FP32_TOL
