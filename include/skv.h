@@ -255,6 +255,32 @@ int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                     int max_prompt, int seq_cap, skv_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Training-side attention: causal FlashAttention backward (fp32).
+ * ------------------------------------------------------------------------ */
+
+/* Bytes of workspace skv_flash_bwd needs: the row deltas, B*N*H floats. */
+size_t skv_flash_bwd_workspace_bytes(int B, int N, int H);
+
+/*
+ * Gradients of causal attention, replacing flash_attention_backward and its
+ * reduce pass (simple-llm/src/gpu/gpu_pass_backward.py:445-580, kernels
+ * create_flash_attention_backward_kernel and _reduce_kernel,
+ * simple-llm/src/gpu/gpu_kernels.py:2038-2455). Per batch b and head h, with
+ * S = scale * Q K^T over keys <= query:
+ *   P = exp(S - M) / L, Dl = rowsum(dO * O), dS = P * (dO V^T - Dl),
+ *   dq = scale * dS K, dk = scale * dS^T Q, dv = P^T dO.
+ * q, k, v, o, dout, dq, dk, dv: [B, N, H, D] fp32 (the reference's
+ * [B*N, H*D] buffers), 16-byte aligned; L, M: [B, N, H] fp32, the forward's
+ * softmax sums and row maxima of the scaled scores (the reference's L and M
+ * buffers). The outputs must not overlap the inputs. D in {16, 32, 64, 128};
+ * B*H <= 65535. Products run on v_mfma_f32_32x32x2_f32 (fp32); no atomics,
+ * so results are bitwise reproducible.
+ */
+int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, const float* k, const float* v,
+                  const float* o, const float* L, const float* M, const float* dout, int B, int N,
+                  int H, int D, float scale, void* ws, size_t ws_bytes, skv_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Byte-level BPE tokenizer (host code, no device work), replacing the
  * reference's C tokenizer (simple-llm/src/common/bpe_tokenizer.c) that
  * common/bpe_tokenizer.py runs as a subprocess.

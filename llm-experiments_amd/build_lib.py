@@ -15,7 +15,7 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(HERE, "libskv.so")
 
 SOURCES = ["skv_api.hip", "append.hip", "decode_attn.hip", "prefill_attn.hip", "model_ops.hip",
-           "sample.hip", "bpe_tokenizer.cpp"]
+           "sample.hip", "flash_bwd.hip", "bpe_tokenizer.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

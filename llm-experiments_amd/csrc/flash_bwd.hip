@@ -1,0 +1,413 @@
+// Causal FlashAttention backward on gfx950: fp32 in and out, on
+// v_mfma_f32_32x32x2_f32 (fp32 products, fp32 accumulation).
+//
+// Reference: simple-llm/src/gpu/gpu_kernels.py:2038-2455 (stage 1, one pass
+// per Q block writing partial dK/dV into a workspace; stage 2, their sum) and
+// the dispatcher gpu/gpu_pass_backward.py:445-580. Per (batch b, head h), with
+// S = scale * Q K^T, masked to key <= query:
+//   P  = exp(S - M) / L          M, L: the forward's row statistics
+//   Dl = rowsum(dO * O)          O: the forward's output
+//   dP = dO V^T,  dS = P * (dP - Dl)
+//   dQ = scale * dS K,  dK = scale * dS^T Q,  dV = P^T dO
+//
+// Design: two kernels, no atomics and every sum in a fixed order, so a call
+// is bitwise reproducible:
+//   k_fbwd_dq   one workgroup per (128 queries, b, h). Per 32-key piece:
+//               S^T = K Q^T and dP^T = V dO^T, then dQ^T += K^T dS^T. It
+//               also writes Dl for the second kernel.
+//   k_fbwd_dkv  one workgroup per (128 keys, b, h). Per 32-query piece:
+//               S = Q K^T and dP = dO V^T, then dV += P^T dO, dK += dS^T Q.
+// Each of the 4 waves owns 32 rows. Its row operands (Q and dO, or K and V)
+// stay in registers for the whole call; the other side is staged through LDS
+// 64 rows at a time, the next rows' global loads issued before the current
+// ones are used. Work past the causal diagonal is skipped per wave.
+//
+// v_mfma_f32_32x32x2_f32 lane layout (lane l, c = l % 32, hf = l / 32):
+//   A (32 x 2): A[c][hf]   B (2 x 32): B[hf][c]
+//   C (32 x 32), register r: row 8*(r/4) + 4*hf + r%4, column c.
+// The k index of a product is free to permute as long as A and B agree:
+// step (g, t) of a D-long dot product takes d = 8g + 4hf + t in half hf, so
+// each lane reads 4 consecutive d with one 16-byte load per 4 steps. A
+// C-layout tile is then directly the A or B operand of the next product,
+// k-step (q, t) taking row 8q + 4hf + t.
+#include "skv_common.h"
+
+namespace skv {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRows = 32 * kWaves;  // rows (queries or keys) of one workgroup
+constexpr int kCols = 64;           // rows of the other side staged per step
+
+struct FbwdArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* o;
+  const float* dout;
+  const float* L;
+  const float* M;
+  float* dq;
+  float* dk;
+  float* dv;
+  float* delta;  // [B, N, H] row deltas Dl, written by k_fbwd_dq
+  int N, H, n_blocks;
+  float scale, sl2;  // scale and scale * log2(e)
+};
+
+__device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Element offset of row n of head h in batch b of a [B, N, H, D] tensor.
+template <int D>
+__device__ __forceinline__ size_t row_off(int b, int n, int N, int H, int h) {
+  return ((size_t)(b * N + n) * H + h) * D;
+}
+
+// 64 rows x D of two tensors, global -> registers -> LDS (row stride D + 4
+// floats: 16-byte aligned rows, and 16-byte reads of 16 consecutive rows hit
+// distinct banks). Rows at or beyond N load as zeros.
+template <int D>
+struct Stage {
+  static constexpr int SP = D + 4;
+  static constexpr int C4 = D / 4;                  // float4 per row
+  static constexpr int NV = kCols * C4 / kThreads;  // float4 per thread per tensor
+  static_assert(NV >= 1 && kCols * C4 % kThreads == 0, "staging shape");
+  f32x4 r0[NV], r1[NV];
+
+  __device__ __forceinline__ void load(const float* t0, const float* t1, int row0, int b, int N,
+                                       int H, int h) {
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int e = threadIdx.x + kThreads * u;
+      const int n = row0 + e / C4;
+      const bool ok = n < N;
+      const size_t off = row_off<D>(b, ok ? n : N - 1, N, H, h) + 4 * (e % C4);
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(t0 + off);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(t1 + off);
+      r0[u] = ok ? x0 : zero4();
+      r1[u] = ok ? x1 : zero4();
+    }
+  }
+  __device__ __forceinline__ void store(float* s0, float* s1) const {
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int e = threadIdx.x + kThreads * u;
+      const int at = (e / C4) * SP + 4 * (e % C4);
+      *reinterpret_cast<f32x4*>(s0 + at) = r0[u];
+      *reinterpret_cast<f32x4*>(s1 + at) = r1[u];
+    }
+  }
+};
+
+// dQ and the row deltas. Grid (n_blocks, B * H); blocks with the most keys
+// (the last queries) are launched first.
+template <int D>
+__global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
+  constexpr int G = D / 8;             // 16-byte pairs of a row fragment
+  constexpr int DT = (D + 31) / 32;    // 32-row tiles of dQ^T
+  constexpr int SP = Stage<D>::SP;
+  __shared__ __attribute__((aligned(16))) float sK[kCols * SP];
+  __shared__ __attribute__((aligned(16))) float sV[kCols * SP];
+
+  const int H = a.H, N = a.N;
+  const int b = blockIdx.y / H, h = blockIdx.y % H;
+  const int blk = a.n_blocks - 1 - (int)blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 31, hf = lane >> 5;
+  const int qrow = blk * kRows + wave * 32 + c;
+  const bool qok = qrow < N;
+  const int qr = qok ? qrow : N - 1;
+  const size_t qoff = row_off<D>(b, qr, N, H, h);
+
+  // this lane's query: Q and dO fragments (d = 8g + 4hf + t), and Dl
+  f32x4 qf[G], df[G];
+  float dl = 0.f;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int d0 = 8 * g + 4 * hf;
+    const f32x4 xq = *reinterpret_cast<const f32x4*>(a.q + qoff + d0);
+    const f32x4 xd = *reinterpret_cast<const f32x4*>(a.dout + qoff + d0);
+    const f32x4 xo = *reinterpret_cast<const f32x4*>(a.o + qoff + d0);
+    qf[g] = qok ? xq : zero4();
+    df[g] = qok ? xd : zero4();
+    const f32x4 od = qok ? xo : zero4();
+    dl += df[g].x * od.x + df[g].y * od.y + df[g].z * od.z + df[g].w * od.w;
+  }
+  dl += __shfl_xor(dl, 32);
+  const size_t srow = (size_t)(b * N + qr) * H + h;
+  if (qok && hf == 0) a.delta[srow] = dl;
+  const float m2 = qok ? a.M[srow] * LOG2E : 0.f;
+  const float il = qok ? 1.f / a.L[srow] : 0.f;  // 0 zeroes every P of an absent row
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+
+  const int q_last = min(blk * kRows + kRows, N) - 1;            // the workgroup's last query
+  // the wave's last query (-1: the wave has none)
+  const int wq_last = blk * kRows + wave * 32 < N ? min(blk * kRows + wave * 32 + 31, N - 1) : -1;
+  const int steps = q_last / kCols + 1;
+  Stage<D> st;
+  st.load(a.k, a.v, 0, b, N, H, h);
+  for (int j = 0; j < steps; ++j) {
+    __syncthreads();
+    st.store(sK, sV);
+    __syncthreads();
+    if (j + 1 < steps) st.load(a.k, a.v, (j + 1) * kCols, b, N, H, h);
+#pragma unroll
+    for (int sub = 0; sub < kCols / 32; ++sub) {
+      const int key0 = j * kCols + sub * 32;
+      if (key0 > wq_last) break;  // wave-uniform: every later key is masked for this wave
+      f32x16 s = f32x16{}, dp = f32x16{};
+      const float* kr = sK + (sub * 32 + c) * SP + 4 * hf;
+      const float* vr = sV + (sub * 32 + c) * SP + 4 * hf;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const f32x4 ka = *reinterpret_cast<const f32x4*>(kr + 8 * g);
+        const f32x4 va = *reinterpret_cast<const f32x4*>(vr + 8 * g);
+        s = mfma(ka.x, qf[g].x, s);
+        dp = mfma(va.x, df[g].x, dp);
+        s = mfma(ka.y, qf[g].y, s);
+        dp = mfma(va.y, df[g].y, dp);
+        s = mfma(ka.z, qf[g].z, s);
+        dp = mfma(va.z, df[g].z, dp);
+        s = mfma(ka.w, qf[g].w, s);
+        dp = mfma(va.w, df[g].w, dp);
+      }
+      // s[r], dp[r]: key key0 + 8(r/4) + 4hf + r%4, query qrow
+      f32x16 ds;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + 8 * (r / 4) + 4 * hf + (r % 4);
+        const float p = key <= qrow ? exp2f(s[r] * a.sl2 - m2) * il : 0.f;
+        ds[r] = p * (dp[r] - dl);
+      }
+      // dQ^T[d][query] += sum_key K[key][d] dS^T[key][query]
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int dcol = dt * 32 + c;
+        const bool dok = (D % 32 == 0) || dcol < D;
+        const float* kc = sK + (sub * 32 + 4 * hf) * SP + (dok ? dcol : D - 1);
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float kv = kc[(8 * qq + t) * SP];
+            acc[dt] = mfma(dok ? kv : 0.f, ds[4 * qq + t], acc[dt]);
+          }
+        }
+      }
+    }
+  }
+  // acc[dt][r]: d = dt*32 + 8(r/4) + 4hf + r%4 of this lane's query
+  if (qok) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = dt * 32 + 8 * qq + 4 * hf;
+        if (d0 < D) {
+          const f32x4 y = {acc[dt][4 * qq] * a.scale, acc[dt][4 * qq + 1] * a.scale,
+                           acc[dt][4 * qq + 2] * a.scale, acc[dt][4 * qq + 3] * a.scale};
+          *reinterpret_cast<f32x4*>(a.dq + qoff + d0) = y;
+        }
+      }
+    }
+  }
+}
+
+// dK and dV. Grid (n_blocks, B * H); block 0 (the most queries) first.
+template <int D>
+__global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
+  constexpr int G = D / 8;
+  constexpr int DT = (D + 31) / 32;
+  constexpr int SP = Stage<D>::SP;
+  __shared__ __attribute__((aligned(16))) float sQ[kCols * SP];
+  __shared__ __attribute__((aligned(16))) float sD[kCols * SP];  // dO
+  __shared__ float sM2[kCols], sIL[kCols], sDL[kCols];
+
+  const int H = a.H, N = a.N;
+  const int b = blockIdx.y / H, h = blockIdx.y % H;
+  const int blk = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 31, hf = lane >> 5;
+  const int wk0 = blk * kRows + wave * 32;  // the wave's first key
+  const int krow = wk0 + c;
+  const bool kok = krow < N;
+  const size_t koff = row_off<D>(b, kok ? krow : N - 1, N, H, h);
+
+  f32x4 kf[G], vf[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int d0 = 8 * g + 4 * hf;
+    const f32x4 xk = *reinterpret_cast<const f32x4*>(a.k + koff + d0);
+    const f32x4 xv = *reinterpret_cast<const f32x4*>(a.v + koff + d0);
+    kf[g] = kok ? xk : zero4();
+    vf[g] = kok ? xv : zero4();
+  }
+  f32x16 dva[DT], dka[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    dva[dt] = f32x16{};
+    dka[dt] = f32x16{};
+  }
+
+  const int j0 = (blk * kRows) / kCols;  // first step holding a query >= the block's first key
+  const int steps = (N + kCols - 1) / kCols;
+  Stage<D> st;
+  float m2 = 0.f, il = 0.f, dl = 0.f;
+  auto load_stats = [&](int j) {
+    if (threadIdx.x < kCols) {
+      const int n = j * kCols + threadIdx.x;
+      const bool ok = n < N;
+      const size_t sr = (size_t)(b * N + (ok ? n : N - 1)) * H + h;
+      const float mm = a.M[sr], ll = a.L[sr], dd = a.delta[sr];
+      m2 = ok ? mm * LOG2E : 0.f;
+      il = ok ? 1.f / ll : 0.f;
+      dl = ok ? dd : 0.f;
+    }
+  };
+  if (j0 < steps) {
+    st.load(a.q, a.dout, j0 * kCols, b, N, H, h);
+    load_stats(j0);
+  }
+  for (int j = j0; j < steps; ++j) {
+    __syncthreads();
+    st.store(sQ, sD);
+    if (threadIdx.x < kCols) {
+      sM2[threadIdx.x] = m2;
+      sIL[threadIdx.x] = il;
+      sDL[threadIdx.x] = dl;
+    }
+    __syncthreads();
+    if (j + 1 < steps) {
+      st.load(a.q, a.dout, (j + 1) * kCols, b, N, H, h);
+      load_stats(j + 1);
+    }
+#pragma unroll
+    for (int sub = 0; sub < kCols / 32; ++sub) {
+      const int q0 = j * kCols + sub * 32;
+      // wave-uniform: every query precedes the wave's keys, or the wave has no key
+      if (q0 + 31 < wk0 || wk0 >= N) continue;
+      f32x16 s = f32x16{}, dp = f32x16{};
+      const float* qr = sQ + (sub * 32 + c) * SP + 4 * hf;
+      const float* dr = sD + (sub * 32 + c) * SP + 4 * hf;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const f32x4 qa = *reinterpret_cast<const f32x4*>(qr + 8 * g);
+        const f32x4 da = *reinterpret_cast<const f32x4*>(dr + 8 * g);
+        s = mfma(qa.x, kf[g].x, s);
+        dp = mfma(da.x, vf[g].x, dp);
+        s = mfma(qa.y, kf[g].y, s);
+        dp = mfma(da.y, vf[g].y, dp);
+        s = mfma(qa.z, kf[g].z, s);
+        dp = mfma(da.z, vf[g].z, dp);
+        s = mfma(qa.w, kf[g].w, s);
+        dp = mfma(da.w, vf[g].w, dp);
+      }
+      // s[r], dp[r]: query q0 + 8(r/4) + 4hf + r%4, key krow
+      f32x16 p, ds;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ql = sub * 32 + 8 * (r / 4) + 4 * hf + (r % 4);
+        const float pr = krow <= j * kCols + ql ? exp2f(s[r] * a.sl2 - sM2[ql]) * sIL[ql] : 0.f;
+        p[r] = pr;
+        ds[r] = pr * (dp[r] - sDL[ql]);
+      }
+      // dV[key][d] += sum_query P^T[key][query] dO[query][d]; dK likewise with dS and Q
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int dcol = dt * 32 + c;
+        const bool dok = (D % 32 == 0) || dcol < D;
+        const int at = (sub * 32 + 4 * hf) * SP + (dok ? dcol : D - 1);
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float xo = sD[at + (8 * qq + t) * SP];
+            const float xq = sQ[at + (8 * qq + t) * SP];
+            dva[dt] = mfma(p[4 * qq + t], dok ? xo : 0.f, dva[dt]);
+            dka[dt] = mfma(ds[4 * qq + t], dok ? xq : 0.f, dka[dt]);
+          }
+        }
+      }
+    }
+  }
+  // dva[dt][r], dka[dt][r]: key wk0 + 8(r/4) + 4hf + r%4, d = dt*32 + c
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const int d = dt * 32 + c;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = wk0 + 8 * (r / 4) + 4 * hf + (r % 4);
+      if (key < N && ((D % 32 == 0) || d < D)) {
+        const size_t off = row_off<D>(b, key, N, H, h) + d;
+        a.dk[off] = dka[dt][r] * a.scale;
+        a.dv[off] = dva[dt][r];
+      }
+    }
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+}  // namespace skv
+
+using namespace skv;
+
+extern "C" size_t skv_flash_bwd_workspace_bytes(int B, int N, int H) {
+  if (B <= 0 || N <= 0 || H <= 0) return 0;
+  return (size_t)B * N * H * sizeof(float);
+}
+
+extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, const float* k,
+                             const float* v, const float* o, const float* L, const float* M,
+                             const float* dout, int B, int N, int H, int D, float scale, void* ws,
+                             size_t ws_bytes, skv_stream_t stream) {
+  const char* fn = "skv_flash_bwd";
+  SKV_REQUIRE(dq && dk && dv && q && k && v && o && L && M && dout, SKV_E_INVALID,
+              "%s: null pointer argument", fn);
+  SKV_REQUIRE(B > 0 && N > 0 && H > 0 && D > 0, SKV_E_INVALID,
+              "%s: dims must be > 0 (B=%d N=%d H=%d D=%d)", fn, B, N, H, D);
+  SKV_REQUIRE(D == 16 || D == 32 || D == 64 || D == 128, SKV_E_UNSUPPORTED,
+              "%s: head_dim %d (supported: 16, 32, 64, 128)", fn, D);
+  SKV_REQUIRE(scale > 0.f, SKV_E_INVALID, "%s: scale must be > 0", fn);
+  SKV_REQUIRE(aligned16(dq) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) &&
+                  aligned16(dout),
+              SKV_E_INVALID, "%s: q, k, v, o, dout and dq must be 16-byte aligned", fn);
+  SKV_REQUIRE((long)B * H <= 65535, SKV_E_UNSUPPORTED, "%s: B*H=%ld above 65535", fn,
+              (long)B * H);
+  SKV_REQUIRE((long)B * N * H * D < (1L << 40), SKV_E_UNSUPPORTED, "%s: tensors too large", fn);
+  const size_t need = skv_flash_bwd_workspace_bytes(B, N, H);
+  SKV_REQUIRE(ws && ws_bytes >= need && aligned16(ws), SKV_E_WORKSPACE,
+              "%s: workspace %zu bytes < %zu required (16-byte aligned)", fn, ws_bytes, need);
+  FbwdArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.L = L; a.M = M;
+  a.dq = dq; a.dk = dk; a.dv = dv;
+  a.delta = static_cast<float*>(ws);
+  a.N = N; a.H = H;
+  a.n_blocks = (N + kRows - 1) / kRows;
+  a.scale = scale;
+  a.sl2 = scale * LOG2E;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)a.n_blocks, (unsigned)(B * H));
+#define SKV_FB(DD)                                                                 \
+  if (D == DD) {                                                                   \
+    hipLaunchKernelGGL((k_fbwd_dq<DD>), grid, dim3(kThreads), 0, s, a);            \
+    int rc = check_launch(fn);                                                     \
+    if (rc) return rc;                                                             \
+    hipLaunchKernelGGL((k_fbwd_dkv<DD>), grid, dim3(kThreads), 0, s, a);           \
+  }
+  SKV_FB(16) SKV_FB(32) SKV_FB(64) SKV_FB(128)
+#undef SKV_FB
+  return check_launch(fn);
+}

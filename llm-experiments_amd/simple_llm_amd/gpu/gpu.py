@@ -25,6 +25,7 @@ from .gpu_kv_cache import (
     kv_cache_set_block_table,
     kv_cache_update,
 )
+from .gpu_pass_backward import flash_attention_backward
 from .gpu_ops import batch_begin, batch_commit, validate_buffer_shape_1d, validate_buffer_shape_2d
 from .gpu_types import (
     BatchState,
@@ -78,4 +79,6 @@ __all__ = [
     "kv_cache_set_block_table",
     "decode_attention",
     "decode_plan",
+    # Training-side attention
+    "flash_attention_backward",
 ]

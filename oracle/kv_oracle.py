@@ -14,6 +14,9 @@ Reference (s-i-e-v-e/llm-experiments, paths relative to simple-llm/src/):
   * causal flash attention:   gpu/gpu_kernels.py:631-768 (mask kv_pos <= q_pos,
     online softmax, O / max(l, 1e-8), L = l, M = m) and the test's closed form
     gpu_test.py:776-810
+  * flash attention backward: gpu/gpu_kernels.py:2038-2455 (P from the saved
+    L and M, D = rowsum(dO * O), dS = P * (dP - D), dQ = scale dS K,
+    dK = scale dS^T Q, dV = P^T dO; partials per Q block, then summed)
 
 How each function is pinned (tests/test_oracle.py):
   cache_offset / append      closed-form offsets over every element of small
@@ -29,6 +32,11 @@ How each function is pinned (tests/test_oracle.py):
   flash_attention            the seed-42 golden fixture (7 reference configs);
                              its L and M statistics by direct sums
   paged_gather               contiguous equality against direct scatter
+  flash_attention_backward   the seed-42 golden fixture of the reference's
+                             backward test (torch float64 autograd); central
+                             finite differences of sum(O * dO); the
+                             reference's stage-1/stage-2 split (per-Q-block
+                             partials summed) restated by loops
 """
 from __future__ import annotations
 
@@ -229,3 +237,40 @@ def flash_attention(Q: np.ndarray, K: np.ndarray, V: np.ndarray, batch_size: int
     v = np.asarray(V, dtype=np.float64).reshape(B, T, H, D)
     o, m, l = prefill_attention(q, k, v, np.zeros(B, dtype=np.int64), None, None, True)
     return o.reshape(B * T, H * D), l.reshape(-1), m.reshape(-1)
+
+
+def flash_attention_backward(Q, K, V, O, L, M, dO, batch_size: int, seq_len: int, n_heads: int,
+                             head_dim: int):
+    """Reference flash_attention_backward contract on [B*T, H*D] buffers (float64).
+
+    Follows the stage-1 kernel (gpu/gpu_kernels.py:2161-2340): P is rebuilt
+    from the forward's statistics, P = exp(scale * q.k - M) / L for
+    key <= query and 0 otherwise; D = rowsum(dO * O) uses the given O;
+    dP = dO V^T; dS = P * (dP - D); dQ = scale * dS K; the partial
+    dK = scale * dS^T Q and dV = P^T dO of each Q block are summed by stage 2
+    (:2378-2455), which is the plain sum over all queries.
+    Returns dQ, dK, dV as [B*T, H*D] float64.
+    """
+    B, T, H, D = batch_size, seq_len, n_heads, head_dim
+    scale = 1.0 / np.sqrt(D)
+
+    def heads(x):
+        return np.asarray(x, dtype=np.float64).reshape(B, T, H, D).transpose(0, 2, 1, 3)
+
+    q, k, v, o, do = heads(Q), heads(K), heads(V), heads(O), heads(dO)
+    m = np.asarray(M, dtype=np.float64).reshape(B, T, H).transpose(0, 2, 1)[..., None]
+    l = np.asarray(L, dtype=np.float64).reshape(B, T, H).transpose(0, 2, 1)[..., None]
+    mask = np.tril(np.ones((T, T), dtype=bool))
+    s = np.einsum("bhqd,bhkd->bhqk", q, k) * scale
+    p = np.where(mask, np.exp(np.where(mask, s, 0.0) - m) / l, 0.0)
+    dlt = (do * o).sum(-1, keepdims=True)
+    dp = np.einsum("bhqd,bhkd->bhqk", do, v)
+    ds = p * (dp - dlt)
+    dq = np.einsum("bhqk,bhkd->bhqd", ds, k) * scale
+    dk = np.einsum("bhqk,bhqd->bhkd", ds, q) * scale
+    dv = np.einsum("bhqk,bhqd->bhkd", p, do)
+
+    def flat(x):
+        return x.transpose(0, 2, 1, 3).reshape(B * T, H * D)
+
+    return flat(dq), flat(dk), flat(dv)

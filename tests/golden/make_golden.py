@@ -13,6 +13,13 @@ a library routine independent of oracle/.
                         (test_flash_attention: causal, seed 42 per config).
                         The "Medium" config (8, 32, 8, 64) is left out to keep
                         the file small; tests regenerate it from the seed.
+  flash_bwd_kat_seed42.npz
+                        simple-llm/src/gpu_test.py:871-1060
+                        (test_flash_attention_backward: Q, K, V, grad_out
+                        drawn in that order after seed 42; expected
+                        gradients by torch float64 autograd of the test's
+                        causal attention with its -1e10 mask, in place of
+                        jax.vjp; O, L, M of the forward stored alongside)
 
 Usage: python tests/golden/make_golden.py
 """
@@ -37,6 +44,8 @@ FLASH_CONFIGS = [
     (2, 64, 2, 32, "Large: 64seq x 32d"),
 ]
 FLASH_STORED = [0, 1, 2, 3, 5, 6]
+# (batch, seq_len, n_heads, head_dim, description), gpu_test.py:874-877
+FLASH_BWD_CONFIGS = [(2, 8, 2, 16, "Small"), (4, 16, 4, 32, "Medium")]
 
 
 def kv_kat_inputs():
@@ -82,6 +91,41 @@ def flash_expected(Q, K, V, batch, seq_len, n_heads, head_dim):
     return o, l.transpose(0, 2, 1).reshape(-1), m.transpose(0, 2, 1).reshape(-1)
 
 
+def flash_bwd_inputs(batch, seq_len, n_heads, head_dim):
+    """Q, K, V, grad_out of test_flash_attention_backward ([B, T, H*D] fp32)."""
+    np.random.seed(42)
+    return tuple(np.random.randn(batch, seq_len, n_heads * head_dim).astype(np.float32)
+                 for _ in range(4))
+
+
+def flash_bwd_expected(Q, K, V, dO, batch, seq_len, n_heads, head_dim):
+    """dQ, dK, dV [B*T, H*D] float64: torch autograd of gpu_test.py:899-915."""
+    def heads(x):
+        return torch.tensor(x, dtype=torch.float64).reshape(
+            batch, seq_len, n_heads, head_dim).transpose(1, 2).requires_grad_(True)
+    q, k, v = heads(Q), heads(K), heads(V)
+    s = (q @ k.transpose(-1, -2)) / np.sqrt(float(head_dim))
+    mask = torch.tril(torch.ones(seq_len, seq_len, dtype=torch.bool))
+    s = torch.where(mask, s, torch.tensor(-1e10, dtype=torch.float64))
+    o = torch.softmax(s, -1) @ v
+    g = torch.tensor(dO, dtype=torch.float64).reshape(batch, seq_len, n_heads,
+                                                      head_dim).transpose(1, 2)
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), g)
+    return tuple(x.transpose(1, 2).reshape(batch * seq_len, -1).numpy() for x in (dq, dk, dv))
+
+
+def write_flash_bwd():
+    out = {}
+    for i, (b, t, h, d, _) in enumerate(FLASH_BWD_CONFIGS):
+        Q, K, V, dO = flash_bwd_inputs(b, t, h, d)
+        o, l, m = flash_expected(Q, K, V, b, t, h, d)
+        dq, dk, dv = flash_bwd_expected(Q, K, V, dO, b, t, h, d)
+        out.update({f"o_{i}": o, f"l_{i}": l, f"m_{i}": m, f"dq_{i}": dq, f"dk_{i}": dk,
+                    f"dv_{i}": dv})
+    out["configs"] = np.array([c[:4] for c in FLASH_BWD_CONFIGS])
+    np.savez_compressed(os.path.join(HERE, "flash_bwd_kat_seed42.npz"), **out)
+
+
 def main():
     k_steps, v_steps, q = kv_kat_inputs()
     # cache holds the 5 steps in order; attention over all of them
@@ -101,6 +145,7 @@ def main():
     out["configs"] = np.array([c[:4] for c in FLASH_CONFIGS])
     out["stored"] = np.array(FLASH_STORED)
     np.savez_compressed(os.path.join(HERE, "flash_kat_seed42.npz"), **out)
+    write_flash_bwd()
     print("wrote", sorted(os.listdir(HERE)))
 
 

@@ -115,6 +115,28 @@ def test_sample_rejects_bad_arguments():
     assert call(M=0) == _lib.SKV_E_INVALID
 
 
+def test_flash_bwd_rejects_bad_arguments():
+    L = _lib.lib()
+    fake = 4096  # never dereferenced: each call below fails validation first
+    B, N, H = 2, 100, 3
+    need = L.skv_flash_bwd_workspace_bytes(B, N, H)
+    assert need == B * N * H * 4 and L.skv_flash_bwd_workspace_bytes(0, N, H) == 0
+
+    def call(D=64, ws_bytes=None, ptr=fake, scale=0.125, n=N):
+        return L.skv_flash_bwd(ptr, fake, fake, fake, fake, fake, fake, fake, fake, fake, B, n,
+                               H, D, scale, fake, need - 4 if ws_bytes is None else ws_bytes,
+                               None)
+
+    assert call() == _lib.SKV_E_WORKSPACE
+    assert call(D=48, ws_bytes=need) == _lib.SKV_E_UNSUPPORTED
+    assert call(D=256, ws_bytes=need) == _lib.SKV_E_UNSUPPORTED
+    assert call(ptr=None, ws_bytes=need) == _lib.SKV_E_INVALID
+    assert call(ptr=fake + 4, ws_bytes=need) == _lib.SKV_E_INVALID  # not 16-byte aligned
+    assert call(scale=0.0, ws_bytes=need) == _lib.SKV_E_INVALID
+    assert call(n=0, ws_bytes=need) == _lib.SKV_E_INVALID
+    assert "workspace" in (call() and _lib.lib().skv_last_error().decode())
+
+
 def test_check_maps_status_to_exceptions():
     L = _lib.lib()
     L.skv_append(None, None, None, None, None, 1, 1, 64, 1, 0, 0, None)
