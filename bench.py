@@ -55,10 +55,10 @@ B, H, D, T_CAP, FILL = 4, 16, 128, 32768, 32000
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["c4", "c1", "c2", "c3", "c5"], default="c4",
+    p.add_argument("--workload", choices=["c4", "c1", "c2", "c3", "c5", "fb"], default="c4",
                    help="BASELINE config: c4 (default, the headline line), c1 tiny LM "
                         "generate, c2 fp32 KV microbench, c3 GPT-2-small ragged batch, "
-                        "c5 GQA paged ragged decode")
+                        "c5 GQA paged ragged decode; fb: flash-attention backward (fp32)")
     p.add_argument("--steps", type=int, default=256)
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -532,6 +532,98 @@ def run_c2(args, ctx):
         roof, cpu)
 
 
+MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+
+
+def run_fb(args, ctx):
+    """Training-side attention: one causal FlashAttention backward (skv_flash_bwd,
+    fp32) per step at B=8, N=2048, H=16, D=64, the attention shape of the
+    reference's largest power-of-two head_dim anchor (hyper.py:74: d_model 1024,
+    16 heads, context 2048), 8 sequences. O, L, M come from a torch fp32
+    forward of the same random q, k, v, computed before timing."""
+    import numpy as np
+    import torch
+
+    from simple_llm_amd import _lib
+
+    B_, N, H_, Dh = 8, 2048, 16, 64
+    dev = ctx.device
+    g = torch.Generator(device=dev).manual_seed(3)
+    q, k, v, do = (torch.randn(B_ * N, H_ * Dh, generator=g, device=dev) for _ in range(4))
+    sc = 1.0 / float(np.sqrt(Dh))
+    with torch.no_grad():
+        o, Ls, Ms = (torch.empty_like(q), torch.empty(B_ * N * H_, device=dev),
+                     torch.empty(B_ * N * H_, device=dev))
+        mask = torch.ones(N, N, dtype=torch.bool, device=dev).tril()
+        for b in range(B_):
+            qb, kb, vb = (x[b * N:(b + 1) * N].view(N, H_, Dh).transpose(0, 1).contiguous()
+                          for x in (q, k, v))
+            s_ = (qb @ kb.transpose(-1, -2).contiguous() * sc).masked_fill(~mask, float("-inf"))
+            m_ = s_.amax(-1, keepdim=True)
+            e_ = torch.exp(s_ - m_)
+            l_ = e_.sum(-1, keepdim=True)
+            o[b * N:(b + 1) * N] = ((e_ / l_) @ vb).transpose(0, 1).reshape(N, H_ * Dh)
+            Ls.view(B_, N, H_)[b] = l_.squeeze(-1).transpose(0, 1)
+            Ms.view(B_, N, H_)[b] = m_.squeeze(-1).transpose(0, 1)
+    L = _lib.lib()
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    ws = torch.empty(L.skv_flash_bwd_workspace_bytes(B_, N, H_), dtype=torch.uint8, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def call():
+        rc = L.skv_flash_bwd(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), q.data_ptr(),
+                             k.data_ptr(), v.data_ptr(), o.data_ptr(), Ls.data_ptr(),
+                             Ms.data_ptr(), do.data_ptr(), B_, N, H_, Dh, sc, ws.data_ptr(),
+                             ws.numel(), stream)
+        _lib.check(rc, "skv_flash_bwd")
+
+    for _ in range(args.warmup):
+        call()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record()
+        call()
+        e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    call_s = float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e-3
+    # five causal products of 2*D flops per (query, key <= query) pair:
+    # S = QK^T, dP = dO V^T, dV = P^T dO, dK = dS^T Q, dQ = dS K
+    flops = 10.0 * Dh * (N * (N + 1) / 2) * B_ * H_
+    roof = {"bound": "mfma", "achieved": flops / call_s / 1e12, "peak": MFMA_FP32_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": flops / call_s / 1e12 / MFMA_FP32_PEAK_TFLOPS,
+            "traffic": None, "kernel": "skv_flash_bwd (k_fbwd_dq + k_fbwd_dkv), HIP events",
+            "mean_call_us": call_s * 1e6, "algorithmic_flops": flops}
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the reference's CPU path differentiates attention with JAX autodiff; the
+        # same backward in torch CPU fp32 autograd, one (sequence, head) at a time
+        qc, kc, vc, doc = (x.view(B_, N, H_, Dh).cpu() for x in (q, k, v, do))
+        maskc = torch.ones(N, N, dtype=torch.bool).tril()
+        n, t0 = 0, time.perf_counter()
+        while n == 0 or time.perf_counter() - t0 < args.cpu_seconds:
+            b, h = divmod(n % (B_ * H_), H_)
+            qh, kh, vh = (x[b, :, h].clone().requires_grad_(True) for x in (qc, kc, vc))
+            s_ = (qh @ kh.T * sc).masked_fill(~maskc, float("-inf"))
+            oh = torch.softmax(s_, -1) @ vh
+            torch.autograd.grad(oh, (qh, kh, vh), doc[b, :, h])
+            n += 1
+        dt = time.perf_counter() - t0
+        cpu = {"value": n * N / H_ / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"{n} (sequence, head) backward passes of N=2048, D=64 in torch CPU "
+                         f"fp32 autograd, {dt:.1f} s; tokens/s = passes * N / H / time"}
+    return _record(
+        "attention backward tokens/sec", B_ * N * args.steps / wall, "tokens/s", args.steps,
+        args.warmup, wall / args.steps * 1e3, "fp32",
+        {"workload": "FB causal flash-attention backward fp32: B=8, N=2048, H=16, D=64 "
+                     "(O, L, M from a torch fp32 forward)", "batch": B_},
+        roof, cpu)
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -548,7 +640,8 @@ def main():
 
         ctx = gpu.context_create()
         ctx.config.decode_chunk_tokens = args.chunk_tokens
-        rec = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c5": run_c5}[args.workload](args, ctx)
+        rec = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c5": run_c5,
+               "fb": run_fb}[args.workload](args, ctx)
         print(json.dumps(rec), flush=True)
         return
     if FILL + args.steps > T_CAP or args.steps < 1 or args.warmup < 0:

@@ -272,9 +272,9 @@ size_t skv_flash_bwd_workspace_bytes(int B, int N, int H);
  * q, k, v, o, dout, dq, dk, dv: [B, N, H, D] fp32 (the reference's
  * [B*N, H*D] buffers), 16-byte aligned; L, M: [B, N, H] fp32, the forward's
  * softmax sums and row maxima of the scaled scores (the reference's L and M
- * buffers). The outputs must not overlap the inputs. D in {16, 32, 64, 128};
- * B*H <= 65535. Products run on v_mfma_f32_32x32x2_f32 (fp32); no atomics,
- * so results are bitwise reproducible.
+ * buffers). The outputs must not overlap the inputs. D in {16, 32, 64, 128}.
+ * Products run on v_mfma_f32_32x32x2_f32 (fp32); no atomics, so results are
+ * bitwise reproducible.
  */
 int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, const float* k, const float* v,
                   const float* o, const float* L, const float* M, const float* dout, int B, int N,

@@ -34,20 +34,44 @@ def hipcc() -> str:
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", CSRC, "-I", INCLUDE, *srcs, "-o", tmp]
+# Extra flags per source. The flash backward keeps its MFMA accumulators in
+# ordinary VGPRs (gfx950 MFMAs take either register file); the default
+# heuristic put them in AGPRs and copied them back and forth every step.
+SOURCE_FLAGS = {"flash_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+_NOISE = "is not a recognized feature for this target"  # hipcc's host pass on -packed-fp32-ops
+
+
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass warns that it does not know the packed-fp32 feature
-    noise = "is not a recognized feature for this target"
-    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if noise not in ln]
+    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if _NOISE not in ln]
     if res.returncode != 0:
         raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
     if verbose and msgs:
         print("\n".join(msgs))
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles every source to an object (in parallel, each with its own
+    extra flags), then links libskv.so."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="skv_build_") as tmpdir:
+        jobs = []
+        for src in SOURCES:
+            obj = os.path.join(tmpdir, src + ".o")
+            jobs.append((obj, [hipcc(), *flags, *SOURCE_FLAGS.get(src, []), "-I", CSRC, "-I",
+                               INCLUDE, "-c", os.path.join(CSRC, src), "-o", obj]))
+        with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 4, 8)) as pool:
+            for f in [pool.submit(_run, cmd, verbose) for _, cmd in jobs]:
+                f.result()
+        tmp = LIB + ".tmp"
+        _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *[o for o, _ in jobs], "-o",
+              tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -55,7 +55,7 @@ struct FbwdArgs {
   float* dk;
   float* dv;
   float* delta;  // [B, N, H] row deltas Dl, written by k_fbwd_dq
-  int N, H, n_blocks;
+  int N, H, BH, n_blocks;
   float scale, sl2;  // scale and scale * log2(e)
 };
 
@@ -63,7 +63,9 @@ __device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+// 2^x on v_exp_f32 (results below 2^-126 flush toward 0, which no
+// probability here needs).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Element offset of row n of head h in batch b of a [B, N, H, D] tensor.
 template <int D>
@@ -73,7 +75,9 @@ __device__ __forceinline__ size_t row_off(int b, int n, int N, int H, int h) {
 
 // 64 rows x D of two tensors, global -> registers -> LDS (row stride D + 4
 // floats: 16-byte aligned rows, and 16-byte reads of 16 consecutive rows hit
-// distinct banks). Rows at or beyond N load as zeros.
+// distinct banks). Rows at or beyond N repeat row N - 1: every product that
+// involves them is masked out by a select, never by a multiply, so their
+// values cannot leak (and no load sits behind a branch).
 template <int D>
 struct Stage {
   static constexpr int SP = D + 4;
@@ -88,12 +92,9 @@ struct Stage {
     for (int u = 0; u < NV; ++u) {
       const int e = threadIdx.x + kThreads * u;
       const int n = row0 + e / C4;
-      const bool ok = n < N;
-      const size_t off = row_off<D>(b, ok ? n : N - 1, N, H, h) + 4 * (e % C4);
-      const f32x4 x0 = *reinterpret_cast<const f32x4*>(t0 + off);
-      const f32x4 x1 = *reinterpret_cast<const f32x4*>(t1 + off);
-      r0[u] = ok ? x0 : zero4();
-      r1[u] = ok ? x1 : zero4();
+      const size_t off = row_off<D>(b, min(n, N - 1), N, H, h) + 4 * (e % C4);
+      r0[u] = *reinterpret_cast<const f32x4*>(t0 + off);
+      r1[u] = *reinterpret_cast<const f32x4*>(t1 + off);
     }
   }
   __device__ __forceinline__ void store(float* s0, float* s1) const {
@@ -107,8 +108,13 @@ struct Stage {
   }
 };
 
-// dQ and the row deltas. Grid (n_blocks, B * H); blocks with the most keys
-// (the last queries) are launched first.
+// Workgroup w takes (b, h) = w % (B*H) and row block rank w / (B*H): all
+// (b, h) of one rank run before the next rank, ranks in order of decreasing
+// work, so the hardware's round-robin of workgroups over the 8 XCDs gives
+// every XCD the same causal load, and the blocks of one (b, h) share the L2
+// of one XCD (w % 8 = (b*H + h) % 8 when B*H is a multiple of 8).
+
+// dQ and the row deltas; rank 0 = the last query block (the most keys).
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   constexpr int G = D / 8;             // 16-byte pairs of a row fragment
@@ -118,8 +124,9 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   __shared__ __attribute__((aligned(16))) float sV[kCols * SP];
 
   const int H = a.H, N = a.N;
-  const int b = blockIdx.y / H, h = blockIdx.y % H;
-  const int blk = a.n_blocks - 1 - (int)blockIdx.x;
+  const int bh = (int)(blockIdx.x % (unsigned)a.BH), rank = (int)(blockIdx.x / (unsigned)a.BH);
+  const int b = bh / H, h = bh % H;
+  const int blk = a.n_blocks - 1 - rank;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 31, hf = lane >> 5;
   const int qrow = blk * kRows + wave * 32 + c;
@@ -127,25 +134,24 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   const int qr = qok ? qrow : N - 1;
   const size_t qoff = row_off<D>(b, qr, N, H, h);
 
-  // this lane's query: Q and dO fragments (d = 8g + 4hf + t), and Dl
+  // this lane's query: Q and dO fragments (d = 8g + 4hf + t), and Dl. A lane
+  // past N works on row N - 1 and masks all of its keys (qlim = -1).
   f32x4 qf[G], df[G];
   float dl = 0.f;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int d0 = 8 * g + 4 * hf;
-    const f32x4 xq = *reinterpret_cast<const f32x4*>(a.q + qoff + d0);
-    const f32x4 xd = *reinterpret_cast<const f32x4*>(a.dout + qoff + d0);
-    const f32x4 xo = *reinterpret_cast<const f32x4*>(a.o + qoff + d0);
-    qf[g] = qok ? xq : zero4();
-    df[g] = qok ? xd : zero4();
-    const f32x4 od = qok ? xo : zero4();
+    qf[g] = *reinterpret_cast<const f32x4*>(a.q + qoff + d0);
+    df[g] = *reinterpret_cast<const f32x4*>(a.dout + qoff + d0);
+    const f32x4 od = *reinterpret_cast<const f32x4*>(a.o + qoff + d0);
     dl += df[g].x * od.x + df[g].y * od.y + df[g].z * od.z + df[g].w * od.w;
   }
   dl += __shfl_xor(dl, 32);
   const size_t srow = (size_t)(b * N + qr) * H + h;
   if (qok && hf == 0) a.delta[srow] = dl;
-  const float m2 = qok ? a.M[srow] * LOG2E : 0.f;
-  const float il = qok ? 1.f / a.L[srow] : 0.f;  // 0 zeroes every P of an absent row
+  const float m2 = a.M[srow] * LOG2E;
+  const float il = 1.f / a.L[srow];
+  const int qlim = qok ? qrow : -1;  // keys <= qlim are unmasked
 
   f32x16 acc[DT];
 #pragma unroll
@@ -187,7 +193,8 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = key0 + 8 * (r / 4) + 4 * hf + (r % 4);
-        const float p = key <= qrow ? exp2f(s[r] * a.sl2 - m2) * il : 0.f;
+        const float e = fast_exp2(s[r] * a.sl2 - m2) * il;
+        const float p = key <= qlim ? e : 0.f;
         ds[r] = p * (dp[r] - dl);
       }
       // dQ^T[d][query] += sum_key K[key][d] dS^T[key][query]
@@ -224,7 +231,7 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   }
 }
 
-// dK and dV. Grid (n_blocks, B * H); block 0 (the most queries) first.
+// dK and dV; rank 0 = key block 0 (the most queries).
 template <int D>
 __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
   constexpr int G = D / 8;
@@ -232,26 +239,26 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
   constexpr int SP = Stage<D>::SP;
   __shared__ __attribute__((aligned(16))) float sQ[kCols * SP];
   __shared__ __attribute__((aligned(16))) float sD[kCols * SP];  // dO
-  __shared__ float sM2[kCols], sIL[kCols], sDL[kCols];
+  __shared__ __attribute__((aligned(16))) float sM2[kCols];
+  __shared__ __attribute__((aligned(16))) float sIL[kCols];
+  __shared__ __attribute__((aligned(16))) float sDL[kCols];
 
   const int H = a.H, N = a.N;
-  const int b = blockIdx.y / H, h = blockIdx.y % H;
-  const int blk = blockIdx.x;
+  const int bh = (int)(blockIdx.x % (unsigned)a.BH), rank = (int)(blockIdx.x / (unsigned)a.BH);
+  const int b = bh / H, h = bh % H;
+  const int blk = rank;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 31, hf = lane >> 5;
   const int wk0 = blk * kRows + wave * 32;  // the wave's first key
-  const int krow = wk0 + c;
-  const bool kok = krow < N;
-  const size_t koff = row_off<D>(b, kok ? krow : N - 1, N, H, h);
+  const int krow = wk0 + c;  // a key past N is masked for every query (query < N <= krow)
+  const size_t koff = row_off<D>(b, min(krow, N - 1), N, H, h);
 
   f32x4 kf[G], vf[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int d0 = 8 * g + 4 * hf;
-    const f32x4 xk = *reinterpret_cast<const f32x4*>(a.k + koff + d0);
-    const f32x4 xv = *reinterpret_cast<const f32x4*>(a.v + koff + d0);
-    kf[g] = kok ? xk : zero4();
-    vf[g] = kok ? xv : zero4();
+    kf[g] = *reinterpret_cast<const f32x4*>(a.k + koff + d0);
+    vf[g] = *reinterpret_cast<const f32x4*>(a.v + koff + d0);
   }
   f32x16 dva[DT], dka[DT];
 #pragma unroll
@@ -263,21 +270,19 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
   const int j0 = (blk * kRows) / kCols;  // first step holding a query >= the block's first key
   const int steps = (N + kCols - 1) / kCols;
   Stage<D> st;
+  // statistics of query j * kCols + threadIdx.x (threads < kCols), clamped
   float m2 = 0.f, il = 0.f, dl = 0.f;
-  auto load_stats = [&](int j) {
-    if (threadIdx.x < kCols) {
-      const int n = j * kCols + threadIdx.x;
-      const bool ok = n < N;
-      const size_t sr = (size_t)(b * N + (ok ? n : N - 1)) * H + h;
-      const float mm = a.M[sr], ll = a.L[sr], dd = a.delta[sr];
-      m2 = ok ? mm * LOG2E : 0.f;
-      il = ok ? 1.f / ll : 0.f;
-      dl = ok ? dd : 0.f;
-    }
-  };
+#define SKV_FB_STATS(J)                                                          \
+  if (threadIdx.x < kCols) {                                                     \
+    const int n_ = min((J) * kCols + (int)threadIdx.x, N - 1);                   \
+    const size_t sr_ = (size_t)(b * N + n_) * H + h;                             \
+    m2 = a.M[sr_] * LOG2E;                                                       \
+    il = 1.f / a.L[sr_];                                                         \
+    dl = a.delta[sr_];                                                           \
+  }
   if (j0 < steps) {
     st.load(a.q, a.dout, j0 * kCols, b, N, H, h);
-    load_stats(j0);
+    SKV_FB_STATS(j0)
   }
   for (int j = j0; j < steps; ++j) {
     __syncthreads();
@@ -290,7 +295,7 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
     __syncthreads();
     if (j + 1 < steps) {
       st.load(a.q, a.dout, (j + 1) * kCols, b, N, H, h);
-      load_stats(j + 1);
+      SKV_FB_STATS(j + 1)
     }
 #pragma unroll
     for (int sub = 0; sub < kCols / 32; ++sub) {
@@ -316,11 +321,19 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
       // s[r], dp[r]: query q0 + 8(r/4) + 4hf + r%4, key krow
       f32x16 p, ds;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ql = sub * 32 + 8 * (r / 4) + 4 * hf + (r % 4);
-        const float pr = krow <= j * kCols + ql ? exp2f(s[r] * a.sl2 - sM2[ql]) * sIL[ql] : 0.f;
-        p[r] = pr;
-        ds[r] = pr * (dp[r] - sDL[ql]);
+      for (int qq = 0; qq < 4; ++qq) {
+        const int ql = sub * 32 + 8 * qq + 4 * hf;
+        const f32x4 m4 = *reinterpret_cast<const f32x4*>(sM2 + ql);
+        const f32x4 i4 = *reinterpret_cast<const f32x4*>(sIL + ql);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(sDL + ql);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int r = 4 * qq + t, query = j * kCols + ql + t;
+          const float e = fast_exp2(s[r] * a.sl2 - m4[t]) * i4[t];
+          const float pr = (krow <= query && query < N) ? e : 0.f;
+          p[r] = pr;
+          ds[r] = pr * (dp[r] - d4[t]);
+        }
       }
       // dV[key][d] += sum_query P^T[key][query] dO[query][d]; dK likewise with dS and Q
 #pragma unroll
@@ -341,6 +354,7 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
       }
     }
   }
+#undef SKV_FB_STATS
   // dva[dt][r], dka[dt][r]: key wk0 + 8(r/4) + 4hf + r%4, d = dt*32 + c
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
@@ -384,8 +398,6 @@ extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, co
   SKV_REQUIRE(aligned16(dq) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) &&
                   aligned16(dout),
               SKV_E_INVALID, "%s: q, k, v, o, dout and dq must be 16-byte aligned", fn);
-  SKV_REQUIRE((long)B * H <= 65535, SKV_E_UNSUPPORTED, "%s: B*H=%ld above 65535", fn,
-              (long)B * H);
   SKV_REQUIRE((long)B * N * H * D < (1L << 40), SKV_E_UNSUPPORTED, "%s: tensors too large", fn);
   const size_t need = skv_flash_bwd_workspace_bytes(B, N, H);
   SKV_REQUIRE(ws && ws_bytes >= need && aligned16(ws), SKV_E_WORKSPACE,
@@ -399,7 +411,9 @@ extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, co
   a.scale = scale;
   a.sl2 = scale * LOG2E;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)a.n_blocks, (unsigned)(B * H));
+  a.BH = B * H;
+  SKV_REQUIRE((long)a.n_blocks * a.BH < (1L << 31), SKV_E_UNSUPPORTED, "%s: grid too large", fn);
+  const dim3 grid((unsigned)(a.n_blocks * a.BH));
 #define SKV_FB(DD)                                                                 \
   if (D == DD) {                                                                   \
     hipLaunchKernelGGL((k_fbwd_dq<DD>), grid, dim3(kThreads), 0, s, a);            \
