@@ -539,8 +539,8 @@ def run_fb(args, ctx):
     """Training-side attention: one causal FlashAttention backward (skv_flash_bwd,
     fp32) per step at B=8, N=2048, H=16, D=64, the attention shape of the
     reference's largest power-of-two head_dim anchor (hyper.py:74: d_model 1024,
-    16 heads, context 2048), 8 sequences. O, L, M come from a torch fp32
-    forward of the same random q, k, v, computed before timing."""
+    16 heads, context 2048), 8 sequences. O, L, M come from skv_flash_fwd on
+    the same random q, k, v, which is timed on its own as `forward`."""
     import numpy as np
     import torch
 
@@ -551,24 +551,33 @@ def run_fb(args, ctx):
     g = torch.Generator(device=dev).manual_seed(3)
     q, k, v, do = (torch.randn(B_ * N, H_ * Dh, generator=g, device=dev) for _ in range(4))
     sc = 1.0 / float(np.sqrt(Dh))
-    with torch.no_grad():
-        o, Ls, Ms = (torch.empty_like(q), torch.empty(B_ * N * H_, device=dev),
-                     torch.empty(B_ * N * H_, device=dev))
-        mask = torch.ones(N, N, dtype=torch.bool, device=dev).tril()
-        for b in range(B_):
-            qb, kb, vb = (x[b * N:(b + 1) * N].view(N, H_, Dh).transpose(0, 1).contiguous()
-                          for x in (q, k, v))
-            s_ = (qb @ kb.transpose(-1, -2).contiguous() * sc).masked_fill(~mask, float("-inf"))
-            m_ = s_.amax(-1, keepdim=True)
-            e_ = torch.exp(s_ - m_)
-            l_ = e_.sum(-1, keepdim=True)
-            o[b * N:(b + 1) * N] = ((e_ / l_) @ vb).transpose(0, 1).reshape(N, H_ * Dh)
-            Ls.view(B_, N, H_)[b] = l_.squeeze(-1).transpose(0, 1)
-            Ms.view(B_, N, H_)[b] = m_.squeeze(-1).transpose(0, 1)
     L = _lib.lib()
+    o = torch.empty_like(q)
+    Ls, Ms = torch.empty(B_ * N * H_, device=dev), torch.empty(B_ * N * H_, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def fwd():
+        _lib.check(L.skv_flash_fwd(o.data_ptr(), Ls.data_ptr(), Ms.data_ptr(), q.data_ptr(),
+                                   k.data_ptr(), v.data_ptr(), B_, N, H_, Dh, sc, stream),
+                   "skv_flash_fwd")
+
+    # the forward (O, L, M for the backward), timed on its own with HIP events
+    fwd()
+    fevs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(10)]
+    for e0, e1 in fevs:
+        e0.record()
+        fwd()
+        e1.record()
+    torch.cuda.synchronize()
+    fwd_s = float(np.mean([a.elapsed_time(b) for a, b in fevs])) * 1e-3
+    fwd_flops = 4.0 * Dh * (N * (N + 1) / 2) * B_ * H_  # S = QK^T and O = PV, causal pairs
+    forward = {"mean_us": fwd_s * 1e6, "tflops": fwd_flops / fwd_s / 1e12,
+               "peak_tflops": MFMA_FP32_PEAK_TFLOPS,
+               "frac": fwd_flops / fwd_s / 1e12 / MFMA_FP32_PEAK_TFLOPS, "flops": fwd_flops,
+               "kernel": "skv_flash_fwd (k_flash_fwd), O, L, M in fp32"}
     dq, dk, dv = (torch.empty_like(q) for _ in range(3))
     ws = torch.empty(L.skv_flash_bwd_workspace_bytes(B_, N, H_), dtype=torch.uint8, device=dev)
-    stream = _lib.stream_handle(dev)
 
     def call():
         rc = L.skv_flash_bwd(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), q.data_ptr(),
@@ -620,8 +629,8 @@ def run_fb(args, ctx):
         "attention backward tokens/sec", B_ * N * args.steps / wall, "tokens/s", args.steps,
         args.warmup, wall / args.steps * 1e3, "fp32",
         {"workload": "FB causal flash-attention backward fp32: B=8, N=2048, H=16, D=64 "
-                     "(O, L, M from a torch fp32 forward)", "batch": B_},
-        roof, cpu)
+                     "(O, L, M from skv_flash_fwd)", "batch": B_},
+        roof, cpu, forward=forward)
 
 
 def main():

@@ -162,9 +162,13 @@ size_t skv_prefill_workspace_bytes(int B, int C, int H_q, int D, int n_splits);
  * and zeros for i >= n_new[b]. The chunk's own K/V must already be in the
  * cache at positions start[b] .. start[b]+n_new[b]-1 (skv_append_chunk).
  * q, out: [B, C, H_q, D] of q_dt / out_dt; n_new may be NULL (C for all).
- * Requires start[b] + n_new[b] <= T_cap. bf16 caches only: Q, K, V and the
- * probabilities enter v_mfma_f32_32x32x16_bf16 as bf16, accumulation and
- * softmax are fp32. D in {64, 128}; G = H_q / H_kv in {1, 2, 4, 8}.
+ * Requires start[b] + n_new[b] <= T_cap.
+ * bf16 cache: Q, K, V and the probabilities enter v_mfma_f32_32x32x16_bf16
+ * as bf16, accumulation and softmax are fp32; D in {64, 128}; G = H_q / H_kv
+ * in {1, 2, 4, 8}; split over the prefix by n_splits.
+ * fp32 cache: q and out fp32, every product in fp32 (v_mfma_f32_32x32x2_f32,
+ * the kernel of skv_flash_fwd); D in {16, 32, 64, 128}, any G; n_splits and
+ * the workspace are not used.
  */
 int skv_prefill_attn(void* out, const void* q, const void* k_cache, const void* v_cache,
                      const int32_t* start, const int32_t* n_new, int B, int C, int H_q,
@@ -255,8 +259,21 @@ int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                     int max_prompt, int seq_cap, skv_stream_t stream);
 
 /* ------------------------------------------------------------------------
- * Training-side attention: causal FlashAttention backward (fp32).
+ * Training-side attention in fp32: causal FlashAttention forward and backward.
  * ------------------------------------------------------------------------ */
+
+/*
+ * Causal attention with the softmax statistics, replacing flash_attention
+ * (simple-llm/src/gpu/gpu_pass_forward.py:497-588, kernel
+ * create_flash_attention_kernel simple-llm/src/gpu/gpu_kernels.py:499-770):
+ * per batch b and head h, with S = scale * Q K^T over keys <= query,
+ *   M = row max of S, L = sum exp(S - M), out = softmax(S) V.
+ * q, k, v, out: [B, N, H, D] fp32 (the reference's [B*N, H*D] buffers),
+ * 16-byte aligned; L, M: [B, N, H] fp32, or NULL to skip them.
+ * D in {16, 32, 64, 128}. Products on v_mfma_f32_32x32x2_f32 (fp32).
+ */
+int skv_flash_fwd(float* out, float* L, float* M, const float* q, const float* k, const float* v,
+                  int B, int N, int H, int D, float scale, skv_stream_t stream);
 
 /* Bytes of workspace skv_flash_bwd needs: the row deltas, B*N*H floats. */
 size_t skv_flash_bwd_workspace_bytes(int B, int N, int H);

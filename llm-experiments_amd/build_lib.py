@@ -15,7 +15,7 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(HERE, "libskv.so")
 
 SOURCES = ["skv_api.hip", "append.hip", "decode_attn.hip", "prefill_attn.hip", "model_ops.hip",
-           "sample.hip", "flash_bwd.hip", "bpe_tokenizer.cpp"]
+           "sample.hip", "flash_fp32.hip", "bpe_tokenizer.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -37,7 +37,7 @@ def hipcc() -> str:
 # Extra flags per source. The flash backward keeps its MFMA accumulators in
 # ordinary VGPRs (gfx950 MFMAs take either register file); the default
 # heuristic put them in AGPRs and copied them back and forth every step.
-SOURCE_FLAGS = {"flash_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+SOURCE_FLAGS = {"flash_fp32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 _NOISE = "is not a recognized feature for this target"  # hipcc's host pass on -packed-fp32-ops
 

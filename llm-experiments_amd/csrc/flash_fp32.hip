@@ -1,5 +1,8 @@
-// Causal FlashAttention backward on gfx950: fp32 in and out, on
-// v_mfma_f32_32x32x2_f32 (fp32 products, fp32 accumulation).
+// Causal FlashAttention in fp32 on gfx950: the forward with its row
+// statistics (skv_flash_fwd, also the fp32-cache path of skv_prefill_attn)
+// and the backward (skv_flash_bwd), on v_mfma_f32_32x32x2_f32 (fp32
+// products, fp32 accumulation). The notes below describe the backward; the
+// forward reuses its tiling.
 //
 // Reference: simple-llm/src/gpu/gpu_kernels.py:2038-2455 (stage 1, one pass
 // per Q block writing partial dK/dV into a workspace; stage 2, their sum) and
@@ -86,13 +89,15 @@ struct Stage {
   static_assert(NV >= 1 && kCols * C4 % kThreads == 0, "staging shape");
   f32x4 r0[NV], r1[NV];
 
-  __device__ __forceinline__ void load(const float* t0, const float* t1, int row0, int b, int N,
-                                       int H, int h) {
+  // rows row0 .. row0+63 of two tensors whose row t starts at t0 + t * rs
+  // (and t1 + t * rs), rows clamped to n_rows - 1
+  __device__ __forceinline__ void load(const float* t0, const float* t1, int row0, int n_rows,
+                                       size_t rs) {
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
       const int e = threadIdx.x + kThreads * u;
-      const int n = row0 + e / C4;
-      const size_t off = row_off<D>(b, min(n, N - 1), N, H, h) + 4 * (e % C4);
+      const int n = min(row0 + e / C4, n_rows - 1);
+      const size_t off = (size_t)n * rs + 4 * (e % C4);
       r0[u] = *reinterpret_cast<const f32x4*>(t0 + off);
       r1[u] = *reinterpret_cast<const f32x4*>(t1 + off);
     }
@@ -161,13 +166,16 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   // the wave's last query (-1: the wave has none)
   const int wq_last = blk * kRows + wave * 32 < N ? min(blk * kRows + wave * 32 + 31, N - 1) : -1;
   const int steps = q_last / kCols + 1;
+  const size_t rs = (size_t)H * D;
+  const float* kh = a.k + row_off<D>(b, 0, N, H, h);
+  const float* vh = a.v + row_off<D>(b, 0, N, H, h);
   Stage<D> st;
-  st.load(a.k, a.v, 0, b, N, H, h);
+  st.load(kh, vh, 0, N, rs);
   for (int j = 0; j < steps; ++j) {
     __syncthreads();
     st.store(sK, sV);
     __syncthreads();
-    if (j + 1 < steps) st.load(a.k, a.v, (j + 1) * kCols, b, N, H, h);
+    if (j + 1 < steps) st.load(kh, vh, (j + 1) * kCols, N, rs);
 #pragma unroll
     for (int sub = 0; sub < kCols / 32; ++sub) {
       const int key0 = j * kCols + sub * 32;
@@ -280,8 +288,11 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
     il = 1.f / a.L[sr_];                                                         \
     dl = a.delta[sr_];                                                           \
   }
+  const size_t rs = (size_t)H * D;
+  const float* qh = a.q + row_off<D>(b, 0, N, H, h);
+  const float* dh = a.dout + row_off<D>(b, 0, N, H, h);
   if (j0 < steps) {
-    st.load(a.q, a.dout, j0 * kCols, b, N, H, h);
+    st.load(qh, dh, j0 * kCols, N, rs);
     SKV_FB_STATS(j0)
   }
   for (int j = j0; j < steps; ++j) {
@@ -294,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
     }
     __syncthreads();
     if (j + 1 < steps) {
-      st.load(a.q, a.dout, (j + 1) * kCols, b, N, H, h);
+      st.load(qh, dh, (j + 1) * kCols, N, rs);
       SKV_FB_STATS(j + 1)
     }
 #pragma unroll
@@ -371,6 +382,152 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Forward: causal attention with the forward's row statistics, fp32.
+// ---------------------------------------------------------------------------
+
+struct FfwdArgs {
+  const float* q;  // [B, C, Hq, D]
+  const float* k;  // [B, T_cap, Hkv, D]
+  const float* v;
+  const int32_t* start;  // per-sequence position of query 0 (NULL: 0)
+  const int32_t* n_new;  // per-sequence valid queries (NULL: C)
+  float* out;            // [B, C, Hq, D]; rows i >= n_new[b] get zeros
+  float* L;              // [B, C, Hq] softmax sums (may be NULL)
+  float* M;              // [B, C, Hq] row maxima of the scaled scores (may be NULL)
+  int C, Hq, Hkv, T_cap, BH, n_blocks;
+  float sl2;  // scale * log2(e)
+};
+
+// One workgroup per (128 queries, b, query head); rank-major order as in the
+// backward. Each wave owns 32 queries (lane c, both halves): per 32-key piece
+// S^T = K Q^T, an online softmax over the piece, then O^T += V^T P^T. The
+// running max moves only when a piece's max exceeds it by more than 8 (log2
+// units), so O and l are rescaled on few pieces; the true maximum is kept
+// beside it for M and the final L.
+template <int D>
+__global__ __launch_bounds__(kThreads) void k_flash_fwd(FfwdArgs a) {
+  constexpr int G8 = D / 8;
+  constexpr int DT = (D + 31) / 32;
+  constexpr int SP = Stage<D>::SP;
+  __shared__ __attribute__((aligned(16))) float sK[kCols * SP];
+  __shared__ __attribute__((aligned(16))) float sV[kCols * SP];
+
+  const int Hq = a.Hq, C = a.C;
+  const int bh = (int)(blockIdx.x % (unsigned)a.BH), rank = (int)(blockIdx.x / (unsigned)a.BH);
+  const int b = bh / Hq, h = bh % Hq, hk = h / (Hq / a.Hkv);
+  const int blk = a.n_blocks - 1 - rank;
+  const int P = a.start ? min(max(a.start[b], 0), a.T_cap) : 0;
+  const int n = max(0, min(a.n_new ? min(a.n_new[b], C) : C, a.T_cap - P));  // valid queries
+  const int kv_end = P + n;  // keys [0, kv_end) exist
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 31, hf = lane >> 5;
+  const int qi = blk * kRows + wave * 32 + c;  // this lane's query (row of the chunk)
+  const bool qok = qi < n;
+  const int qlim = qok ? P + qi : -1;          // keys <= qlim are unmasked
+  const size_t qoff = (((size_t)b * C + min(qi, max(n, 1) - 1)) * Hq + h) * D;
+
+  f32x4 qf[G8];
+#pragma unroll
+  for (int g = 0; g < G8; ++g) qf[g] = *reinterpret_cast<const f32x4*>(a.q + qoff + 8 * g + 4 * hf);
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+  float m_run = -INFINITY, m_true = -INFINITY, l = 0.f;
+
+  // keys this workgroup and this wave need
+  const int blk_q = min(blk * kRows + kRows, n);  // valid queries of the block end here
+  const int steps = blk * kRows < n ? (P + blk_q + kCols - 1) / kCols : 0;
+  const int wq_last = blk * kRows + wave * 32 < n ? P + min(blk * kRows + wave * 32 + 31, n - 1)
+                                                  : -1;
+  const size_t rs = (size_t)a.Hkv * D;
+  const float* kh = a.k + ((size_t)b * a.T_cap * a.Hkv + hk) * D;
+  const float* vh = a.v + ((size_t)b * a.T_cap * a.Hkv + hk) * D;
+  Stage<D> st;
+  if (steps > 0) st.load(kh, vh, 0, kv_end, rs);
+  for (int j = 0; j < steps; ++j) {
+    __syncthreads();
+    st.store(sK, sV);
+    __syncthreads();
+    if (j + 1 < steps) st.load(kh, vh, (j + 1) * kCols, kv_end, rs);
+#pragma unroll
+    for (int sub = 0; sub < kCols / 32; ++sub) {
+      const int key0 = j * kCols + sub * 32;
+      if (key0 > wq_last) break;  // wave-uniform: every later key is masked for this wave
+      f32x16 s = f32x16{};
+      const float* kr = sK + (sub * 32 + c) * SP + 4 * hf;
+#pragma unroll
+      for (int g = 0; g < G8; ++g) {
+        const f32x4 ka = *reinterpret_cast<const f32x4*>(kr + 8 * g);
+        s = mfma(ka.x, qf[g].x, s);
+        s = mfma(ka.y, qf[g].y, s);
+        s = mfma(ka.z, qf[g].z, s);
+        s = mfma(ka.w, qf[g].w, s);
+      }
+      // s[r]: key key0 + 8(r/4) + 4hf + r%4 of this lane's query, in log2 units
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + 8 * (r / 4) + 4 * hf + (r % 4);
+        s[r] = key <= qlim ? s[r] * a.sl2 : -INFINITY;
+        tmax = fmaxf(tmax, s[r]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));  // both halves hold the same query
+      m_true = fmaxf(m_true, tmax);
+      const bool upd = tmax > m_run + 8.f;  // also true on the first piece with a key
+      if (__ballot(upd) != 0ull) {          // wave-uniform branch
+        const float alpha = upd ? fast_exp2(m_run - tmax) : 1.f;  // m_run = -inf: 0
+        if (upd) m_run = tmax;
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;  // nothing unmasked yet
+      f32x16 p;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[r] = fast_exp2(s[r] - m_use);
+        l += p[r];
+      }
+      // O^T[d][query] += sum_key V[key][d] P^T[key][query]
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int dcol = dt * 32 + c;
+        const bool dok = (D % 32 == 0) || dcol < D;
+        const float* vc = sV + (sub * 32 + 4 * hf) * SP + (dok ? dcol : D - 1);
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float vv = vc[(8 * qq + t) * SP];
+            acc[dt] = mfma(dok ? vv : 0.f, p[4 * qq + t], acc[dt]);
+          }
+        }
+      }
+    }
+  }
+  const float lt = l + __shfl_xor(l, 32);
+  if (qi >= C) return;
+  const size_t orow = ((size_t)b * C + qi) * Hq + h;
+  const float inv = qok ? 1.f / lt : 0.f;  // a valid row saw its own key: lt >= 1
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int d0 = dt * 32 + 8 * qq + 4 * hf;
+      if (d0 < D) {
+        const f32x4 y = {acc[dt][4 * qq] * inv, acc[dt][4 * qq + 1] * inv,
+                         acc[dt][4 * qq + 2] * inv, acc[dt][4 * qq + 3] * inv};
+        *reinterpret_cast<f32x4*>(a.out + orow * D + d0) = y;
+      }
+    }
+  }
+  if (hf == 0 && qok) {
+    if (a.L) a.L[orow] = lt * fast_exp2(m_run - m_true);  // relative to the true maximum
+    if (a.M) a.M[orow] = m_true * (1.f / LOG2E);          // natural units, as the scores
+  }
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
@@ -424,4 +581,47 @@ extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, co
   SKV_FB(16) SKV_FB(32) SKV_FB(64) SKV_FB(128)
 #undef SKV_FB
   return check_launch(fn);
+}
+
+namespace skv {
+
+// Causal fp32 attention of C queries per sequence over the keys [0, start[b]
+// + i] of a [B, T_cap, Hkv, D] key/value layout (shared by skv_flash_fwd and
+// skv_prefill_attn on fp32 caches). Pointers are checked by the callers.
+int attn_fwd_f32(float* out, float* L, float* M, const float* q, const float* k, const float* v,
+                 const int32_t* start, const int32_t* n_new, int B, int C, int Hq, int Hkv, int D,
+                 int T_cap, float scale, hipStream_t s, const char* fn) {
+  SKV_REQUIRE(D == 16 || D == 32 || D == 64 || D == 128, SKV_E_UNSUPPORTED,
+              "%s: head_dim %d (supported: 16, 32, 64, 128)", fn, D);
+  SKV_REQUIRE(aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v), SKV_E_INVALID,
+              "%s: q, k, v and out must be 16-byte aligned", fn);
+  FfwdArgs a;
+  a.q = q; a.k = k; a.v = v; a.start = start; a.n_new = n_new;
+  a.out = out; a.L = L; a.M = M;
+  a.C = C; a.Hq = Hq; a.Hkv = Hkv; a.T_cap = T_cap;
+  a.BH = B * Hq;
+  a.n_blocks = (C + kRows - 1) / kRows;
+  a.sl2 = scale * LOG2E;
+  SKV_REQUIRE((long)a.n_blocks * a.BH < (1L << 31), SKV_E_UNSUPPORTED, "%s: grid too large", fn);
+  const dim3 grid((unsigned)(a.n_blocks * a.BH));
+#define SKV_FF(DD) \
+  if (D == DD) hipLaunchKernelGGL((k_flash_fwd<DD>), grid, dim3(kThreads), 0, s, a);
+  SKV_FF(16) SKV_FF(32) SKV_FF(64) SKV_FF(128)
+#undef SKV_FF
+  return check_launch(fn);
+}
+
+}  // namespace skv
+
+extern "C" int skv_flash_fwd(float* out, float* L, float* M, const float* q, const float* k,
+                             const float* v, int B, int N, int H, int D, float scale,
+                             skv_stream_t stream) {
+  const char* fn = "skv_flash_fwd";
+  SKV_REQUIRE(out && q && k && v, SKV_E_INVALID, "%s: null pointer argument", fn);
+  SKV_REQUIRE(B > 0 && N > 0 && H > 0 && D > 0, SKV_E_INVALID,
+              "%s: dims must be > 0 (B=%d N=%d H=%d D=%d)", fn, B, N, H, D);
+  SKV_REQUIRE(scale > 0.f, SKV_E_INVALID, "%s: scale must be > 0", fn);
+  SKV_REQUIRE((long)B * N * H * D < (1L << 40), SKV_E_UNSUPPORTED, "%s: tensors too large", fn);
+  return attn_fwd_f32(out, L, M, q, k, v, nullptr, nullptr, B, N, H, H, D, N, scale,
+                      (hipStream_t)stream, fn);
 }

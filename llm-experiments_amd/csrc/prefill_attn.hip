@@ -453,15 +453,20 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
               H_kv);
   SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(q_dt) && dt_ok(out_dt), SKV_E_INVALID, "%s: bad dtype",
               fn);
-  SKV_REQUIRE(cache_dt == SKV_BF16, SKV_E_UNSUPPORTED,
-              "%s: the MFMA prefill reads bf16 caches (got fp32)", fn);
+  SKV_REQUIRE(scale > 0.f, SKV_E_INVALID, "%s: scale must be > 0", fn);
+  if (cache_dt == SKV_F32) {  // fp32 cache: the fp32 MFMA path, no split
+    SKV_REQUIRE(q_dt == SKV_F32 && out_dt == SKV_F32, SKV_E_UNSUPPORTED,
+                "%s: an fp32 cache takes fp32 q and out", fn);
+    return attn_fwd_f32(static_cast<float*>(out), nullptr, nullptr, static_cast<const float*>(q),
+                        static_cast<const float*>(k_cache), static_cast<const float*>(v_cache),
+                        start, n_new, B, C, H_q, H_kv, D, T_cap, scale, (hipStream_t)stream, fn);
+  }
   SKV_REQUIRE(D == 64 || D == 128, SKV_E_UNSUPPORTED, "%s: D=%d (supported: 64, 128)", fn, D);
   const int G = H_q / H_kv;
   SKV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, SKV_E_UNSUPPORTED,
               "%s: no kernel for G=%d", fn, G);
   SKV_REQUIRE(n_splits >= 1 && n_splits <= 32, SKV_E_INVALID, "%s: n_splits=%d out of range", fn,
               n_splits);
-  SKV_REQUIRE(scale > 0.f, SKV_E_INVALID, "%s: scale must be > 0", fn);
   if (n_splits > 1) {
     const size_t need = skv_prefill_workspace_bytes(B, C, H_q, D, n_splits);
     SKV_REQUIRE(ws && ws_bytes >= need, SKV_E_WORKSPACE, "%s: workspace %zu bytes < %zu required",

@@ -193,6 +193,12 @@ constexpr float LN2 = 0.6931471805599453f;
 namespace skv {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+
+// Causal fp32 attention over a [B, T_cap, Hkv, D] key/value layout, query
+// row i of sequence b at position start[b] + i (flash_fp32.hip).
+int attn_fwd_f32(float* out, float* L, float* M, const float* q, const float* k, const float* v,
+                 const int32_t* start, const int32_t* n_new, int B, int C, int Hq, int Hkv, int D,
+                 int T_cap, float scale, hipStream_t s, const char* fn);
 }  // namespace skv
 
 #define SKV_REQUIRE(cond, code, ...)                          \

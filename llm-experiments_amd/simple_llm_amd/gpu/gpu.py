@@ -26,6 +26,7 @@ from .gpu_kv_cache import (
     kv_cache_update,
 )
 from .gpu_pass_backward import flash_attention_backward
+from .gpu_pass_forward import flash_attention
 from .gpu_ops import batch_begin, batch_commit, validate_buffer_shape_1d, validate_buffer_shape_2d
 from .gpu_types import (
     BatchState,
@@ -80,5 +81,6 @@ __all__ = [
     "decode_attention",
     "decode_plan",
     # Training-side attention
+    "flash_attention",
     "flash_attention_backward",
 ]

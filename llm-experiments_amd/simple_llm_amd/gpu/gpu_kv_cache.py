@@ -343,9 +343,12 @@ def kv_cache_prefill(ctx: GPUContext, cache: KVCache, layer_idx: int, new_k: tor
     flash_attention, gpu/gpu_kernels.py:695-701, shifted by the cached
     prefix). The layer's fills advance by n_new. Returns the new fills.
 
+    A bfloat16 cache runs the bf16 MFMA prefill; a float32 cache runs every
+    product in fp32 (float32 q and out).
+
     Raises ValueError (before any GPU work) on a bad layer, shapes, a chunk
-    that would overflow a sequence ("Cache is full"), a paged cache, or an
-    attention request on a float32 cache (the MFMA prefill reads bf16).
+    that would overflow a sequence ("Cache is full"), a paged cache, or a
+    float32 cache with non-float32 q/output.
     """
     _check_layer(cache, layer_idx)
     if cache.paged:
@@ -380,9 +383,10 @@ def kv_cache_prefill(ctx: GPUContext, cache: KVCache, layer_idx: int, new_k: tor
             _check_tensor(t, nm, dev)
             if tuple(t.shape) != (B, C, Hq, D):
                 raise ValueError(f"{nm} must be [{B}, {C}, {Hq}, {D}], got {tuple(t.shape)}")
-        if cache.dtype != torch.bfloat16:
-            raise ValueError("kv_cache_prefill: attention over a float32 cache is not "
-                             "supported (the MFMA prefill reads bf16 caches)")
+        if cache.dtype == torch.float32 and (q.dtype != torch.float32 or
+                                             out.dtype != torch.float32):
+            raise ValueError("kv_cache_prefill: attention over a float32 cache takes float32 "
+                             "q and output")
     batch_count(ctx)
     L = _lib.lib()
     stream = _lib.stream_handle(dev)

@@ -137,6 +137,21 @@ def test_flash_bwd_rejects_bad_arguments():
     assert "workspace" in (call() and _lib.lib().skv_last_error().decode())
 
 
+def test_flash_fwd_rejects_bad_arguments():
+    L = _lib.lib()
+    fake = 4096  # never dereferenced: each call below fails validation first
+
+    def call(D=64, ptr=fake, scale=0.125, n=100):
+        return L.skv_flash_fwd(ptr, None, None, fake, fake, fake, 2, n, 3, D, scale, None)
+
+    assert call(D=48) == _lib.SKV_E_UNSUPPORTED
+    assert call(D=256) == _lib.SKV_E_UNSUPPORTED
+    assert call(ptr=None) == _lib.SKV_E_INVALID
+    assert call(ptr=fake + 4) == _lib.SKV_E_INVALID  # not 16-byte aligned
+    assert call(scale=-1.0) == _lib.SKV_E_INVALID
+    assert call(n=0) == _lib.SKV_E_INVALID
+
+
 def test_check_maps_status_to_exceptions():
     L = _lib.lib()
     L.skv_append(None, None, None, None, None, 1, 1, 64, 1, 0, 0, None)

@@ -2,9 +2,9 @@
 skv_advance, driven through kv_cache_prefill) with the CPU oracle. Needs the
 MI355X.
 
-The prefill reads bf16 caches and feeds Q, K, V and the softmax
-probabilities to v_mfma_f32_32x32x16_bf16 in bf16, with fp32 accumulation
-and softmax. Tolerance: the north star's 2e-2 relative error for bf16
+On bf16 caches the prefill feeds Q, K, V and the softmax probabilities to
+v_mfma_f32_32x32x16_bf16 in bf16, with fp32 accumulation and softmax (fp32
+caches take the fp32 kernel, tested in test_flash_fwd_gpu.py). Tolerance: the north star's 2e-2 relative error for bf16
 storage with fp32 accumulation, norm-wise per (sequence, query, head),
 against the float64 oracle fed the same bf16-rounded q, K and V. Cache bytes
 and fills after the chunk append: bit-exact.
@@ -186,8 +186,8 @@ def test_prefill_rejects_bad_calls(gpu_ctx):
                              torch.zeros((2, 4, 3, 64), device="cuda"))
     f32 = gpu.kv_cache_create(gpu_ctx, gpu.KVCacheConfig(2, 100, 1, 4, 64))
     q = torch.zeros((2, 4, 4, 64), device="cuda")
-    with pytest.raises(ValueError, match="float32 cache"):
-        gpu.kv_cache_prefill(gpu_ctx, f32, 0, q, q, q, torch.empty_like(q))
+    with pytest.raises(ValueError, match="float32 cache takes float32"):
+        gpu.kv_cache_prefill(gpu_ctx, f32, 0, q, q, q.bfloat16(), torch.empty_like(q))
     np.testing.assert_array_equal(f32.seq_lens(), [0, 0])  # nothing ran
 
 
