@@ -202,6 +202,28 @@ def _record(metric, value, unit, steps, warmup, ms_per_step, dtype, config, roof
     return rec
 
 
+def _time_cached_cpu(params, n_heads, batch, t_cap, budget_s):
+    """The same cached algorithm as the GPU path on the CPU (torch fp32,
+    oracle/model_oracle.TorchCachedDecoder): steps of `batch` sequences from
+    an empty cache until the budget is spent (at most t_cap steps)."""
+    import numpy as np
+    import torch
+
+    from oracle import model_oracle as mo
+
+    with torch.no_grad():
+        dec = mo.TorchCachedDecoder(params, n_heads, batch, t_cap)
+        vocab = int(np.asarray(params["embedding"]).shape[0])
+        toks = np.random.default_rng(0).integers(0, vocab, (t_cap, batch))
+        dec.step(toks[0])  # warm-up
+        n, t0 = 0, time.perf_counter()
+        while n + 1 < t_cap and time.perf_counter() - t0 < budget_s:
+            dec.step(toks[n + 1])
+            n += 1
+        dt = time.perf_counter() - t0
+    return n, dt
+
+
 def _time_reference_generate(params, prompt, n_heads, context, budget_s, max_tokens):
     """The reference's generate loop (generate.py:29-69, greedy): a full
     float32 torch CPU forward over the left-padded window per token."""
@@ -268,7 +290,7 @@ def run_c1(args, ctx):
     params, model, runs, wbytes = _model_workload(args, ctx, tm, [prompt], 256, "c1",
                                                   [torch.float32])
     r = runs["float32"]
-    cpu = None
+    cpu = cpu_cached = None
     if not args.no_cpu_baseline:
         n, dt = _time_reference_generate(params, prompt, 4, 256, args.cpu_seconds, 192)
         cpu = {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
@@ -276,6 +298,11 @@ def run_c1(args, ctx):
                "sample": f"{n} greedy tokens of the reference's generate loop (full float32 "
                          f"forward over the 256-token left-padded window per token, torch CPU), "
                          f"{dt:.1f} s"}
+        n2, dt2 = _time_cached_cpu(params, 4, 1, 256, args.cpu_seconds)
+        cpu_cached = {"value": n2 / dt2, "unit": "tokens/s", "cores": torch.get_num_threads(),
+                      "kind": "port",
+                      "sample": f"{n2} steps of the cached recurrence (torch CPU fp32, batch 1, "
+                                f"positions 1..{n2}), {dt2:.1f} s"}
     return _record(
         "decode tokens/sec", r["tokens_per_s"], "tokens/s", r["steps"], 1, r["step_us"] / 1e3,
         "fp32",
@@ -287,7 +314,7 @@ def run_c1(args, ctx):
                                             "step replayed from one HIP graph",
          "achieved": wbytes / (r["step_us"] * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": wbytes / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, "traffic": None},
-        cpu, runs=runs)
+        cpu, runs=runs, cpu_cached_baseline=cpu_cached)
 
 
 def run_c3(args, ctx):
@@ -312,7 +339,7 @@ def run_c3(args, ctx):
     for k, run in runs.items():
         by = wbytes + 16 * 12 * 2 * mean_fill * 768 * kv[k]
         roof[k] = by / (run["step_us"] * 1e-6) / 1e9
-    cpu = None
+    cpu = cpu_cached = None
     if not args.no_cpu_baseline:
         n, dt = _time_reference_generate(params, prompts[0], 12, 1024, args.cpu_seconds, 4)
         cpu = {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
@@ -320,6 +347,11 @@ def run_c3(args, ctx):
                "sample": f"{n} greedy tokens of one sequence through the reference's generate "
                          f"loop (full float32 forward over the 1024-token window per token, "
                          f"~292 GFLOP each, torch CPU), {dt:.1f} s; the reference runs batch 1"}
+        n2, dt2 = _time_cached_cpu(params, 12, 16, 1024, args.cpu_seconds)
+        cpu_cached = {"value": 16 * n2 / dt2, "unit": "tokens/s",
+                      "cores": torch.get_num_threads(), "kind": "port",
+                      "sample": f"{n2} steps of the cached recurrence for 16 sequences (torch "
+                                f"CPU fp32, fp32 KV, positions 1..{n2}), {dt2:.1f} s"}
     r32 = runs["float32"]
     return _record(
         "decode tokens/sec", r32["tokens_per_s"], "tokens/s", r32["steps"], 1,
@@ -332,7 +364,7 @@ def run_c3(args, ctx):
          "frac": roof["float32"] / HBM_PEAK_GBS, "traffic": None,
          "note": "per step: all weights + mean K/V prefix of 16 sequences, over step time",
          "achieved_bf16_kv": roof["bfloat16"]},
-        cpu, runs=runs)
+        cpu, runs=runs, cpu_cached_baseline=cpu_cached)
 
 
 def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt, label):

@@ -33,6 +33,8 @@ How each function is pinned (tests/test_model_oracle.py):
                         through a spy forward, while the window is not full
                         and once the sequence is longer than the window
   torch_forward_fp32    equals forward to float32 accuracy
+  TorchCachedDecoder    its step logits equal decode_step's (the float64
+                        cached recurrence) to float32 accuracy
 """
 from __future__ import annotations
 
@@ -237,3 +239,58 @@ def torch_forward_fp32(params: dict, tokens, n_heads: int):
         f = 0.5 * f * (1 + torch.tanh(0.7978845608028654 * (f + 0.044715 * f ** 3)))
         x = x + f @ lp["ff_w2"] + lp["ff_b2"]
     return x @ E.T
+
+
+class TorchCachedDecoder:
+    """The cached recurrence of decode_step in float32 torch on the CPU,
+    batched: bench.py's second CPU baseline for C1/C3 (the same algorithm as
+    the GPU path, so it separates the algorithmic gain of the cache from the
+    hardware gain). K/V live in [B, H, T_cap, D] tensors per layer; one call
+    advances every sequence by one token."""
+
+    def __init__(self, params: dict, n_heads: int, batch: int, t_cap: int):
+        import torch
+
+        self.torch = torch
+        f = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32))  # noqa: E731
+        self.E, self.PE = f(params["embedding"]), f(params["pos_encoding"])
+        self.L = [{k: f(lp[k]) for k in LAYER_FIELDS} for lp in params["layers"]]
+        self.H, self.B, self.T = n_heads, batch, t_cap
+        d = self.E.shape[1]
+        self.D = d // n_heads
+        shape = (batch, n_heads, t_cap, self.D)
+        self.k = [torch.zeros(shape) for _ in self.L]
+        self.v = [torch.zeros(shape) for _ in self.L]
+        self.len = torch.zeros(batch, dtype=torch.long)
+
+    def step(self, tokens) -> "np.ndarray":
+        """Feeds tokens[b] at position len[b] of each sequence; returns the
+        float32 logits [B, V] and advances every length by one."""
+        torch = self.torch
+        B, H, D = self.B, self.H, self.D
+        ids = torch.as_tensor(np.asarray(tokens), dtype=torch.long)
+        pos = self.len.clone()
+        x = self.E[ids] + self.PE[pos]
+        rows = torch.arange(B)
+        mask = torch.arange(self.T)[None, :] > pos[:, None]  # [B, T]: beyond the new token
+
+        def ln(y, g, b):
+            mu = y.mean(-1, keepdim=True)
+            var = ((y - mu) ** 2).mean(-1, keepdim=True)
+            return (y - mu) / torch.sqrt(var + 1e-5) * g + b
+
+        for li, lp in enumerate(self.L):
+            h = ln(x, lp["ln_gamma1"], lp["ln_beta1"])
+            q = (h @ lp["attn_wq"]).reshape(B, H, 1, D)
+            self.k[li][rows, :, pos] = (h @ lp["attn_wk"]).reshape(B, H, D)
+            self.v[li][rows, :, pos] = (h @ lp["attn_wv"]).reshape(B, H, D)
+            s = (q @ self.k[li].transpose(-1, -2))[:, :, 0] / (D ** 0.5)  # [B, H, T]
+            s = s.masked_fill(mask[:, None, :], float("-inf"))
+            a = (torch.softmax(s, -1)[:, :, None] @ self.v[li])[:, :, 0]  # [B, H, D]
+            x = x + a.reshape(B, H * D) @ lp["attn_wo"]
+            h = ln(x, lp["ln_gamma2"], lp["ln_beta2"])
+            f = h @ lp["ff_w1"] + lp["ff_b1"]
+            f = 0.5 * f * (1 + torch.tanh(0.7978845608028654 * (f + 0.044715 * f ** 3)))
+            x = x + f @ lp["ff_w2"] + lp["ff_b2"]
+        self.len += 1
+        return (x @ self.E.T).numpy()

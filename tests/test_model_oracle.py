@@ -170,3 +170,20 @@ def test_torch_fp32_forward_matches_oracle():
     want = mo.forward(p, toks, 4)
     err = np.linalg.norm(got - want, axis=-1) / np.linalg.norm(want, axis=-1)
     assert err.max() < 1e-4
+
+
+def test_torch_cached_decoder_matches_decode_step():
+    """The float32 batched cache decoder (bench.py's same-algorithm CPU
+    baseline) equals the float64 cached recurrence step by step."""
+    params = mo.init_params(61, 32, 2, 40, seed=3, std=0.1)
+    rng = np.random.default_rng(8)
+    B, steps = 3, 12
+    toks = rng.integers(0, 61, (B, steps))
+    dec = mo.TorchCachedDecoder(params, 4, B, 40)
+    state = mo.DecodeState(2, B)
+    for t in range(steps):
+        got = dec.step(toks[:, t])
+        want = mo.decode_step(params, state, toks[:, t], [t] * B, 4)
+        err = np.linalg.norm(got - want, axis=1) / np.linalg.norm(want, axis=1)
+        assert err.max() < 1e-5, (t, err.max())
+    assert dec.len.tolist() == [steps] * B
