@@ -143,6 +143,30 @@ int skv_decode_attn_paged(void* out, const void* q, const void* k_pool,
                           int out_dt, skv_stream_t stream);
 
 /*
+ * One decode step of one layer in one call: exactly skv_append followed by
+ * skv_decode_attn (kv_cache_update then attention_with_kv_cache,
+ * simple-llm/src/gpu/gpu_kv_cache.py:113-186, 194-289), without the
+ * separate append launch. new_k, new_v: [B, H_kv, D] of in_dt. Sequence b
+ * with 0 <= lens[b] < capacity writes its token at lens[b] (rounded to the
+ * cache dtype) and attends [0, lens[b]]; others attend their clamped fill
+ * unchanged. lens[b] is advanced on the device after the attention. The plan
+ * (skv_decode_plan) must cover the lengths after the append.
+ */
+int skv_append_decode_attn(void* out, const void* q, void* k_cache, void* v_cache,
+                           const void* new_k, const void* new_v, int32_t* lens, int B, int H_q,
+                           int H_kv, int D, int T_cap, float scale, int chunk_tokens,
+                           int n_chunks_max, void* ws, size_t ws_bytes, int cache_dt, int in_dt,
+                           int q_dt, int out_dt, skv_stream_t stream);
+
+/* Paged variant of skv_append_decode_attn. */
+int skv_append_decode_attn_paged(void* out, const void* q, void* k_pool, void* v_pool,
+                                 const void* new_k, const void* new_v, int32_t* lens,
+                                 const int32_t* block_table, int max_blocks, int block_size,
+                                 int B, int H_q, int H_kv, int D, float scale, int chunk_tokens,
+                                 int n_chunks_max, void* ws, size_t ws_bytes, int cache_dt,
+                                 int in_dt, int q_dt, int out_dt, skv_stream_t stream);
+
+/*
  * Split count for skv_prefill_attn (host-only): about one workgroup per CU.
  * max_kv_end = the largest start[b] + n_new[b] of the call.
  */

@@ -62,12 +62,47 @@ struct DecodeArgs {
   long long* cum;  // [B + 1] exclusive prefix sums of the clamped lengths
   float* ws_o;   // [Hq][n_slots][D]
   float* ws_ml;  // [Hq][n_slots][2]  (m in log2 units, l)
+  // Fused append (skv_append_decode_attn*): the token new_k/new_v[b] goes to
+  // position lens[b] (if lens[b] in [0, cap)) before the attention, which
+  // then covers it; NULL for plain decode attention.
+  const void* new_k;  // [B, Hkv, D] of in_dt
+  const void* new_v;
+  int in_dt;
 };
 
+__device__ __forceinline__ bool appends(const DecodeArgs& a, int b) {
+  return a.new_k != nullptr && a.lens[b] >= 0 && a.lens[b] < a.cap;
+}
+
 // Lengths outside [0, cap] are clamped so no row outside the cache (or block
-// table entry outside the table) is ever addressed.
+// table entry outside the table) is ever addressed; a fused append adds its
+// token.
 __device__ __forceinline__ int clamped_len(const DecodeArgs& a, int b) {
-  return min(max(a.lens[b], 0), a.cap);
+  return min(max(a.lens[b], 0), a.cap) + (appends(a, b) ? 1 : 0);
+}
+
+// Stores the EPL values x (rounded to the cache's precision in place) at p.
+template <typename TC, int EPL>
+__device__ __forceinline__ void store_row(TC* p, float (&x)[EPL]) {
+  if constexpr (sizeof(TC) == 4) {
+#pragma unroll
+    for (int i = 0; i < EPL / 4; ++i)
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(p) + 4 * i) =
+          make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+  } else {
+    uint32_t w[EPL / 2];
+#pragma unroll
+    for (int e = 0; e < EPL; e += 2) {
+      const uint16_t lo = f32_to_bf16(x[e]), hi = f32_to_bf16(x[e + 1]);
+      x[e] = bf16_to_f32(lo);
+      x[e + 1] = bf16_to_f32(hi);
+      w[e / 2] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    if constexpr (EPL == 8)
+      *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    else
+      *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+  }
 }
 
 template <typename TC, int D, bool PAGED>
@@ -172,17 +207,21 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
   const TC* kb = static_cast<const TC*>(a.k);
   const TC* vb = static_cast<const TC*>(a.v);
   const int step = S * TPG;
+  // A fused append's token is the last of its sequence: the main loop stops
+  // before it (mend) and substream 0 takes it from the input after the loop.
+  const bool has_new = appends(a, b) && end == clamped_len(a, b);
+  const int mend = has_new ? end - 1 : end;
 
   // Loads of the TPG tokens from t0 on (rows past end are clamped: masked in
   // consume, never out of bounds).
 #define SKV_LOAD_TILE(KF, VF, T0)                                             \
   {                                                                           \
     _Pragma("unroll") for (int u = 0; u < TPG; ++u) {                         \
-      const int t_ = min((T0) + u, end - 1);                                  \
+      const int t_ = min((T0) + u, mend - 1);                                  \
       KF[u].load(row_ptr<TC, D, PAGED>(kb, a, b, t_, hk) + e0);               \
     }                                                                         \
     _Pragma("unroll") for (int u = 0; u < TPG; ++u) {                         \
-      const int t_ = min((T0) + u, end - 1);                                  \
+      const int t_ = min((T0) + u, mend - 1);                                  \
       VF[u].load(row_ptr<TC, D, PAGED>(vb, a, b, t_, hk) + e0);               \
     }                                                                         \
   }
@@ -196,7 +235,7 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
         _Pragma("unroll") for (int e = 0; e < EPL; ++e) d =                   \
             fmaf(q[h][e], KF[u].get(e), d);                                   \
         d = row16_sum(d);                                                     \
-        s[u] = ((T0) + u < end) ? d : -INFINITY;                              \
+        s[u] = ((T0) + u < mend) ? d : -INFINITY;                              \
       }                                                                       \
       float mx = m[h];                                                        \
       _Pragma("unroll") for (int u = 0; u < TPG; ++u) mx = fmaxf(mx, s[u]);   \
@@ -220,18 +259,18 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
     // instead of one per group).
     Frag<TC, EPL> ka[TPG], va[TPG], kn[TPG], vn[TPG];
     int t0 = start + sub * TPG;
-    if (t0 < end) SKV_LOAD_TILE(ka, va, t0);
-    while (t0 < end) {
-      if (t0 + step < end) SKV_LOAD_TILE(kn, vn, t0 + step);
+    if (t0 < mend) SKV_LOAD_TILE(ka, va, t0);
+    while (t0 < mend) {
+      if (t0 + step < mend) SKV_LOAD_TILE(kn, vn, t0 + step);
       SKV_CONSUME(ka, va, t0);
       t0 += step;
-      if (t0 >= end) break;
-      if (t0 + step < end) SKV_LOAD_TILE(ka, va, t0 + step);
+      if (t0 >= mend) break;
+      if (t0 + step < mend) SKV_LOAD_TILE(ka, va, t0 + step);
       SKV_CONSUME(kn, vn, t0);
       t0 += step;
     }
   } else {
-    for (int t0 = start + sub * TPG; t0 < end; t0 += step) {
+    for (int t0 = start + sub * TPG; t0 < mend; t0 += step) {
       Frag<TC, EPL> kf[TPG], vf[TPG];
       SKV_LOAD_TILE(kf, vf, t0);
       SKV_CONSUME(kf, vf, t0);
@@ -239,6 +278,37 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
   }
 #undef SKV_CONSUME
 #undef SKV_LOAD_TILE
+
+  if (has_new && sub == 0) {
+    // The appended token: the input row, rounded to the cache's precision,
+    // is stored at position end - 1 and attended like the cached ones.
+    const int tn = end - 1;
+    float kx[EPL], vx[EPL];
+    const size_t src = ((size_t)b * a.Hkv + hk) * D + e0;
+    if constexpr (EPL == 8) {
+      load8_f32(a.new_k, src, a.in_dt, kx);
+      load8_f32(a.new_v, src, a.in_dt, vx);
+    } else {
+      load4_f32(a.new_k, src, a.in_dt, kx);
+      load4_f32(a.new_v, src, a.in_dt, vx);
+    }
+    store_row<TC, EPL>(const_cast<TC*>(row_ptr<TC, D, PAGED>(kb, a, b, tn, hk)) + e0, kx);
+    store_row<TC, EPL>(const_cast<TC*>(row_ptr<TC, D, PAGED>(vb, a, b, tn, hk)) + e0, vx);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) d = fmaf(q[h][e], kx[e], d);
+      d = row16_sum(d);
+      const float mx = fmaxf(m[h], d);
+      const float alpha = fast_exp2(m[h] - mx);  // 0 if the row saw no token yet
+      const float p = fast_exp2(d - mx);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(p, vx[e], acc[h][e] * alpha);
+      l[h] = l[h] * alpha + p;
+      m[h] = mx;
+    }
+  }
 
   if (S == 1) {
     // One row per head: it holds the whole piece's partial. A row that saw no
@@ -330,10 +400,17 @@ __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, in
                                                       const long long* __restrict__ cum,
                                                       const float* __restrict__ ws_o,
                                                       const float* __restrict__ ws_ml, int Hq,
-                                                      int chunk, int n_wg, int n_slots) {
+                                                      int chunk, int n_wg, int n_slots,
+                                                      int32_t* __restrict__ lens_inc, int cap) {
   constexpr int NS = 8;
   constexpr int EPL = D / 32;
   const int hq = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  // fused append: the sequence's length moves past its new token once pass 1
+  // (which read it) has finished; nothing below reads lens
+  if (lens_inc && hq == 0 && tid == 0) {
+    const int p = lens_inc[b];
+    if (p >= 0 && p < cap) lens_inc[b] = p + 1;
+  }
   const int st = tid >> 5, li = tid & 31;
   const size_t obase = ((size_t)b * Hq + hq) * D;
   const long long c0 = cum[b], c1 = cum[b + 1];
@@ -443,8 +520,13 @@ template <bool PAGED>
 int decode_common(void* out, const void* q, const void* k, const void* v, const int32_t* lens,
                   const int32_t* bt, int max_blocks, int block_size, int B, int Hq, int Hkv,
                   int D, int T_cap, float scale, int chunk, int n_chunks_max, void* ws,
-                  size_t ws_bytes, int cache_dt, int q_dt, int out_dt, hipStream_t s) {
-  const char* fn = PAGED ? "skv_decode_attn_paged" : "skv_decode_attn";
+                  size_t ws_bytes, int cache_dt, int q_dt, int out_dt, hipStream_t s,
+                  const void* new_k = nullptr, const void* new_v = nullptr, int in_dt = 0) {
+  const bool app = new_k != nullptr;
+  const char* fn = app ? (PAGED ? "skv_append_decode_attn_paged" : "skv_append_decode_attn")
+                       : (PAGED ? "skv_decode_attn_paged" : "skv_decode_attn");
+  SKV_REQUIRE(!app || (new_v && dt_ok(in_dt)), SKV_E_INVALID,
+              "%s: new_v missing or bad input dtype", fn);
   SKV_REQUIRE(out && q && k && v && lens && ws, SKV_E_INVALID, "%s: null pointer argument", fn);
   SKV_REQUIRE(!PAGED || bt, SKV_E_INVALID, "%s: null block table", fn);
   SKV_REQUIRE(B > 0 && Hq > 0 && Hkv > 0, SKV_E_INVALID, "%s: dims must be > 0", fn);
@@ -490,18 +572,22 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   a.ws_o = static_cast<float*>(ws);
   a.ws_ml = a.ws_o + parts * D;
   a.cum = reinterpret_cast<long long*>(a.ws_ml + parts * 2);
+  a.new_k = new_k;
+  a.new_v = new_v;
+  a.in_dt = in_dt;
   const int G = Hq / Hkv;
   int rc = cache_dt == SKV_BF16 ? dispatch_partial<uint16_t, PAGED>(a, D, G, s)
                                 : dispatch_partial<float, PAGED>(a, D, G, s);
   if (rc) return rc;
   rc = check_launch(fn);
   if (rc) return rc;
+  int32_t* lens_inc = app ? const_cast<int32_t*>(lens) : nullptr;
   if (D == 64)
     hipLaunchKernelGGL(k_decode_merge<64>, dim3(Hq, B), dim3(256), 0, s, out, out_dt, a.cum,
-                       a.ws_o, a.ws_ml, Hq, chunk, a.n_wg, a.n_slots);
+                       a.ws_o, a.ws_ml, Hq, chunk, a.n_wg, a.n_slots, lens_inc, a.cap);
   else
     hipLaunchKernelGGL(k_decode_merge<128>, dim3(Hq, B), dim3(256), 0, s, out, out_dt, a.cum,
-                       a.ws_o, a.ws_ml, Hq, chunk, a.n_wg, a.n_slots);
+                       a.ws_o, a.ws_ml, Hq, chunk, a.n_wg, a.n_slots, lens_inc, a.cap);
   return check_launch(fn);
 }
 
@@ -574,4 +660,31 @@ extern "C" int skv_decode_attn_paged(void* out, const void* q, const void* k_poo
   return decode_common<true>(out, q, k_pool, v_pool, lens, block_table, max_blocks, block_size, B,
                              H_q, H_kv, D, 0, scale, chunk_tokens, n_chunks_max, ws, ws_bytes,
                              cache_dt, q_dt, out_dt, (hipStream_t)stream);
+}
+
+extern "C" int skv_append_decode_attn(void* out, const void* q, void* k_cache, void* v_cache,
+                                      const void* new_k, const void* new_v, int32_t* lens, int B,
+                                      int H_q, int H_kv, int D, int T_cap, float scale,
+                                      int chunk_tokens, int n_chunks_max, void* ws,
+                                      size_t ws_bytes, int cache_dt, int in_dt, int q_dt,
+                                      int out_dt, skv_stream_t stream) {
+  if (!new_k)
+    return set_error(SKV_E_INVALID, "skv_append_decode_attn: null pointer argument");
+  return decode_common<false>(out, q, k_cache, v_cache, lens, nullptr, 0, 0, B, H_q, H_kv, D,
+                              T_cap, scale, chunk_tokens, n_chunks_max, ws, ws_bytes, cache_dt,
+                              q_dt, out_dt, (hipStream_t)stream, new_k, new_v, in_dt);
+}
+
+extern "C" int skv_append_decode_attn_paged(void* out, const void* q, void* k_pool, void* v_pool,
+                                            const void* new_k, const void* new_v, int32_t* lens,
+                                            const int32_t* block_table, int max_blocks,
+                                            int block_size, int B, int H_q, int H_kv, int D,
+                                            float scale, int chunk_tokens, int n_chunks_max,
+                                            void* ws, size_t ws_bytes, int cache_dt, int in_dt,
+                                            int q_dt, int out_dt, skv_stream_t stream) {
+  if (!new_k)
+    return set_error(SKV_E_INVALID, "skv_append_decode_attn_paged: null pointer argument");
+  return decode_common<true>(out, q, k_pool, v_pool, lens, block_table, max_blocks, block_size, B,
+                             H_q, H_kv, D, 0, scale, chunk_tokens, n_chunks_max, ws, ws_bytes,
+                             cache_dt, q_dt, out_dt, (hipStream_t)stream, new_k, new_v, in_dt);
 }

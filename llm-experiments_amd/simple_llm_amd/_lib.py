@@ -59,6 +59,10 @@ _SIGNATURES = {
     "skv_next_tokens": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "skv_decode_attn": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _Z,
                              _I, _I, _I, _P]),
+    "skv_append_decode_attn": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I,
+                                    _P, _Z, _I, _I, _I, _I, _P]),
+    "skv_append_decode_attn_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
+                                          _I, _F, _I, _I, _P, _Z, _I, _I, _I, _I, _P]),
     "skv_decode_attn_paged": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I,
                                    _I, _P, _Z, _I, _I, _I, _P]),
 }

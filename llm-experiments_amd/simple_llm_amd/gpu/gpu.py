@@ -19,6 +19,7 @@ from .gpu_kv_cache import (
     decode_attention,
     decode_plan,
     kv_cache_append,
+    kv_cache_append_attend,
     kv_cache_create,
     kv_cache_prefill,
     kv_cache_reset,
@@ -76,6 +77,7 @@ __all__ = [
     "kv_cache_update",
     "attention_with_kv_cache",
     "kv_cache_append",
+    "kv_cache_append_attend",
     "kv_cache_prefill",
     "kv_cache_set_block_table",
     "decode_attention",

@@ -292,6 +292,68 @@ def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.T
     _lib.check(rc, "skv_decode_attn")
 
 
+def kv_cache_append_attend(ctx: GPUContext, cache: KVCache, layer_idx: int, new_k: torch.Tensor,
+                           new_v: torch.Tensor, q: torch.Tensor, out: torch.Tensor,
+                           scale: Optional[float] = None,
+                           max_len: Optional[int] = None) -> np.ndarray:
+    """kv_cache_append followed by decode_attention in one call (extension).
+
+    Appends new_k/new_v ([batch_size, n_kv_heads, head_dim], or flat) at each
+    sequence's fill (full sequences are skipped), then attends q
+    ([batch_size, n_heads, head_dim]) over the fills including the new token,
+    writing out. The same results as the two calls, without the separate
+    append launch (skv_append_decode_attn). max_len bounds the fills after
+    the append (default: the host mirror's). Returns the new fills.
+    """
+    _check_layer(cache, layer_idx)
+    layer = cache.layers[layer_idx]
+    dev = layer.lens.device
+    e_kv = cache.n_kv_heads * cache.head_dim
+    for t, n in ((new_k, "new_k"), (new_v, "new_v")):
+        _check_tensor(t, n, dev)
+        if t.numel() != cache.batch_size * e_kv:
+            raise ValueError(f"{n} must hold batch_size*n_kv_heads*head_dim = "
+                             f"{cache.batch_size * e_kv} elements, got {t.numel()}")
+    if new_k.dtype != new_v.dtype:
+        raise ValueError("new_k and new_v must share a dtype")
+    _check_tensor(q, "q_new", dev)
+    _check_tensor(out, "output", dev)
+    e_q = cache.n_heads * cache.head_dim
+    if q.numel() != cache.batch_size * e_q or out.numel() != cache.batch_size * e_q:
+        raise ValueError(f"q_new/output must hold batch_size*n_heads*head_dim = "
+                         f"{cache.batch_size * e_q} elements")
+    batch_count(ctx)
+    cap = cache.block_table.shape[1] * cache.block_size if cache.paged else cache.max_seq_len
+    after = np.where(layer.host_lens < cap, layer.host_lens + 1, layer.host_lens)
+    if max_len is None:
+        max_len = int(after.max())
+    total = int(np.minimum(after, max_len).sum())
+    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_kv_heads, max_len, total)
+    L = _lib.lib()
+    need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
+    ws = _workspace(ctx, need)
+    sc = float(scale) if scale is not None else 1.0 / float(np.sqrt(cache.head_dim))
+    stream = _lib.stream_handle(dev)
+    cdt, idt = _lib.dtype_code(cache.dtype), _lib.dtype_code(new_k.dtype)
+    qdt, odt = _lib.dtype_code(q.dtype), _lib.dtype_code(out.dtype)
+    kc, vc = layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr()
+    if cache.paged:
+        rc = L.skv_append_decode_attn_paged(
+            out.data_ptr(), q.data_ptr(), kc, vc, new_k.data_ptr(), new_v.data_ptr(),
+            layer.lens.data_ptr(), cache.block_table.data_ptr(), cache.block_table.shape[1],
+            cache.block_size, cache.batch_size, cache.n_heads, cache.n_kv_heads, cache.head_dim,
+            sc, chunk, nchunks, ws.data_ptr(), ws.numel(), cdt, idt, qdt, odt, stream)
+    else:
+        rc = L.skv_append_decode_attn(
+            out.data_ptr(), q.data_ptr(), kc, vc, new_k.data_ptr(), new_v.data_ptr(),
+            layer.lens.data_ptr(), cache.batch_size, cache.n_heads, cache.n_kv_heads,
+            cache.head_dim, cache.max_seq_len, sc, chunk, nchunks, ws.data_ptr(), ws.numel(), cdt,
+            idt, qdt, odt, stream)
+    _lib.check(rc, "skv_append_decode_attn")
+    layer.host_lens = after
+    return after.copy()
+
+
 def attention_with_kv_cache(ctx: GPUContext, cache: KVCache, layer_idx: int, q_new: GPUBuffer2D,
                             output: GPUBuffer2D) -> None:
     """Attention of the newest query over the cached K/V (reference :194-289).

@@ -421,3 +421,65 @@ def test_decode_full_size_c4_sampled(gpu_ctx):
         np.testing.assert_array_equal(kh[fill, 0], ko.bf16_round(kn[b, h]))
         want = ko.decode_attention(q[b:b + 1, h:h + 1], kh[None], vh[None], [fill + 1])
         assert rel_err(got[b:b + 1, h:h + 1], want) < 1e-4
+
+
+# ---------------------------------------------------------------------------
+# Fused append + decode attention (skv_append_decode_attn)
+# ---------------------------------------------------------------------------
+
+FUSED_CASES = [
+    # B, T, Hq, Hkv, D, cache dtype, input dtype, paged
+    (8, 300, 8, 8, 64, torch.float32, torch.float32, False),      # C2 head shape
+    (4, 600, 16, 16, 128, torch.bfloat16, torch.float32, False),  # C4 head shape, fp32 input
+    (6, 400, 32, 8, 128, torch.bfloat16, torch.bfloat16, True),   # C5 GQA paged
+    (3, 200, 16, 2, 64, torch.bfloat16, torch.float32, False),    # G = 8
+    (16, 128, 12, 12, 64, torch.float32, torch.float32, False),   # C3 head shape
+]
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,D,cdt,idt,paged", FUSED_CASES)
+def test_append_attend_equals_append_then_attend(gpu_ctx, B, T, Hq, Hkv, D, cdt, idt, paged):
+    """Three steps of the fused call against skv_append + skv_decode_attn on a
+    copy of the same cache: bit-identical caches and fills, outputs equal to
+    fp32 rounding (the new token enters the online softmax in its own step),
+    and against the oracle. One sequence starts empty and one full (skipped)."""
+    banner(f"fused append+attend B={B} T={T} Hq={Hq} Hkv={Hkv} D={D} {cdt} in={idt} "
+           f"paged={paged}")
+    gpu = _gpu()
+    rng = np.random.default_rng(B * 31 + T)
+    lens = rng.integers(1, T - 4, B)
+    lens[0], lens[-1] = 0, T  # an empty sequence and a full one
+    ca, k, v, _ = _filled_cache(gpu, gpu_ctx, np.random.default_rng(7), B, T, Hq, Hkv, D, cdt,
+                                lens, paged)
+    cb, _, _, _ = _filled_cache(gpu, gpu_ctx, np.random.default_rng(7), B, T, Hq, Hkv, D, cdt,
+                                lens, paged)
+    kw, vw = k.copy(), v.copy()
+    fills = lens.copy()
+    for step in range(3):
+        kn = rng.standard_normal((B, Hkv, D)).astype(np.float32)
+        vn = rng.standard_normal((B, Hkv, D)).astype(np.float32)
+        q = rng.standard_normal((B, Hq, D)).astype(np.float32)
+        out_a = torch.empty((B, Hq, D), device="cuda")
+        out_b = torch.empty_like(out_a)
+        gpu.kv_cache_append(gpu_ctx, ca, 0, to_dev(kn, idt), to_dev(vn, idt))
+        gpu.decode_attention(gpu_ctx, ca, 0, to_dev(q), out_a)
+        got_fills = gpu.kv_cache_append_attend(gpu_ctx, cb, 0, to_dev(kn, idt), to_dev(vn, idt),
+                                               to_dev(q), out_b)
+        # the oracle's view: the same append rule and rounding
+        knr = ko.bf16_round(kn) if (cdt == torch.bfloat16 or idt == torch.bfloat16) else kn
+        vnr = ko.bf16_round(vn) if (cdt == torch.bfloat16 or idt == torch.bfloat16) else vn
+        for b in range(B):
+            if fills[b] < T:
+                kw[b, fills[b]], vw[b, fills[b]] = knr[b], vnr[b]
+                fills[b] += 1
+        np.testing.assert_array_equal(got_fills, fills)
+        np.testing.assert_array_equal(cb.layers[0].lens.cpu().numpy(), fills)
+        np.testing.assert_array_equal(ca.layers[0].lens.cpu().numpy(), fills)
+        ka, va = cache_host(ca.layers[0], ca)
+        kb_, vb_ = cache_host(cb.layers[0], cb)
+        np.testing.assert_array_equal(ka, kb_)
+        np.testing.assert_array_equal(va, vb_)
+        a_, b_ = out_a.cpu().numpy(), out_b.cpu().numpy()
+        assert rel_err(b_, a_) < 1e-6, step
+        want = ko.decode_attention(q, kw, vw, fills)
+        assert rel_err(b_, want) < 1e-4, step
