@@ -6,15 +6,17 @@ accumulation, filled to 32000 with N(0,1) K/V. One step = the append of one
 new k/v row per sequence into the cache, then single-query attention of
 every sequence over its filled prefix (QK^T, softmax, PV): the reference's
 kv_cache_update + attention_with_kv_cache
-(simple-llm/src/gpu/gpu_kv_cache.py:113-186, 194-289), driven through this
-build's drop-in API. The timed steps go 32000 -> 32000+K filled positions
+(simple-llm/src/gpu/gpu_kv_cache.py:113-186, 194-289), run through this
+build's kv_cache_append_attend, which computes exactly that pair in one call
+(the new token is written and attended inside the attention's first pass). The timed steps go 32000 -> 32000+K filled positions
 (the cache is rewound to 32000 after warm-up), exactly as the config states
 for K = 256.
 
 Output: one JSON line (rank 0) with
   value      decode tokens/s = B * K / wall time of the K timed steps
-  roofline   decode attention (split-K pass 1 + merge pass 2, bracketed by
-             HIP events on the launch stream) against 8 TB/s HBM:
+  roofline   the step's fused append + decode attention (split-K pass 1 +
+             merge pass 2, bracketed by HIP events on the launch stream)
+             against 8 TB/s HBM:
              achieved = algorithmic bytes per call / mean call time, where
              bytes = sum_b 2*H_kv*L_b*D*2 (K and V rows read) + H_q*D*(4+4)
              (q read, out written); traffic = HBM bytes per call measured by
@@ -391,10 +393,10 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
         layer.host_lens = v.astype(np.int64).copy()
 
     def step(i, ev=None):
-        gpu.kv_cache_append(ctx, cache, 0, k_all[i], v_all[i])
         if ev is not None:
             ev[0].record()
-        gpu.decode_attention(ctx, cache, 0, q_all[i], out, max_len=max_len)
+        gpu.kv_cache_append_attend(ctx, cache, 0, k_all[i], v_all[i], q_all[i], out,
+                                   max_len=max_len)
         if ev is not None:
             ev[1].record()
 
@@ -424,7 +426,7 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
                           for f in fills]))
     mean_s = float(ms.mean()) * 1e-3
     chunk, n_chunks = gpu.decode_plan(ctx, B, Hkv, max_len, int(lens0.sum()))
-    roof = {"kernel": "decode attention (k_decode_partial + k_decode_merge)", "bound": "hbm",
+    roof = {"kernel": "append + decode attention (k_decode_partial + k_decode_merge)", "bound": "hbm",
             "achieved": byts / mean_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": byts / mean_s / 1e9 / HBM_PEAK_GBS, "traffic": None,
             "mean_call_us": mean_s * 1e6, "algorithmic_bytes_per_call": byts,
@@ -713,10 +715,10 @@ def main():
     max_len = FILL + args.steps  # split-K plan sized for the longest step
 
     def step(i, ev=None):
-        gpu.kv_cache_append(ctx, cache, 0, k_all[i], v_all[i])
         if ev is not None:
             ev[0].record()
-        gpu.decode_attention(ctx, cache, 0, q_all[i], out, max_len=max_len)
+        gpu.kv_cache_append_attend(ctx, cache, 0, k_all[i], v_all[i], q_all[i], out,
+                                   max_len=max_len)
         if ev is not None:
             ev[1].record()
 
@@ -774,7 +776,7 @@ def main():
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "decode attention (k_decode_partial + k_decode_merge)",
+            "kernel": "append + decode attention (k_decode_partial + k_decode_merge)",
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,

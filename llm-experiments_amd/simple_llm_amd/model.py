@@ -12,7 +12,7 @@ projections, tanh GELU MLP, tied logits, positional table of
 jax_backend.py:25-33). One decode step runs every sequence's next token
 through all layers as HIP kernels of libskv.so: embedding + position,
 fused q/k/v projection (the LayerNorm before it folded into its reads), the
-cache append (skv_append), decode attention (skv_decode_attn), output
+cache append and decode attention in one call (skv_append_decode_attn), output
 projection with residual, MLP (LayerNorm folded in, GELU, residual), tied
 logits and the next token: skv_argmax when greedy (temperature 0, the
 reference's jnp.argmax branch, jax_backend.py:466-469), otherwise skv_sample
@@ -230,11 +230,11 @@ class TransformerModel:
             chk(L.skv_linear(qkv, x, lw["wqkv_t"].data_ptr(), None, None, lw["g1"].data_ptr(),
                              lw["be1"].data_ptr(), 1e-5, B, 3 * d, d, 0, d, lw_ws, lw_n, s),
                 "skv_linear")
-            chk(L.skv_append(kc, vc, k_ptr, v_ptr, layer.lens.data_ptr(), B, H, D, T, cdt,
-                             _lib.F32, s), "skv_append")
-            chk(L.skv_decode_attn(attn, q_ptr, kc, vc, layer.lens.data_ptr(), B, H, H, D, T, scale,
-                                  chunk, n_chunks, ws.data_ptr(), ws.numel(), cdt, _lib.F32,
-                                  _lib.F32, s), "skv_decode_attn")
+            # append k, v at each sequence's fill and attend [0, fill] (one call)
+            chk(L.skv_append_decode_attn(attn, q_ptr, kc, vc, k_ptr, v_ptr, layer.lens.data_ptr(),
+                                         B, H, H, D, T, scale, chunk, n_chunks, ws.data_ptr(),
+                                         ws.numel(), cdt, _lib.F32, _lib.F32, _lib.F32, s),
+                "skv_append_decode_attn")
             # x += attn . Wo
             chk(L.skv_linear(x, attn, lw["wo_t"].data_ptr(), None, x, None, None, 0.0, B, d, d, 0,
                              0, lw_ws, lw_n, s), "skv_linear")
