@@ -240,8 +240,8 @@ int skv_linear(float* y, const float* x, const float* w_t, const float* bias,
 /* Workspace skv_linear can use for these sizes (0: it never splits them). */
 size_t skv_linear_workspace_bytes(int M, int N, int K);
 
-/* Workspace of skv_argmax (per-slice candidates and counters); zero it
- * once before its first use; not shared by concurrent calls. */
+/* Workspace of skv_argmax: per-slice candidates, 0 bytes when N <= 2048
+ * (ws may then be NULL); calls that share it must be stream ordered. */
 size_t skv_argmax_workspace_bytes(int M, int N);
 
 /* out[m] = index of the largest x[m, :], the first on ties

@@ -26,26 +26,6 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Split reductions: every workgroup of a group writes its partial result,
-// then arrives on the group's counter; exactly one workgroup (the last to
-// arrive) sees true, after all partials are visible to it, and resets the
-// counter to zero for the next call. Counters must be zero before the first
-// call. The last workgroup sums the partials in a fixed order, so results do
-// not depend on arrival order.
-__device__ __forceinline__ bool last_arrival(int* counter, int n) {
-  __shared__ int is_last;
-  __syncthreads();  // this workgroup's partial stores are issued
-  if (threadIdx.x == 0) {
-    __threadfence();  // release them device-wide (across XCDs)
-    const int prev = atomicAdd(counter, 1);
-    is_last = prev == n - 1;
-    if (is_last) atomicExch(counter, 0);
-  }
-  __syncthreads();
-  if (is_last) __threadfence();  // acquire the other workgroups' partials
-  return is_last != 0;
-}
-
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -159,13 +139,25 @@ struct LinArgs {
 // 16 wavefronts of 12 steps) runs in further passes.
 //
 // With LN, each x row is layer-normalized as it is read: the mean and 1/std
-// of the workgroup's rows are computed first (one pass over values shifted by
+// of the workgroup's rows are computed first (sums of the values shifted by
 // the row's first element, var = E[(x-c)^2] - E[x-c]^2), which takes the
-// LayerNorm launch out of the step.
+// LayerNorm launch out of the step. When one pass of the workgroup covers all
+// of K, its wavefronts already hold every x value of their rows, and the sums
+// come from those registers (reduced across lanes and then wavefronts through
+// LDS); otherwise a separate pass reads the rows again. Skipping that second
+// read of x took the 16 x 768 -> 2304 projection from 9.4 to 7.4 us.
+// Passes of more than 4 steps run with 8 wavefronts, which leaves each up to
+// 256 registers.
 template <int TILES, int STEPS, bool LN>
-__global__ __launch_bounds__(kLinMaxWaves * 64) void k_linear(LinArgs a) {
-  extern __shared__ float red[];  // [W][TILES][64][4] partial tiles
+__global__ __launch_bounds__(STEPS > 4 ? 512 : kLinMaxWaves * 64) void k_linear(LinArgs a) {
+  extern __shared__ float red[];  // [W][TILES][4][64] partial tiles
   __shared__ float stat[kLinRowsPerBlock][2];
+  // Row statistics from the registers when a pass covers all of K, for one
+  // row tile and passes of 4+ steps: with fewer, the x rows are short (the
+  // second read costs little) and the cross-wavefront sum of 16 wavefronts
+  // costs more (16 x 256 -> 768: 0.25 us slower, measured on MI355X).
+  constexpr bool kRegStats = LN && TILES == 1 && STEPS >= 4;
+  __shared__ float lsum[kRegStats ? kLinMaxWaves : 1][16][2];
   const int NW = blockDim.x >> 6;
   const int n0 = blockIdx.x * 16;
   const int m0 = blockIdx.y * kLinRowsPerBlock;
@@ -175,36 +167,43 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void k_linear(LinArgs a) {
   const int n = n0 + lr;
   const bool n_ok = n < a.N;
   const float* wrow = a.wt + (size_t)(n_ok ? n : 0) * a.K;
-  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
   // Loads read a clamped, in-bounds address and select zero afterwards: a
   // load inside a condition cannot be hoisted, and the compiler then splits
   // it into four guarded 4-byte loads. K % 4 == 0, so K - 4 starts a float4.
+  // The selects come after the scheduling barrier below, so that no use of a
+  // loaded value sits among the loads: with one there, the scheduler may wait
+  // for each load before issuing the next to save registers (seen at 6 steps:
+  // 12 round trips in series).
   const int klast = a.K - 4;
-  auto load4 = [](const float* p, bool ok, float4 z) {
-    const float4 v = *reinterpret_cast<const float4*>(p);
-    return ok ? v : z;
+  auto load4 = [](const float* p) { return *reinterpret_cast<const float4*>(p); };
+  auto keep = [](float4& v, bool ok) {
+    if (!ok) v = make_float4(0.f, 0.f, 0.f, 0.f);
   };
 
-  // Epilogue thread (t, ll) = (wave, lane) of the first TILES wavefronts:
-  // its bias and residual values are loaded now, with everything else.
-  const bool epi = wave < TILES && wave * 16 < rows && n0 + (l & 15) < a.N;
+  // Epilogue: thread (wave, l) finishes the accumulator slots p = wave + j NW
+  // (j = 0..3, p < 4 TILES) of lane l: row tile t = p / 4, slot i = p % 4,
+  // row m0 + 16 t + 4 (l / 16) + i, column nn. Every wavefront takes part
+  // (NW >= TILES), and its bias and residual values are loaded now, with
+  // everything else.
   const bool partial = a.part != nullptr;  // split K: raw sums, no epilogue here
   const int nn = n0 + (l & 15);
+  const bool n_in = nn < a.N;
+  auto slot_row = [&](int p) { return m0 + 16 * (p >> 2) + 4 * (l >> 4) + (p & 3); };
   float bias_v = 0.f, resv[4] = {0.f, 0.f, 0.f, 0.f};
   size_t oidx[4] = {0, 0, 0, 0};
-  if (epi && !partial) {
+  if (n_in && !partial) {
     if (a.bias) bias_v = a.bias[nn];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = m0 + wave * 16 + 4 * (l >> 4) + i;
-      if (m >= a.M) continue;
+    for (int j = 0; j < 4; ++j) {
+      const int p = wave + j * NW, m = slot_row(p);
+      if (p >= 4 * TILES || m >= a.M) continue;
       if (a.split > 0) {
         const int seg = nn / a.split;
-        oidx[i] = ((size_t)seg * a.M + m) * a.split + (nn - seg * a.split);
+        oidx[j] = ((size_t)seg * a.M + m) * a.split + (nn - seg * a.split);
       } else {
-        oidx[i] = (size_t)m * a.N + nn;
+        oidx[j] = (size_t)m * a.N + nn;
       }
-      if (a.res) resv[i] = a.res[oidx[i]];
+      if (a.res) resv[j] = a.res[oidx[j]];
     }
   }
 
@@ -215,34 +214,74 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void k_linear(LinArgs a) {
   const int pass_k = NW * STEPS * 16;
   const int kz0 = blockIdx.z * a.kz;
   const int kz1 = min(a.K, kz0 + a.kz);
+  // LN statistics from the registers (one row tile): one pass holds all of K
+  const bool whole = kRegStats && kz0 == 0 && kz1 == a.K && pass_k >= a.K;
+  const float cshift = kRegStats ? a.x[(size_t)(m0 + min(lr, rows - 1)) * a.K] : 0.f;
   for (int kp = kz0; kp < kz1; kp += pass_k) {
     const int kb = kp + wave * STEPS * 16 + 4 * lk;
     float4 w[STEPS], xv[TILES][STEPS], g[LN ? STEPS : 1], be[LN ? STEPS : 1];
 #pragma unroll
-    for (int st = 0; st < STEPS; ++st) {
-      const int kk = kb + 16 * st;
-      w[st] = load4(wrow + min(kk, klast), n_ok && kk < kz1, zero4);
-    }
+    for (int st = 0; st < STEPS; ++st) w[st] = load4(wrow + min(kb + 16 * st, klast));
 #pragma unroll
     for (int t = 0; t < TILES; ++t)
 #pragma unroll
-      for (int st = 0; st < STEPS; ++st) {
-        const int r = t * 16 + lr, kk = kb + 16 * st;
-        xv[t][st] = load4(a.x + (size_t)(m0 + min(r, rows - 1)) * a.K + min(kk, klast),
-                          r < rows && kk < kz1, zero4);
-      }
+      for (int st = 0; st < STEPS; ++st)
+        xv[t][st] = load4(a.x + (size_t)(m0 + min(t * 16 + lr, rows - 1)) * a.K +
+                          min(kb + 16 * st, klast));
     if constexpr (LN) {
 #pragma unroll
       for (int st = 0; st < STEPS; ++st) {
-        const int kk = kb + 16 * st;
-        g[st] = load4(a.ln_g + min(kk, klast), kk < kz1, zero4);
-        be[st] = load4(a.ln_b + min(kk, klast), kk < kz1, zero4);
+        g[st] = load4(a.ln_g + min(kb + 16 * st, klast));
+        be[st] = load4(a.ln_b + min(kb + 16 * st, klast));
       }
     }
     // keep every load above issued before the first use below
     __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+      const bool kin = kb + 16 * st < kz1;
+      keep(w[st], n_ok && kin);
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) keep(xv[t][st], t * 16 + lr < rows && kin);
+      if constexpr (LN) {
+        keep(g[st], kin);
+        keep(be[st], kin);
+      }
+    }
     if constexpr (LN) {
-      if (kp == kz0) {
+      if (kp == kz0 && whole) {
+        // lanes lr + 16 j (j = 0..3) of every wavefront hold row lr
+        float su = 0.f, sq = 0.f;
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+          if (kb + 16 * st >= kz1) continue;
+          const float4 v = xv[0][st];
+          const float d0 = v.x - cshift, d1 = v.y - cshift, d2 = v.z - cshift, d3 = v.w - cshift;
+          su += (d0 + d1) + (d2 + d3);
+          sq += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+        su += __shfl_xor(su, 16);
+        sq += __shfl_xor(sq, 16);
+        su += __shfl_xor(su, 32);
+        sq += __shfl_xor(sq, 32);
+        if (lk == 0) {
+          lsum[wave][lr][0] = su;
+          lsum[wave][lr][1] = sq;
+        }
+        __syncthreads();
+        if (wave == 0 && lk == 0) {
+          su = 0.f;
+          sq = 0.f;
+          for (int wv = 0; wv < NW; ++wv) {
+            su += lsum[wv][lr][0];
+            sq += lsum[wv][lr][1];
+          }
+          const float ms = su / a.K;
+          stat[lr][0] = cshift + ms;
+          stat[lr][1] = 1.f / sqrtf(fmaxf(sq / a.K - ms * ms, 0.f) + a.ln_eps);
+        }
+        __syncthreads();
+      } else if (kp == kz0) {
         // row statistics over the whole row, one wavefront per row
         for (int r = wave; r < rows; r += NW) {
           const float* xr = a.x + (size_t)(m0 + r) * a.K;
@@ -289,25 +328,25 @@ __global__ __launch_bounds__(kLinMaxWaves * 64) void k_linear(LinArgs a) {
         acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t][st].w, w[st].w, acc[t], 0, 0, 0);
       }
   }
+  // slot p of every wavefront's tile, lane-contiguous (no bank conflicts)
 #pragma unroll
   for (int t = 0; t < TILES; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[((wave * TILES + t) * 64 + l) * 4 + i] = acc[t][i];
+    for (int i = 0; i < 4; ++i) red[((wave * TILES + t) * 4 + i) * 64 + l] = acc[t][i];
   __syncthreads();
-  // thread -> (row tile t = wave, lane l): sums the wavefronts' partial tiles
-  if (!epi) return;
+  if (!n_in) return;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + wave * 16 + 4 * (l >> 4) + i;
-    if (m >= a.M) continue;
-    float v = bias_v;
-    for (int wv = 0; wv < NW; ++wv) v += red[((wv * TILES + wave) * 64 + l) * 4 + i];
+  for (int j = 0; j < 4; ++j) {
+    const int p = wave + j * NW, m = slot_row(p);
+    if (p >= 4 * TILES || m >= a.M) continue;
+    float v = bias_v;  // then the wavefronts' partial sums, in order
+    for (int wv = 0; wv < NW; ++wv) v += red[(wv * TILES * 4 + p) * 64 + l];
     if (partial) {
       a.part[((size_t)blockIdx.z * a.M + m) * a.N + nn] = v;
       continue;
     }
     if (a.act == 1) v = gelu_tanh(v);
-    a.y[oidx[i]] = v + resv[i];
+    a.y[oidx[j]] = v + resv[j];
   }
 }
 
@@ -356,47 +395,71 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
   }
 }
 
-constexpr int kArgCols = 2048;  // columns per argmax workgroup
+constexpr int kArgCols = 2048;  // columns per argmax workgroup (8 per thread)
 
-// grid (slices, M): each workgroup finds the first maximum of its slice of
-// row m; the last slice to arrive picks the winner over the slices in order.
-__global__ __launch_bounds__(256) void k_argmax(int32_t* __restrict__ out,
-                                                const float* __restrict__ x, int n,
-                                                float* __restrict__ cand_v,
-                                                int* __restrict__ cand_i,
-                                                int* __restrict__ counters) {
-  __shared__ float sv[4];
-  __shared__ int si[4];
-  const int sl = blockIdx.x, m = blockIdx.y, ns = gridDim.x;
-  const float* xr = x + (size_t)m * n;
-  const int c0 = sl * kArgCols, c1 = min(n, c0 + kArgCols);
-  float bv = -INFINITY;
-  int bi = n;  // larger than any index: loses every tie
-  for (int j = c0 + threadIdx.x; j < c1; j += 256) better(bv, bi, xr[j], j);
+__device__ __forceinline__ void block_better(float& bv, int& bi) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     const float ov = __shfl_xor(bv, o);
     const int oi = __shfl_xor(bi, o);
     better(bv, bi, ov, oi);
   }
+}
+
+// grid (slices, M): each workgroup finds the first maximum of its 2048-column
+// slice of row m, all eight loads of a thread in flight at once. With one
+// slice the winner is the answer; otherwise it goes to the candidate arrays
+// and k_argmax_pick chooses among the slices in a second launch. (A last-
+// arriving workgroup could pick instead, but its device-scope fence costs
+// every one of the ~400 workgroups an L2 write-back, serialized per XCD:
+// 18 us per call against 6 us for the two launches, measured on MI355X.)
+__global__ __launch_bounds__(256) void k_argmax(int32_t* __restrict__ out,
+                                                const float* __restrict__ x, int n,
+                                                float* __restrict__ cand_v,
+                                                int* __restrict__ cand_i) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int sl = blockIdx.x, m = blockIdx.y, ns = gridDim.x;
+  const float* xr = x + (size_t)m * n;
+  const int c0 = sl * kArgCols, c1 = min(n, c0 + kArgCols);
+  float v[kArgCols / 256];
+#pragma unroll
+  for (int u = 0; u < kArgCols / 256; ++u) v[u] = xr[min(c0 + (int)threadIdx.x + 256 * u, c1 - 1)];
+  float bv = -INFINITY;
+  int bi = n;  // larger than any index: loses every tie
+#pragma unroll
+  for (int u = 0; u < kArgCols / 256; ++u) {
+    const int j = c0 + threadIdx.x + 256 * u;
+    if (j < c1) better(bv, bi, v[u], j);
+  }
+  block_better(bv, bi);
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     sv[w] = bv;
     si[w] = bi;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int i = 1; i < 4; ++i) better(bv, bi, sv[i], si[i]);
+  if (threadIdx.x != 0) return;
+  for (int i = 1; i < 4; ++i) better(bv, bi, sv[i], si[i]);
+  if (ns == 1) {
+    out[m] = bi < n ? bi : 0;  // a row of NaN only: token 0
+  } else {
     cand_v[(size_t)m * ns + sl] = bv;
     cand_i[(size_t)m * ns + sl] = bi;
   }
-  if (!last_arrival(counters + m, ns)) return;
-  if (threadIdx.x == 0) {
-    float v = -INFINITY;
-    int i = n;
-    for (int k = 0; k < ns; ++k) better(v, i, cand_v[(size_t)m * ns + k], cand_i[(size_t)m * ns + k]);
-    out[m] = i < n ? i : 0;  // a row of NaN/-inf only: token 0
-  }
+}
+
+// one wavefront per row: the first maximum over the slices' candidates
+__global__ __launch_bounds__(64) void k_argmax_pick(int32_t* __restrict__ out,
+                                                    const float* __restrict__ cand_v,
+                                                    const int* __restrict__ cand_i, int ns, int n) {
+  const int m = blockIdx.x;
+  float bv = -INFINITY;
+  int bi = n;
+  for (int k = threadIdx.x; k < ns; k += 64)
+    better(bv, bi, cand_v[(size_t)m * ns + k], cand_i[(size_t)m * ns + k]);
+  block_better(bv, bi);
+  if (threadIdx.x == 0) out[m] = bi < n ? bi : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -476,21 +539,31 @@ extern "C" int skv_linear(float* y, const float* x, const float* w_t, const floa
             split_cols, S > 1 ? kz_steps * 16 : K, S > 1 ? static_cast<float*>(ws) : nullptr};
   const int col_tiles = (N + 15) / 16;
   const int tiles = M >= kLinRowsPerBlock ? 4 : (M + 15) / 16;
-  // Wavefronts per workgroup: narrow layers (few 16-column tiles, one CU
-  // each) split their K range over 16 wavefronts; the wide logits use 8,
-  // since every CU holds several of their workgroups.
+  // Wavefronts per workgroup and 16-k steps per wavefront and pass, measured
+  // on MI355X:
+  //  - one row tile (M <= 16) and 512 < K <= 768: 8 wavefronts of 6 steps,
+  //    one pass (16 x 768 -> 768: 5.6 -> 4.8 us; the 16 x 768 -> 50304
+  //    logits: 38.8 -> 36.4 us);
+  //  - other narrow layers (few 16-column tiles, one CU each) split their K
+  //    range over up to 16 wavefronts of at most 4 steps: deeper passes gain
+  //    nothing, since a CU's weight stream is capped;
+  //  - the wide logits with more row tiles use 8 wavefronts of 3 steps (3
+  //    beat 4 and 12 by keeping more workgroups resident).
+  // Steps never exceed what fits the registers without spilling (checked
+  // with the compiler's resource report: per step, w and x take
+  // (1 + TILES) * 4 registers and LN's gamma and beta 8 more).
   const bool wide = col_tiles >= 1024;
-  int nw = wide ? 8 : (kz_steps < kLinMaxWaves ? kz_steps : kLinMaxWaves);
-  nw = nw < tiles ? tiles : nw;  // wavefront t writes row tile t in the epilogue
   const bool ln = ln_gamma != nullptr;
-  // Steps per pass: at most 4 (measured on MI355X: deeper passes gain
-  // nothing on narrow layers, since a CU's weight stream is capped, and on the
-  // wide logits 3 beat 4 and 12 by keeping more workgroups resident), and no
-  // more than fit the registers without spilling (checked with the
-  // compiler's resource report: per step, w and x take (1 + TILES) * 4
-  // registers and LN's gamma and beta 8 more).
-  const int max_steps = wide ? 3 : ln ? (tiles == 1 ? 4 : tiles == 2 ? 3 : 2) : 4;
-  int steps = (kz_steps + nw - 1) / nw;
+  int nw, max_steps;
+  if (tiles == 1 && kz_steps > 32 && kz_steps <= 48) {
+    nw = 8;  // 6 steps (5 would have no kernel; the extra steps are masked)
+    max_steps = 6;
+  } else {
+    nw = wide ? 8 : (kz_steps < kLinMaxWaves ? kz_steps : kLinMaxWaves);
+    max_steps = wide ? 3 : ln ? (tiles == 1 ? 4 : tiles == 2 ? 3 : 2) : (tiles == 4 ? 3 : 4);
+  }
+  nw = nw < tiles ? tiles : nw;  // the epilogue gives each wavefront at most 4 of the 4 TILES slots
+  int steps = max_steps == 6 ? 6 : (kz_steps + nw - 1) / nw;
   steps = steps > max_steps ? max_steps : steps;
   dim3 grid(col_tiles, (M + kLinRowsPerBlock - 1) / kLinRowsPerBlock, S);
   const size_t lds = (size_t)nw * tiles * 64 * 4 * sizeof(float);
@@ -502,10 +575,10 @@ extern "C" int skv_linear(float* y, const float* x, const float* w_t, const floa
     launched = true;                                                                      \
   }
 #define SKV_LIN2(T, S_) SKV_LIN(T, S_, false) SKV_LIN(T, S_, true)
-  SKV_LIN2(1, 1) SKV_LIN2(1, 2) SKV_LIN2(1, 3) SKV_LIN2(1, 4)
+  SKV_LIN2(1, 1) SKV_LIN2(1, 2) SKV_LIN2(1, 3) SKV_LIN2(1, 4) SKV_LIN2(1, 6)
   SKV_LIN2(2, 1) SKV_LIN2(2, 2) SKV_LIN2(2, 3) SKV_LIN(2, 4, false)
   SKV_LIN2(3, 1) SKV_LIN2(3, 2) SKV_LIN(3, 3, false) SKV_LIN(3, 4, false)
-  SKV_LIN2(4, 1) SKV_LIN2(4, 2) SKV_LIN(4, 3, false) SKV_LIN(4, 4, false)
+  SKV_LIN2(4, 1) SKV_LIN2(4, 2) SKV_LIN(4, 3, false)
 #undef SKV_LIN2
 #undef SKV_LIN
   if (!launched)
@@ -522,7 +595,7 @@ extern "C" int skv_linear(float* y, const float* x, const float* w_t, const floa
 extern "C" size_t skv_argmax_workspace_bytes(int M, int N) {
   if (M <= 0 || N <= 0) return 0;
   const size_t ns = (N + kArgCols - 1) / kArgCols;
-  return (size_t)M * (2 * ns + 1) * 4;
+  return ns > 1 ? (size_t)M * 2 * ns * 4 : 0;
 }
 
 extern "C" int skv_argmax(int32_t* out, const float* x, int M, int N, void* ws, size_t ws_bytes,
@@ -530,14 +603,14 @@ extern "C" int skv_argmax(int32_t* out, const float* x, int M, int N, void* ws, 
   SKV_REQUIRE(out && x && M > 0 && N > 0, SKV_E_INVALID, "skv_argmax: bad arguments");
   SKV_REQUIRE(M <= 65535, SKV_E_UNSUPPORTED, "skv_argmax: M=%d too large", M);
   const size_t need = skv_argmax_workspace_bytes(M, N);
-  SKV_REQUIRE(ws && ws_bytes >= need, SKV_E_WORKSPACE,
+  SKV_REQUIRE(need == 0 || (ws && ws_bytes >= need), SKV_E_WORKSPACE,
               "skv_argmax: workspace %zu bytes < %zu required", ws_bytes, need);
   const int ns = (N + kArgCols - 1) / kArgCols;
-  int* cnt = static_cast<int*>(ws);  // M counters first, then the candidates
-  float* cv = reinterpret_cast<float*>(cnt + M);
+  float* cv = static_cast<float*>(ws);  // M * ns candidate values, then their indices
   int* ci = reinterpret_cast<int*>(cv + (size_t)M * ns);
-  hipLaunchKernelGGL(k_argmax, dim3(ns, M), dim3(256), 0, (hipStream_t)stream, out, x, N, cv, ci,
-                     cnt);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_argmax, dim3(ns, M), dim3(256), 0, s, out, x, N, cv, ci);
+  if (ns > 1) hipLaunchKernelGGL(k_argmax_pick, dim3(M), dim3(64), 0, s, out, cv, ci, ns, N);
   return check_launch("skv_argmax");
 }
 

@@ -152,6 +152,20 @@ def test_flash_fwd_rejects_bad_arguments():
     assert call(n=0) == _lib.SKV_E_INVALID
 
 
+def test_argmax_workspace_and_rejects():
+    L = _lib.lib()
+    # one 2048-column slice per workgroup; candidates (value, index) per slice
+    # when a row needs more than one
+    assert L.skv_argmax_workspace_bytes(16, 50304) == 16 * 2 * 25 * 4
+    assert L.skv_argmax_workspace_bytes(4, 2048) == 0
+    assert L.skv_argmax_workspace_bytes(0, 10) == 0
+    fake = 4096  # never dereferenced: each call below fails validation first
+    assert L.skv_argmax(fake, fake, 16, 50304, None, 0, None) == _lib.SKV_E_WORKSPACE
+    assert L.skv_argmax(fake, fake, 16, 50304, fake, 16 * 2 * 25 * 4 - 1, None) == \
+        _lib.SKV_E_WORKSPACE
+    assert L.skv_argmax(None, fake, 1, 10, None, 0, None) == _lib.SKV_E_INVALID
+
+
 def test_check_maps_status_to_exceptions():
     L = _lib.lib()
     L.skv_append(None, None, None, None, None, 1, 1, 64, 1, 0, 0, None)

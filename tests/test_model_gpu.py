@@ -156,13 +156,24 @@ def test_argmax_first_index_on_ties(gpu_ctx):
         _lib.check(L.skv_argmax(out.data_ptr(), xd.data_ptr(), 6, 50304, ws.data_ptr(),
                                 ws.numel(), _lib.stream_handle()), "argmax")
         np.testing.assert_array_equal(out.cpu().numpy(), np.argmax(x, axis=1))
-    assert not ws[:6 * 4].any()  # counters reset
-    # a row narrower than one slice
+    # a row narrower than one slice: one launch, no workspace
+    assert L.skv_argmax_workspace_bytes(3, 100) == 0
     small = torch.zeros(3, dtype=torch.int32, device="cuda")
     xs = dev(x[:3, :100])
-    _lib.check(L.skv_argmax(small.data_ptr(), xs.data_ptr(), 3, 100, ws.data_ptr(), ws.numel(),
+    _lib.check(L.skv_argmax(small.data_ptr(), xs.data_ptr(), 3, 100, None, 0,
                             _lib.stream_handle()), "argmax")
     np.testing.assert_array_equal(small.cpu().numpy(), np.argmax(x[:3, :100], axis=1))
+    # NaN never wins; a row of NaN only gives token 0; -inf ties take the first index
+    y = np.full((3, 5000), -np.inf, np.float32)
+    y[0, :] = np.nan
+    y[1, 2500:] = np.nan
+    y[2, 4000] = np.nan
+    y[2, 4001] = -1.0
+    got = torch.zeros(3, dtype=torch.int32, device="cuda")
+    wy = torch.zeros(L.skv_argmax_workspace_bytes(3, 5000), dtype=torch.uint8, device="cuda")
+    _lib.check(L.skv_argmax(got.data_ptr(), dev(y).data_ptr(), 3, 5000, wy.data_ptr(), wy.numel(),
+                            _lib.stream_handle()), "argmax")
+    assert got.cpu().tolist() == [0, 0, 4001]
 
 
 def test_next_tokens(gpu_ctx):
