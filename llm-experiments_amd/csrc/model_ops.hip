@@ -148,9 +148,9 @@ struct LinArgs {
 // read of x took the 16 x 768 -> 2304 projection from 9.4 to 7.4 us.
 // Passes of more than 4 steps run with 8 wavefronts, which leaves each up to
 // 256 registers.
-template <int TILES, int STEPS, bool LN>
+template <int TILES, int STEPS, bool LN, bool SPREAD>
 __global__ __launch_bounds__(STEPS > 4 ? 512 : kLinMaxWaves * 64) void k_linear(LinArgs a) {
-  extern __shared__ float red[];  // [W][TILES][4][64] partial tiles
+  extern __shared__ float red[];  // partial tiles of the W wavefronts (layout below)
   __shared__ float stat[kLinRowsPerBlock][2];
   // Row statistics from the registers when a pass covers all of K, for one
   // row tile and passes of 4+ steps: with fewer, the x rows are short (the
@@ -180,22 +180,30 @@ __global__ __launch_bounds__(STEPS > 4 ? 512 : kLinMaxWaves * 64) void k_linear(
     if (!ok) v = make_float4(0.f, 0.f, 0.f, 0.f);
   };
 
-  // Epilogue: thread (wave, l) finishes the accumulator slots p = wave + j NW
-  // (j = 0..3, p < 4 TILES) of lane l: row tile t = p / 4, slot i = p % 4,
-  // row m0 + 16 t + 4 (l / 16) + i, column nn. Every wavefront takes part
-  // (NW >= TILES), and its bias and residual values are loaded now, with
-  // everything else.
+  // Epilogue: thread (wave, l) finishes accumulator slots p (j = 0..3) of
+  // lane l: row tile t = p / 4, slot i = p % 4, row m0 + 16 t + 4 (l / 16) + i,
+  // column nn. SPREAD (the host sets it for M > 4) spreads the slots over
+  // all wavefronts (p = wave + j NW; partials lane-contiguous in LDS,
+  // [W][TILES][4][64]). Otherwise (M <= 4: the valid slots are row tile 0's
+  // first ones anyway) wavefront t < TILES takes row tile t (p = 4 wave + j;
+  // partials [W][TILES][64][4], one 16-byte LDS write per lane). Measured on
+  // MI355X: spreading took C3 (16 rows) from 704 to 674 us per step; the
+  // compact form saved C1 (1 row) 4 us. Each kernel carries one form only (a
+  // runtime choice between the two was slower for both). Bias and residual
+  // values are loaded now, with everything else.
+  constexpr bool spread = SPREAD;
   const bool partial = a.part != nullptr;  // split K: raw sums, no epilogue here
   const int nn = n0 + (l & 15);
   const bool n_in = nn < a.N;
+  auto slot_of = [&](int j) { return spread ? wave + j * NW : 4 * wave + j; };
   auto slot_row = [&](int p) { return m0 + 16 * (p >> 2) + 4 * (l >> 4) + (p & 3); };
   float bias_v = 0.f, resv[4] = {0.f, 0.f, 0.f, 0.f};
   size_t oidx[4] = {0, 0, 0, 0};
-  if (n_in && !partial) {
+  if (n_in && !partial && (spread || wave < TILES)) {
     if (a.bias) bias_v = a.bias[nn];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int p = wave + j * NW, m = slot_row(p);
+      const int p = slot_of(j), m = slot_row(p);
       if (p >= 4 * TILES || m >= a.M) continue;
       if (a.split > 0) {
         const int seg = nn / a.split;
@@ -328,19 +336,22 @@ __global__ __launch_bounds__(STEPS > 4 ? 512 : kLinMaxWaves * 64) void k_linear(
         acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t][st].w, w[st].w, acc[t], 0, 0, 0);
       }
   }
-  // slot p of every wavefront's tile, lane-contiguous (no bank conflicts)
+  auto red_at = [&](int wv, int p) -> float& {
+    return spread ? red[((wv * TILES + (p >> 2)) * 4 + (p & 3)) * 64 + l]
+                   : red[((wv * TILES + (p >> 2)) * 64 + l) * 4 + (p & 3)];
+  };
 #pragma unroll
   for (int t = 0; t < TILES; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[((wave * TILES + t) * 4 + i) * 64 + l] = acc[t][i];
+    for (int i = 0; i < 4; ++i) red_at(wave, 4 * t + i) = acc[t][i];
   __syncthreads();
-  if (!n_in) return;
+  if (!n_in || (!spread && wave >= TILES)) return;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int p = wave + j * NW, m = slot_row(p);
+    const int p = slot_of(j), m = slot_row(p);
     if (p >= 4 * TILES || m >= a.M) continue;
     float v = bias_v;  // then the wavefronts' partial sums, in order
-    for (int wv = 0; wv < NW; ++wv) v += red[(wv * TILES * 4 + p) * 64 + l];
+    for (int wv = 0; wv < NW; ++wv) v += red_at(wv, p);
     if (partial) {
       a.part[((size_t)blockIdx.z * a.M + m) * a.N + nn] = v;
       continue;
@@ -569,16 +580,19 @@ extern "C" int skv_linear(float* y, const float* x, const float* w_t, const floa
   const size_t lds = (size_t)nw * tiles * 64 * 4 * sizeof(float);
   hipStream_t s = (hipStream_t)stream;
   bool launched = false;
-#define SKV_LIN(T, S_, L)                                                                 \
-  if (!launched && tiles == T && steps == S_ && ln == L) {                                \
-    hipLaunchKernelGGL((k_linear<T, S_, L>), grid, dim3(nw * 64), lds, s, a);             \
+  const bool spread = M > 4;  // more than one row tile implies it
+#define SKV_LIN(T, S_, L, SP)                                                             \
+  if (!launched && tiles == T && steps == S_ && ln == L && spread == SP) {                \
+    hipLaunchKernelGGL((k_linear<T, S_, L, SP>), grid, dim3(nw * 64), lds, s, a);         \
     launched = true;                                                                      \
   }
-#define SKV_LIN2(T, S_) SKV_LIN(T, S_, false) SKV_LIN(T, S_, true)
-  SKV_LIN2(1, 1) SKV_LIN2(1, 2) SKV_LIN2(1, 3) SKV_LIN2(1, 4) SKV_LIN2(1, 6)
-  SKV_LIN2(2, 1) SKV_LIN2(2, 2) SKV_LIN2(2, 3) SKV_LIN(2, 4, false)
-  SKV_LIN2(3, 1) SKV_LIN2(3, 2) SKV_LIN(3, 3, false) SKV_LIN(3, 4, false)
-  SKV_LIN2(4, 1) SKV_LIN2(4, 2) SKV_LIN(4, 3, false)
+#define SKV_LIN2(T, S_) SKV_LIN(T, S_, false, true) SKV_LIN(T, S_, true, true)
+#define SKV_LIN1(S_) SKV_LIN2(1, S_) SKV_LIN(1, S_, false, false) SKV_LIN(1, S_, true, false)
+  SKV_LIN1(1) SKV_LIN1(2) SKV_LIN1(3) SKV_LIN1(4) SKV_LIN1(6)
+  SKV_LIN2(2, 1) SKV_LIN2(2, 2) SKV_LIN2(2, 3) SKV_LIN(2, 4, false, true)
+  SKV_LIN2(3, 1) SKV_LIN2(3, 2) SKV_LIN(3, 3, false, true) SKV_LIN(3, 4, false, true)
+  SKV_LIN2(4, 1) SKV_LIN2(4, 2) SKV_LIN(4, 3, false, true)
+#undef SKV_LIN1
 #undef SKV_LIN2
 #undef SKV_LIN
   if (!launched)
