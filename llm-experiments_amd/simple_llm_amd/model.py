@@ -104,8 +104,8 @@ class _Buffers:
         self.ff = torch.zeros((B, mlp), device=dev)
         self.logits = torch.zeros((B, vocab), device=dev)
         self.argmax = torch.zeros(B, dtype=torch.int32, device=dev)
-        # split-argmax workspace: zero-filled once, its arrival counters
-        # return to zero after every call
+        # argmax workspace: the per-slice candidates of rows wider than one
+        # slice (stream ordered, like the step's other buffers)
         L = _lib.lib()
         arg = L.skv_argmax_workspace_bytes(B, vocab)
         self.arg_ws = torch.zeros(max(arg, 4), dtype=torch.uint8, device=dev)
