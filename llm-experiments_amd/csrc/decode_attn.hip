@@ -183,17 +183,50 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
   const int hk = hg * a.hw + hl;
   const int S = a.S;
 
+  // With the prefetching loop (fp32 caches, G = 1) the query rows are loaded
+  // as raw words, two vector loads per head without a branch on q's dtype
+  // (for bf16 the second repeats the first), and converted and scaled only
+  // after the first token group's K/V loads are issued: the q round trip then
+  // overlaps the K/V one instead of preceding it (short pieces, as in a model
+  // step). The other loops convert at once, which keeps one copy of q in
+  // registers.
+  const bool q_bf16 = a.q_dt == SKV_BF16;
   float q[G][EPL];
+  uint32_t qraw[PF ? G : 1][EPL];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const size_t qoff = ((size_t)b * a.Hq + hk * G + h) * D + e0;
-    if constexpr (EPL == 8)
-      load8_f32(a.q, qoff, a.q_dt, q[h]);
-    else  // D = 64
-      load4_f32(a.q, qoff, a.q_dt, q[h]);
+    if constexpr (PF) {
+      const char* qp = static_cast<const char*>(a.q) + qoff * (q_bf16 ? 2 : 4);
+      if constexpr (EPL == 8) {
+        const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(qp);
+        const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(q_bf16 ? qp : qp + 16);
+        qraw[h][0] = w0.x; qraw[h][1] = w0.y; qraw[h][2] = w0.z; qraw[h][3] = w0.w;
+        qraw[h][4] = w1.x; qraw[h][5] = w1.y; qraw[h][6] = w1.z; qraw[h][7] = w1.w;
+      } else {  // D = 64
+        const u32x2_t w0 = *reinterpret_cast<const u32x2_t*>(qp);
+        const u32x2_t w1 = *reinterpret_cast<const u32x2_t*>(q_bf16 ? qp : qp + 8);
+        qraw[h][0] = w0.x; qraw[h][1] = w0.y; qraw[h][2] = w1.x; qraw[h][3] = w1.y;
+      }
+    } else {
+      if constexpr (EPL == 8)
+        load8_f32(a.q, qoff, a.q_dt, q[h]);
+      else  // D = 64
+        load4_f32(a.q, qoff, a.q_dt, q[h]);
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) q[h][e] *= a.qscale;
+      for (int e = 0; e < EPL; ++e) q[h][e] *= a.qscale;
+    }
   }
+  auto ready_q = [&]() {  // the prefetching loop's deferred conversion
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const float v = q_bf16 ? ((e & 1) ? bf16w_hi(qraw[h][e >> 1]) : bf16w_lo(qraw[h][e >> 1]))
+                               : __uint_as_float(qraw[h][e]);
+        q[h][e] = v * a.qscale;
+      }
+  };
 
   float m[G], l[G], acc[G][EPL];
 #pragma unroll
@@ -213,18 +246,23 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
   const int mend = has_new ? end - 1 : end;
 
   // Loads of the TPG tokens from t0 on (rows past end are clamped: masked in
-  // consume, never out of bounds).
-#define SKV_LOAD_TILE(KF, VF, T0)                                             \
+  // consume, never out of bounds). FLOOR: also for t0 >= mend, where the rows
+  // clamp to max(mend - 1, 0): a cached row, or (mend = 0: the piece holds
+  // only an appended token) row 0, which that append is writing, so it exists.
+#define SKV_LOAD_TILE_(KF, VF, T0, FLOOR)                                     \
   {                                                                           \
     _Pragma("unroll") for (int u = 0; u < TPG; ++u) {                         \
-      const int t_ = min((T0) + u, mend - 1);                                  \
+      int t_ = min((T0) + u, mend - 1);                                        \
+      if (FLOOR) t_ = max(t_, 0);                                             \
       KF[u].load(row_ptr<TC, D, PAGED>(kb, a, b, t_, hk) + e0);               \
     }                                                                         \
     _Pragma("unroll") for (int u = 0; u < TPG; ++u) {                         \
-      const int t_ = min((T0) + u, mend - 1);                                  \
+      int t_ = min((T0) + u, mend - 1);                                        \
+      if (FLOOR) t_ = max(t_, 0);                                             \
       VF[u].load(row_ptr<TC, D, PAGED>(vb, a, b, t_, hk) + e0);               \
     }                                                                         \
   }
+#define SKV_LOAD_TILE(KF, VF, T0) SKV_LOAD_TILE_(KF, VF, T0, false)
   // Online softmax and PV of the TPG tokens from t0 held in KF, VF.
 #define SKV_CONSUME(KF, VF, T0)                                               \
   {                                                                           \
@@ -259,7 +297,12 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
     // instead of one per group).
     Frag<TC, EPL> ka[TPG], va[TPG], kn[TPG], vn[TPG];
     int t0 = start + sub * TPG;
-    if (t0 < mend) SKV_LOAD_TILE(ka, va, t0);
+    // The first group is loaded unconditionally (rows floored, unused when
+    // t0 >= mend): behind a branch, the join before q's conversion made the
+    // compiler wait for every load issued, the K/V ones included.
+    SKV_LOAD_TILE_(ka, va, t0, true);
+    __builtin_amdgcn_sched_barrier(0);  // the conversion stays after these loads
+    ready_q();
     while (t0 < mend) {
       if (t0 + step < mend) SKV_LOAD_TILE(kn, vn, t0 + step);
       SKV_CONSUME(ka, va, t0);
@@ -278,6 +321,7 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
   }
 #undef SKV_CONSUME
 #undef SKV_LOAD_TILE
+#undef SKV_LOAD_TILE_
 
   if (has_new && sub == 0) {
     // The appended token: the input row, rounded to the cache's precision,
