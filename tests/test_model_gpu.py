@@ -46,7 +46,8 @@ def lib():
 @pytest.mark.parametrize("M,N,K", [(1, 256, 256), (5, 100, 260), (16, 768, 768),
                                    (17, 3072, 768), (64, 48, 3072), (100, 1024, 64),
                                    (3, 50304, 768), (2, 80, 4100), (16, 768, 3072),
-                                   (1, 256, 1024), (7, 200, 700), (16, 64, 520)])
+                                   (1, 256, 1024), (7, 200, 700), (16, 64, 520),
+                                   (4, 96, 768), (4, 2304, 256)])  # M = 4: last compact-epilogue row count
 @pytest.mark.parametrize("epi", ["plain", "bias_gelu", "bias_res", "split", "ln_gelu"])
 def test_linear_matches_numpy(gpu_ctx, M, N, K, epi):
     banner(f"linear M={M} N={N} K={K} {epi}")
