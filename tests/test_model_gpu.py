@@ -219,6 +219,27 @@ def test_model_logits_match_oracle_teacher_forced(gpu_ctx, kv, tol):
     assert err < tol
 
 
+@pytest.mark.parametrize("kv,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, 2e-2)])
+def test_c3_shape_logits_match_oracle(gpu_ctx, kv, tol):
+    """BASELINE configs[2] at its full shape (12 layers, d 768, 12 heads x 64,
+    MLP 3072, vocab 50304, context 1024, batch 16, N(0, 0.02) from seed 0):
+    the first 12 teacher-forced steps of every sequence against the float64
+    forward. Same kernels and launch shapes as the bench's C3 step."""
+    banner(f"C3 shape logits kv={kv}")
+    m, params = make_model(gpu_ctx, 50304, 768, 12, 12, 1024, seed=0, std=0.02, kv=kv)
+    toks = np.random.default_rng(7).integers(0, 50304, (16, 12))
+    got = m.forward(toks)
+    want = mo.forward(params, toks, 12)
+    err = rel_rows(got, want)
+    print(f"rel_err={err:.3e}")
+    assert err < tol
+    # greedy choices agree wherever the float64 top-2 margin is not a near-tie
+    for row_got, row_want in zip(got.reshape(-1, 50304), want.reshape(-1, 50304)):
+        top2 = np.sort(row_want)[-2:]
+        if top2[1] - top2[0] > 1e-3 * max(1.0, abs(top2[1])):
+            assert int(np.argmax(row_got)) == int(np.argmax(row_want))
+
+
 def c1_model(gpu_ctx):
     """4 layers, d 256, 4 heads x 64, MLP 1024, vocab 256,
     context 256, N(0, 0.02) from seed 0."""
