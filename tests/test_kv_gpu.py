@@ -423,6 +423,59 @@ def test_decode_full_size_c4_sampled(gpu_ctx):
         assert rel_err(got[b:b + 1, h:h + 1], want) < 1e-4
 
 
+def test_decode_full_size_c5(gpu_ctx):
+    """C5 at full size, built as bench.py builds it: 64 sequences, 32 query
+    heads over 8 kv heads, D=128, bf16 16-token pages under a seeded random
+    page table, lognormal lengths (median 1500, sigma 0.8, clipped to
+    [16, 8192]). The paged decode equals the same data gathered into a
+    contiguous cache bit for bit (C5's own check), and the C restatement of
+    the oracle on the same bf16 values within 1e-4."""
+    banner("decode C5 full size")
+    from oracle import c_oracle
+    gpu = _gpu()
+    B, Hq, Hkv, D, bs = 64, 32, 8, 128, 16
+    r = np.random.default_rng(0)
+    lens = np.clip(np.exp(r.normal(np.log(1500), 0.8, B)), 16, 8192).astype(np.int64)
+    max_seq = 8192
+    need = -(-lens // bs)
+    n_blocks = int(need.sum())
+    cache = gpu.kv_cache_create(gpu_ctx, gpu.KVCacheConfig(B, max_seq, 1, Hq, D, n_kv_heads=Hkv,
+                                                           dtype=torch.bfloat16, block_size=bs,
+                                                           n_blocks=n_blocks))
+    perm = r.permutation(n_blocks).astype(np.int32)
+    table = np.zeros((B, -(-max_seq // bs)), np.int32)
+    o = 0
+    for b in range(B):
+        table[b, :need[b]] = perm[o:o + need[b]]
+        o += need[b]
+    gpu.kv_cache_set_block_table(cache, torch.from_numpy(table))
+    layer = cache.layers[0]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for buf in (layer.k_cache.buffer, layer.v_cache.buffer):
+        buf.copy_(torch.randn(buf.shape, generator=g, device="cuda"))
+    layer.lens.copy_(torch.from_numpy(lens.astype(np.int32)))
+    layer.host_lens[:] = lens
+    q = r.standard_normal((B, Hq, D)).astype(np.float32)
+    got = _decode(gpu, gpu_ctx, cache, q, max_len=int(lens.max()))
+    # the pool gathered into a contiguous [B, T, H_kv, D] cache
+    nb = int(need.max())
+    tab = torch.from_numpy(table[:, :nb].astype(np.int64)).cuda()
+    kc = layer.k_cache.buffer.view(n_blocks, bs, Hkv, D)[tab].reshape(B, nb * bs, Hkv, D)
+    vc = layer.v_cache.buffer.view(n_blocks, bs, Hkv, D)[tab].reshape(B, nb * bs, Hkv, D)
+    cc = gpu.kv_cache_create(gpu_ctx, gpu.KVCacheConfig(B, nb * bs, 1, Hq, D, n_kv_heads=Hkv,
+                                                        dtype=torch.bfloat16))
+    cc.layers[0].k_cache.buffer.copy_(kc.reshape(-1, Hkv * D))
+    cc.layers[0].v_cache.buffer.copy_(vc.reshape(-1, Hkv * D))
+    cc.layers[0].lens.copy_(torch.from_numpy(lens.astype(np.int32)))
+    cc.layers[0].host_lens[:] = lens
+    np.testing.assert_array_equal(got, _decode(gpu, gpu_ctx, cc, q, max_len=int(lens.max())))
+    bits = lambda x: x.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    want = c_oracle.decode_attn(q, bits(kc), bits(vc), lens, cache_bf16=True)
+    err = rel_err(got, want)
+    print(f"rel_err={err:.3e}")
+    assert err < 1e-4  # the same bf16 values, fp32 accumulation on both sides
+
+
 # ---------------------------------------------------------------------------
 # Fused append + decode attention (skv_append_decode_attn)
 # ---------------------------------------------------------------------------
