@@ -425,7 +425,7 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
     byts = float(np.mean([algorithmic_bytes(f, h_q=Hq, h_kv=Hkv, d=Dh, s_kv=s_kv, s_q=4, s_o=4)
                           for f in fills]))
     mean_s = float(ms.mean()) * 1e-3
-    chunk, n_chunks = gpu.decode_plan(ctx, B, Hkv, max_len, int(lens0.sum()))
+    chunk, n_chunks = gpu.decode_plan(ctx, B, Hq, Hkv, max_len, int(lens0.sum()))
     roof = {"kernel": "append + decode attention (k_decode_partial + k_decode_merge)", "bound": "hbm",
             "achieved": byts / mean_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": byts / mean_s / 1e9 / HBM_PEAK_GBS, "traffic": None,
@@ -746,7 +746,7 @@ def main():
     achieved = bytes_per_call / mean_s / 1e9
     assert cache.layers[0].lens.cpu().tolist() == [FILL + args.steps] * B
 
-    chunk, n_chunks = gpu.decode_plan(ctx, B, H, max_len)
+    chunk, n_chunks = gpu.decode_plan(ctx, B, H, H, max_len)
     prefill = None if args.no_prefill else time_prefill(ctx, cache, reps=10)
     cpu = None
     if not args.no_cpu_baseline:

@@ -640,26 +640,35 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
 
 using namespace skv;
 
-extern "C" int skv_decode_plan(int B, int H_kv, int max_len, long long total_len, int chunk_hint,
-                               int* chunk_tokens, int* n_chunks_max) {
+extern "C" int skv_decode_plan(int B, int H_q, int H_kv, int max_len, long long total_len,
+                               int chunk_hint, int* chunk_tokens, int* n_chunks_max) {
   SKV_REQUIRE(chunk_tokens && n_chunks_max, SKV_E_INVALID, "skv_decode_plan: null output");
-  SKV_REQUIRE(B > 0 && H_kv > 0 && max_len > 0, SKV_E_INVALID,
-              "skv_decode_plan: dims must be > 0 (B=%d H_kv=%d max_len=%d)", B, H_kv, max_len);
+  SKV_REQUIRE(B > 0 && H_q > 0 && H_kv > 0 && max_len > 0, SKV_E_INVALID,
+              "skv_decode_plan: dims must be > 0 (B=%d H_q=%d H_kv=%d max_len=%d)", B, H_q, H_kv,
+              max_len);
+  SKV_REQUIRE(H_q % H_kv == 0, SKV_E_INVALID,
+              "skv_decode_plan: H_q=%d is not a multiple of H_kv=%d", H_q, H_kv);
   int chunk;
   if (chunk_hint > 0) {
     chunk = (int)(((long)chunk_hint + 15) / 16 * 16);
   } else {
     // About 512 busy workgroups per call: two per CU on MI355X's 256 CUs.
-    // On C4 (4 x 32K tokens) this measured fastest: 1 or 2 workgroups on
-    // every CU stream at the same rate, while grids that leave some CUs one
-    // workgroup more than others (e.g. 336 workgroups) or that use more,
-    // shorter chunks were 5-15% slower. A workgroup owns chunk tokens of the
-    // flat token stream (every sequence's filled tokens end to end), so the
-    // chunk follows the batch's total fill and a ragged batch splits as
-    // evenly as a uniform one. Chunks are 32 to 8192 tokens.
+    // Grids that leave some CUs one workgroup more than others (e.g. 336
+    // workgroups) or that use more, shorter chunks measured 5-15% slower on
+    // C4 (4 x 32K tokens). A workgroup owns chunk tokens of the flat token
+    // stream (every sequence's filled tokens end to end), so the chunk
+    // follows the batch's total fill and a ragged batch splits as evenly as
+    // a uniform one. Chunks are 32 to 8192 tokens.
+    // Without grouped queries (H_q == H_kv) a workgroup does little VALU
+    // work per byte, and one workgroup per CU with twice the chunk streams
+    // faster once chunks are long: C4 161.6 -> 159.5 us per call (256 ->
+    // 512 tokens), as a plain non-temporal read of K and V does (87.3% ->
+    // 89.5% of 8 TB/s). With G = 4 (C5) the per-wavefront exp and dot work
+    // needs the second workgroup: 119 -> 159 us per call at one per CU.
     const long long tot = total_len > 0 ? total_len : (long long)B * max_len;
     const long long groups = H_kv / heads_per_group(H_kv);
-    const long long target = 2 * kNumCUs;
+    long long target = 2 * kNumCUs;
+    if (H_q == H_kv && (tot * groups + kNumCUs - 1) / kNumCUs >= 256) target = kNumCUs;
     long long per = (tot * groups + target - 1) / target;
     per = (per + 31) / 32 * 32;
     if (per < 32) per = 32;

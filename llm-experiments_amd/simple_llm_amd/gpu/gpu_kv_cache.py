@@ -234,14 +234,14 @@ def _workspace(ctx: GPUContext, nbytes: int) -> torch.Tensor:
     return ws
 
 
-def decode_plan(ctx: GPUContext, batch_size: int, n_kv_heads: int, max_len: int,
+def decode_plan(ctx: GPUContext, batch_size: int, n_heads: int, n_kv_heads: int, max_len: int,
                 total_len: int = 0) -> tuple[int, int]:
     """(chunk_tokens, n_chunks_max) of the split-K decode for these sizes.
 
     total_len: filled tokens over the batch (0: batch_size * max_len)."""
     L = _lib.lib()
     c, n = ctypes.c_int(), ctypes.c_int()
-    rc = L.skv_decode_plan(batch_size, n_kv_heads, max(int(max_len), 1), int(total_len),
+    rc = L.skv_decode_plan(batch_size, n_heads, n_kv_heads, max(int(max_len), 1), int(total_len),
                            int(ctx.config.decode_chunk_tokens), ctypes.byref(c), ctypes.byref(n))
     _lib.check(rc, "skv_decode_plan")
     return c.value, n.value
@@ -268,7 +268,8 @@ def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.T
     if max_len is None:
         max_len = int(layer.host_lens.max())
     total = int(np.minimum(layer.host_lens, max_len).sum())
-    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_kv_heads, max_len, total)
+    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
+                                  total)
     L = _lib.lib()
     need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
     ws = _workspace(ctx, need)
@@ -328,7 +329,8 @@ def kv_cache_append_attend(ctx: GPUContext, cache: KVCache, layer_idx: int, new_
     if max_len is None:
         max_len = int(after.max())
     total = int(np.minimum(after, max_len).sum())
-    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_kv_heads, max_len, total)
+    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
+                                  total)
     L = _lib.lib()
     need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
     ws = _workspace(ctx, need)

@@ -199,7 +199,8 @@ class TransformerModel:
         key = ("plan", cache.batch_size)
         if key not in self._bufs:
             T = cache.max_seq_len
-            chunk, n = gpu.decode_plan(self.ctx, cache.batch_size, cache.n_kv_heads, T,
+            chunk, n = gpu.decode_plan(self.ctx, cache.batch_size, cache.n_heads,
+                                       cache.n_kv_heads, T,
                                        cache.batch_size * T)
             L = _lib.lib()
             need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, n)

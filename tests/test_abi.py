@@ -24,10 +24,10 @@ def test_version():
     assert _lib.lib().skv_version() == 100
 
 
-def _plan(B, Hkv, max_len, hint=0, total=0):
+def _plan(B, Hkv, max_len, hint=0, total=0, Hq=None):
     c, n = ctypes.c_int(), ctypes.c_int()
-    rc = _lib.lib().skv_decode_plan(B, Hkv, max_len, total, hint, ctypes.byref(c),
-                                    ctypes.byref(n))
+    rc = _lib.lib().skv_decode_plan(B, Hkv if Hq is None else Hq, Hkv, max_len, total, hint,
+                                    ctypes.byref(c), ctypes.byref(n))
     return rc, c.value, n.value
 
 
@@ -43,13 +43,22 @@ def test_decode_plan_covers_every_length(B, Hkv, L):
 
 
 def test_decode_plan_c4_and_ragged_total():
-    # C4: 4 sequences x 16 kv heads (one head group) at 32256 -> 256-token
-    # chunks, 4 * 126 = 504 workgroups (two per CU), 127 slots per sequence
-    assert _plan(4, 16, 32256) == (0, 256, 127)
-    # a ragged batch plans from its total fill, not from B * max_len
-    rc, chunk, n = _plan(64, 8, 8192, total=64 * 2000)
+    # C4 (MHA): 4 sequences x 16 kv heads (one head group) at 32256 -> one
+    # workgroup per CU: 512-token chunks, 4 * 63 = 252 workgroups, 64 slots
+    # per sequence
+    assert _plan(4, 16, 32256) == (0, 512, 64)
+    # the same stream with 4 query heads per kv head keeps two per CU:
+    # 256-token chunks, 4 * 126 = 504 workgroups, 127 slots
+    assert _plan(4, 16, 32256, Hq=64) == (0, 256, 127)
+    # a ragged batch plans from its total fill, not from B * max_len (C5:
+    # 64 sequences, 32 query / 8 kv heads)
+    rc, chunk, n = _plan(64, 8, 8192, total=64 * 2000, Hq=32)
     assert rc == 0 and chunk == 256 and n == 33
-    assert _plan(64, 8, 8192)[1] > chunk
+    assert _plan(64, 8, 8192, Hq=32)[1] > chunk
+    # short MHA streams (C2: 8 x 2048, 8 heads; C3: 16 x 1024, 12 heads)
+    # stay at two workgroups per CU, with the 32-token minimum chunk
+    assert _plan(8, 8, 2048)[:2] == (0, 32)
+    assert _plan(16, 12, 1024)[:2] == (0, 32)
 
 
 def test_decode_plan_hint_and_errors():
@@ -58,6 +67,9 @@ def test_decode_plan_hint_and_errors():
     assert _plan(0, 16, 100)[0] == _lib.SKV_E_INVALID
     assert _plan(4, 16, 0)[0] == _lib.SKV_E_INVALID
     assert b"dims must be > 0" in _lib.lib().skv_last_error()
+    assert _plan(4, 16, 100, Hq=0)[0] == _lib.SKV_E_INVALID
+    assert _plan(4, 16, 100, Hq=24)[0] == _lib.SKV_E_INVALID
+    assert b"not a multiple" in _lib.lib().skv_last_error()
 
 
 def test_workspace_bytes():
