@@ -289,16 +289,20 @@ def test_paged_equals_contiguous_bitwise(gpu_ctx):
     np.testing.assert_array_equal(a, b)
 
 
-@pytest.mark.parametrize("L", [1, 2, 15, 16, 17, 255, 256, 257, 1023, 1024, 1025, 2047, 2048])
-def test_decode_chunk_boundaries(gpu_ctx, L):
-    banner(f"decode boundary L={L}")
+# fp32 at 256-token chunks; bf16 (4 tokens in flight per lane) at the
+# 512-token chunks the plan gives long MHA streams
+@pytest.mark.parametrize("dtype,chunk", [(torch.float32, 256), (torch.bfloat16, 512)])
+@pytest.mark.parametrize("L", [1, 2, 15, 16, 17, 255, 256, 257, 511, 513, 1023, 1024, 1025, 2047,
+                               2048])
+def test_decode_chunk_boundaries(gpu_ctx, L, dtype, chunk):
+    banner(f"decode boundary L={L} {dtype} chunk={chunk}")
     gpu = _gpu()
-    gpu_ctx.config.decode_chunk_tokens = 256
+    gpu_ctx.config.decode_chunk_tokens = chunk
     try:
         rng = np.random.default_rng(L)
         B, T, H, D = 2, 2048, 4, 128
         lens = np.array([L, max(1, L // 2)])
-        cache, k, v, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, H, H, D, torch.float32, lens)
+        cache, k, v, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, H, H, D, dtype, lens)
         q = rng.standard_normal((B, H, D)).astype(np.float32)
         got = _decode(gpu, gpu_ctx, cache, q)
         want = ko.decode_attention(q, k, v, lens)
