@@ -190,7 +190,8 @@ size_t skv_prefill_workspace_bytes(int B, int C, int H_q, int D, int n_splits);
  * Requires start[b] + n_new[b] <= T_cap.
  * bf16 cache: Q, K, V and the probabilities enter v_mfma_f32_32x32x16_bf16
  * as bf16, accumulation and softmax are fp32; D in {64, 128}; G = H_q / H_kv
- * in {1, 2, 4, 8}; split over the prefix by n_splits.
+ * in {1, 2, 4, 8}; split over the prefix by n_splits; out, q and ws 16-byte
+ * aligned.
  * fp32 cache: q and out fp32, every product in fp32 (v_mfma_f32_32x32x2_f32,
  * the kernel of skv_flash_fwd); D in {16, 32, 64, 128}, any G; n_splits and
  * the workspace are not used.

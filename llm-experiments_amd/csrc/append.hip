@@ -87,28 +87,54 @@ __global__ __launch_bounds__(256) void k_append_one(TC* __restrict__ kc, TC* __r
   if (threadIdx.x == 0) lens[b] = pos + 1;
 }
 
-// Chunk append: grid (row tiles, B). Rows i < n_new[b] of sequence b go to
-// position lens[b] + i. lens is read only.
+// V consecutive elements of a row from src (one 16-byte load) into dst, in
+// dst's type: one 16-byte store, two for bf16 -> fp32, one 8-byte store for
+// fp32 -> bf16 (round to nearest even).
+template <typename TC, typename TI>
+__device__ __forceinline__ void copy_vec(TC* __restrict__ dst, const TI* __restrict__ src) {
+  if constexpr (sizeof(TC) == sizeof(TI)) {
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+  } else {
+    constexpr int V = In16<TI>::N;
+    float f[V];
+    In16<TI>::load(src, f);
+    if constexpr (sizeof(TC) == 2) {
+      *reinterpret_cast<uint2*>(dst) =
+          make_uint2((uint32_t)f32_to_bf16(f[0]) | ((uint32_t)f32_to_bf16(f[1]) << 16),
+                     (uint32_t)f32_to_bf16(f[2]) | ((uint32_t)f32_to_bf16(f[3]) << 16));
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; e += 4)
+        *reinterpret_cast<float4*>(dst + e) = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
+    }
+  }
+}
+
+// Chunk append: grid (tiles of C * E / V threads, B), one 16-byte input
+// vector of K and one of V per thread, so every load of the grid is in
+// flight at once. (Four rows per workgroup in a loop, with 2-byte stores for
+// fp32 -> bf16, took 16 us for C4's 50 MB chunk, 3.1 TB/s, on MI355X.)
+// Rows i < n_new[b] of sequence b go to position lens[b] + i. lens is read
+// only.
 template <typename TC, typename TI>
 __global__ __launch_bounds__(256) void k_append_chunk(TC* __restrict__ kc, TC* __restrict__ vc,
                                                       const TI* __restrict__ kn,
                                                       const TI* __restrict__ vn,
                                                       const int32_t* __restrict__ lens,
                                                       const int32_t* __restrict__ n_new, int C,
-                                                      int E, int T_cap, int rows_per_block) {
+                                                      int E, int T_cap) {
+  constexpr int V = In16<TI>::N;  // elements per 16-byte input vector
   const int b = blockIdx.y;
+  const int nv = E / V;           // vectors per row
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  const int r = g / nv, e = (g - r * nv) * V;
   const int n = n_new ? min(n_new[b], C) : C;
-  const int pos0 = lens[b];
-  const int r0 = blockIdx.x * rows_per_block;
-  const int r1 = min(r0 + rows_per_block, n);
-  for (int r = r0; r < r1; ++r) {
-    const int pos = pos0 + r;
-    if (pos < 0 || pos >= T_cap) break;
-    const size_t dst = ((size_t)b * T_cap + pos) * E;
-    const size_t src = ((size_t)b * C + r) * E;
-    copy_row<TC, TI>(kc + dst, kn + src, E, threadIdx.x, blockDim.x);
-    copy_row<TC, TI>(vc + dst, vn + src, E, threadIdx.x, blockDim.x);
-  }
+  const int pos = lens[b] + r;
+  if (r >= n || pos < 0 || pos >= T_cap) return;
+  const size_t dst = ((size_t)b * T_cap + pos) * E + e;
+  const size_t src = ((size_t)b * C + r) * E + e;
+  copy_vec<TC, TI>(kc + dst, kn + src);
+  copy_vec<TC, TI>(vc + dst, vn + src);
 }
 
 __global__ void k_advance(int32_t* __restrict__ lens, const int32_t* __restrict__ n_new,
@@ -190,12 +216,13 @@ extern "C" int skv_append_chunk(void* k_cache, void* v_cache, const void* k_new,
   SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(in_dt), SKV_E_INVALID, "skv_append_chunk: bad dtype");
   SKV_REQUIRE(D % 8 == 0, SKV_E_UNSUPPORTED, "skv_append_chunk: D=%d must be a multiple of 8", D);
   const int E = H_kv * D;
-  const int rows = 4;
-  dim3 grid((C + rows - 1) / rows, B), block(256);
+  SKV_REQUIRE((size_t)C * E < (1u << 31), SKV_E_UNSUPPORTED, "skv_append_chunk: chunk too large");
+  const int V = in_dt == SKV_BF16 ? 8 : 4;  // elements per 16-byte input vector
+  dim3 grid((unsigned)(((size_t)C * (E / V) + 255) / 256), B), block(256);
   hipStream_t s = (hipStream_t)stream;
 #define SKV_CHUNK_CASE(TC, TI)                                                                \
   hipLaunchKernelGGL((k_append_chunk<TC, TI>), grid, block, 0, s, (TC*)k_cache, (TC*)v_cache, \
-                     (const TI*)k_new, (const TI*)v_new, lens, n_new, C, E, T_cap, rows)
+                     (const TI*)k_new, (const TI*)v_new, lens, n_new, C, E, T_cap)
   if (cache_dt == SKV_F32 && in_dt == SKV_F32) SKV_CHUNK_CASE(float, float);
   else if (cache_dt == SKV_F32 && in_dt == SKV_BF16) SKV_CHUNK_CASE(float, uint16_t);
   else if (cache_dt == SKV_BF16 && in_dt == SKV_F32) SKV_CHUNK_CASE(uint16_t, float);

@@ -375,35 +375,55 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
   }
 }
 
-// Merge of the split partials: one thread per (row, d). Rows i >= n_new[b]
-// are zeros. Splits that saw no token of a row (m = -inf, l = 0) drop out.
-__global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a, int D) {
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+// Four consecutive outputs (16-byte aligned for fp32, 8-byte for bf16).
+__device__ __forceinline__ void store4(void* out, size_t i, int dt, const float (&o)[4]) {
+  if (dt == SKV_BF16) {
+    const uint32_t w0 = (uint32_t)f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
+    const uint32_t w1 = (uint32_t)f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + i) = make_uint2(w0, w1);
+  } else {
+    *reinterpret_cast<float4*>(static_cast<float*>(out) + i) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// Merge of the split partials, grid (tiles of C * Hq * D/4 threads, B): one
+// thread per 4 consecutive d of a row, 16-byte partial loads, 32-bit index
+// arithmetic. (One thread per element with 64-bit divisions took 31 us on
+// C4's 55 MB, 1.7 TB/s, measured on MI355X.) Rows i >= n_new[b] are zeros.
+// Splits that saw no token of a row (m = -inf, l = 0) drop out.
+template <int D>
+__global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a) {
+  constexpr int V = D / 4;  // threads per row
+  const int b = blockIdx.y;
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= a.C * a.Hq * V) return;
+  const int rb = g / V, d = (g % V) * 4;  // row within the sequence: i * Hq + h
+  const int i = rb / a.Hq;
   const size_t rows = (size_t)a.B * a.C * a.Hq;
-  if (idx >= rows * D) return;
-  const size_t row = idx / D;
-  const int d = (int)(idx % D);
-  const int b = (int)(row / ((size_t)a.C * a.Hq));
-  const int i = (int)((row / a.Hq) % a.C);
+  const size_t row = (size_t)b * a.C * a.Hq + rb;
   const int P = min(max(a.start[b], 0), a.T_cap);
   const int n = max(0, min(a.n_new ? min(a.n_new[b], a.C) : a.C, a.T_cap - P));
-  if (i >= n) {
-    store_elem(a.out, idx, a.out_dt, 0.f);
-    return;
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+  if (i < n) {
+    float M = -INFINITY;
+    for (int s = 0; s < a.n_splits; ++s) M = fmaxf(M, a.ws_ml[(s * rows + row) * 2]);
+    float L = 0.f;
+    for (int s = 0; s < a.n_splits; ++s) {
+      const size_t pr = s * rows + row;
+      const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + pr * 2);
+      if (ml.x == -INFINITY) continue;
+      const float wgt = fast_exp2(ml.x - M);
+      const float4 x = *reinterpret_cast<const float4*>(a.ws_o + pr * D + d);
+      L = fmaf(wgt, ml.y, L);
+      o[0] = fmaf(wgt, x.x, o[0]);
+      o[1] = fmaf(wgt, x.y, o[1]);
+      o[2] = fmaf(wgt, x.z, o[2]);
+      o[3] = fmaf(wgt, x.w, o[3]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = o[e] / L;
   }
-  const size_t sstride = rows;
-  float M = -INFINITY;
-  for (int s = 0; s < a.n_splits; ++s) M = fmaxf(M, a.ws_ml[(s * sstride + row) * 2]);
-  float L = 0.f, O = 0.f;
-  for (int s = 0; s < a.n_splits; ++s) {
-    const size_t pr = s * sstride + row;
-    const float ms = a.ws_ml[pr * 2];
-    if (ms == -INFINITY) continue;
-    const float wgt = fast_exp2(ms - M);
-    L = fmaf(wgt, a.ws_ml[pr * 2 + 1], L);
-    O = fmaf(wgt, a.ws_o[pr * D + d], O);
-  }
-  store_elem(a.out, idx, a.out_dt, O / L);
+  store4(a.out, row * D + d, a.out_dt, o);
 }
 
 // Zero-fill of rows i >= n_new[b] when there is no merge pass.
@@ -473,6 +493,9 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
                         start, n_new, B, C, H_q, H_kv, D, T_cap, scale, (hipStream_t)stream, fn);
   }
   SKV_REQUIRE(D == 64 || D == 128, SKV_E_UNSUPPORTED, "%s: D=%d (supported: 64, 128)", fn, D);
+  SKV_REQUIRE((((uintptr_t)out | (uintptr_t)q | (uintptr_t)ws) & 15) == 0, SKV_E_INVALID,
+              "%s: out, q and ws must be 16-byte aligned", fn);
+  SKV_REQUIRE((size_t)C * H_q * D < (1u << 31), SKV_E_UNSUPPORTED, "%s: chunk too large", fn);
   const int G = H_q / H_kv;
   SKV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, SKV_E_UNSUPPORTED,
               "%s: no kernel for G=%d", fn, G);
@@ -511,9 +534,11 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
   if (rc) return rc;
   const size_t elems = (size_t)B * C * H_q * D;
   const unsigned mblocks = (unsigned)((elems + 255) / 256);
-  if (n_splits > 1)
-    hipLaunchKernelGGL(k_prefill_merge, dim3(mblocks), dim3(256), 0, s, a, D);
-  else if (n_new)
+  if (n_splits > 1) {
+    const dim3 mgrid((unsigned)(((size_t)C * H_q * (D / 4) + 255) / 256), (unsigned)B);
+    if (D == 64) hipLaunchKernelGGL(k_prefill_merge<64>, mgrid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(k_prefill_merge<128>, mgrid, dim3(256), 0, s, a);
+  } else if (n_new)
     hipLaunchKernelGGL(k_prefill_zero_tail, dim3(mblocks), dim3(256), 0, s, a, D);
   return check_launch(fn);
 }

@@ -164,6 +164,25 @@ def test_flash_fwd_rejects_bad_arguments():
     assert call(n=0) == _lib.SKV_E_INVALID
 
 
+def test_prefill_rejects_bad_arguments():
+    L = _lib.lib()
+    fake = 4096  # never dereferenced: each call below fails validation first
+
+    def call(out=fake, D=128, Hq=4, ns=1, ws=None, ws_bytes=0):
+        return L.skv_prefill_attn(out, fake, fake, fake, fake, None, 2, 16, Hq, 4, D, 1024, 0.125,
+                                  ns, ws, ws_bytes, 1, 1, 1, None)
+
+    assert call(D=96) == _lib.SKV_E_UNSUPPORTED
+    assert call(out=fake + 8) == _lib.SKV_E_INVALID  # bf16 path: 16-byte alignment
+    assert b"16-byte aligned" in L.skv_last_error()
+    assert call(ns=2, ws=fake + 4, ws_bytes=1 << 30) == _lib.SKV_E_INVALID
+    assert call(Hq=12) == _lib.SKV_E_UNSUPPORTED  # G = 3
+    assert call(ns=33) == _lib.SKV_E_INVALID
+    need = L.skv_prefill_workspace_bytes(2, 16, 4, 128, 2)
+    assert need == 2 * 2 * 16 * 4 * (128 + 2) * 4
+    assert call(ns=2, ws=fake, ws_bytes=need - 1) == _lib.SKV_E_WORKSPACE
+
+
 def test_argmax_workspace_and_rejects():
     L = _lib.lib()
     # one 2048-column slice per workgroup; candidates (value, index) per slice
