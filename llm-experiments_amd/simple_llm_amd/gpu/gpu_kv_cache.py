@@ -325,10 +325,12 @@ def kv_cache_append_attend(ctx: GPUContext, cache: KVCache, layer_idx: int, new_
                          f"{cache.batch_size * e_q} elements")
     batch_count(ctx)
     cap = cache.block_table.shape[1] * cache.block_size if cache.paged else cache.max_seq_len
-    after = np.where(layer.host_lens < cap, layer.host_lens + 1, layer.host_lens)
+    after = np.minimum(layer.host_lens + 1, cap)  # full sequences stay put
     if max_len is None:
         max_len = int(after.max())
-    total = int(np.minimum(after, max_len).sum())
+        total = int(after.sum())
+    else:
+        total = int(np.minimum(after, max_len).sum())
     chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
                                   total)
     L = _lib.lib()

@@ -484,6 +484,21 @@ def test_decode_full_size_c5(gpu_ctx):
 # Fused append + decode attention (skv_append_decode_attn)
 # ---------------------------------------------------------------------------
 
+def test_launches_follow_torch_current_stream(gpu_ctx):
+    """The ops enqueue on torch's current stream: the raw stream query the
+    launches use equals torch's Stream handle, also inside a stream context."""
+    from simple_llm_amd import _lib
+    dev = gpu_ctx.device
+    idx = dev.index or 0
+    assert _lib.stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream
+    assert _lib.stream_handle(idx) == torch.cuda.current_stream(dev).cuda_stream
+    side = torch.cuda.Stream(device=dev)  # default priority
+    with torch.cuda.stream(side):
+        assert _lib.stream_handle(dev) == side.cuda_stream
+        assert side.cuda_stream != torch.cuda.default_stream(dev).cuda_stream
+    assert _lib.stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream
+
+
 FUSED_CASES = [
     # B, T, Hq, Hkv, D, cache dtype, input dtype, paged
     (8, 300, 8, 8, 64, torch.float32, torch.float32, False),      # C2 head shape
