@@ -110,12 +110,14 @@ def check(rc: int, what: str) -> None:
     raise SkvError(f"{msg} (status {rc})")
 
 
+_DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16}
+
+
 def dtype_code(dt: torch.dtype) -> int:
-    if dt == torch.float32:
-        return F32
-    if dt == torch.bfloat16:
-        return BF16
-    raise ValueError(f"unsupported dtype {dt} (float32 or bfloat16)")
+    code = _DTYPE_CODES.get(dt)
+    if code is None:
+        raise ValueError(f"unsupported dtype {dt} (float32 or bfloat16)")
+    return code
 
 
 _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)

@@ -141,6 +141,10 @@ def _check_layer(cache: KVCache, layer_idx: int) -> None:
 
 def _check_tensor(t: torch.Tensor, name: str, device: torch.device) -> None:
     # Kernels dereference these pointers on the GPU: host tensors never reach them.
+    # Fast path first (get_device() is an int; t.device builds an object).
+    if (device.type == "cuda" and t.is_cuda and t.get_device() == (device.index or 0)
+            and t.is_contiguous() and t.data_ptr() % 16 == 0):
+        return
     if device.type != "cuda" or not t.is_cuda:
         raise ValueError(f"{name}: the KV cache and its operands must live on the ROCm "
                          f"device (cache on {device}, {name} on {t.device})")
