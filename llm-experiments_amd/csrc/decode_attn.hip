@@ -472,26 +472,44 @@ __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, in
   float M = -INFINITY, L = 0.f, O[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) O[e] = 0.f;
-#pragma unroll 4
-  for (int n = st; n < np; n += NS) {
-    const float mn = ws_ml[(base + n) * 2];
-    const float ln = ws_ml[(base + n) * 2 + 1];
-    float on[EPL];
-    const float* src = ws_o + (base + n) * D + li * EPL;
-    if constexpr (EPL == 4) {
-      const float4 x = *reinterpret_cast<const float4*>(src);
-      on[0] = x.x; on[1] = x.y; on[2] = x.z; on[3] = x.w;
-    } else {
+  // Stream st merges pieces st, st + NS, st + 2 NS, ... in that order. The
+  // partials of U pieces are loaded together, at indices clamped to the last
+  // piece (in bounds), so one memory round trip serves U pieces. The merge
+  // step has no branch: a clamped copy past np gets weights 1 (state) and 0
+  // (its finite values), an exact no-op. (With a bounds check per piece the
+  // compiler moved each piece's loads behind its check, one round trip per
+  // piece.)
+  constexpr int U = 8;
+  for (int n0 = st; n0 < np; n0 += U * NS) {
+    float mn[U], ln[U], on[U][EPL];
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) on[e] = src[e];
+    for (int u = 0; u < U; ++u) {
+      const size_t pn = base + min(n0 + u * NS, np - 1);
+      const float2 ml = *reinterpret_cast<const float2*>(ws_ml + pn * 2);
+      mn[u] = ml.x;
+      ln[u] = ml.y;
+      const float* src = ws_o + pn * D + li * EPL;
+      if constexpr (EPL == 4) {
+        const float4 x = *reinterpret_cast<const float4*>(src);
+        on[u][0] = x.x; on[u][1] = x.y; on[u][2] = x.z; on[u][3] = x.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) on[u][e] = src[e];
+      }
     }
-    // every piece holds at least one token, so mn is finite
-    const float Mn = fmaxf(M, mn);
-    const float wa = fast_exp2(M - Mn), wb = fast_exp2(mn - Mn);
-    L = L * wa + ln * wb;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) O[e] = O[e] * wa + on[e] * wb;
-    M = Mn;
+    for (int u = 0; u < U; ++u) {
+      // every piece holds at least one token, so mn is finite; piece u = 0 is
+      // always valid (n0 < np), so M is finite for every later u
+      const bool ok = n0 + u * NS < np;
+      const float Mn = ok ? fmaxf(M, mn[u]) : M;
+      const float wa = ok ? fast_exp2(M - Mn) : 1.f;
+      const float wb = ok ? fast_exp2(mn[u] - Mn) : 0.f;
+      L = L * wa + ln[u] * wb;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) O[e] = O[e] * wa + on[u][e] * wb;
+      M = Mn;
+    }
   }
   __shared__ float sm_ml[NS][2];
   __shared__ float sm_o[NS][D];
