@@ -64,6 +64,8 @@ int skv_version(void);
  * at gpu_kv_cache.py:148-152).
  * k_new, v_new: [B, H_kv, D] of in_dt. k_cache, v_cache: [B, T_cap, H_kv, D]
  * of cache_dt (fp32 copy is exact; bf16 storage rounds to nearest even).
+ * Any D > 0 (16-byte vectors when H_kv * D is a multiple of 8 and the
+ * pointers are 16-byte aligned, element copies otherwise).
  */
 int skv_append(void* k_cache, void* v_cache, const void* k_new, const void* v_new,
                int32_t* lens, int B, int H_kv, int D, int T_cap, int cache_dt,
@@ -121,7 +123,10 @@ size_t skv_decode_workspace_bytes(int B, int H_q, int D, int n_chunks_max);
  *   out[b, h, :] = softmax(scale * q[b, h, :] . K[b, 0:lens[b], h/G, :]^T)
  *                  . V[b, 0:lens[b], h/G, :],           G = H_q / H_kv.
  * No length cap (the reference caps lens at 256). lens[b] == 0 gives zeros.
- * q, out: [B, H_q, D] of q_dt / out_dt. D in {64, 128}; G in {1, 2, 4, 8}.
+ * q, out: [B, H_q, D] of q_dt / out_dt. G in {1, 2, 4, 8}. D: any head dim
+ * from 1 to 256 (the reference takes any, gpu_kernels.py:2846); 64 and 128
+ * run kernels tuned per shape, others the same kernels at the head dim
+ * padded to 32, 64, 128 or 256; G = 8 takes D <= 128.
  * Split-K: pass 1 writes per-piece (max, sum, unnormalised o) partials into
  * ws; pass 2 merges them. n_chunks_max >= 2. A sequence whose tokens lie
  * past the first B * (n_chunks_max - 1) * chunk_tokens tokens of the flat
@@ -189,12 +194,13 @@ size_t skv_prefill_workspace_bytes(int B, int C, int H_q, int D, int n_splits);
  * q, out: [B, C, H_q, D] of q_dt / out_dt; n_new may be NULL (C for all).
  * Requires start[b] + n_new[b] <= T_cap.
  * bf16 cache: Q, K, V and the probabilities enter v_mfma_f32_32x32x16_bf16
- * as bf16, accumulation and softmax are fp32; D in {64, 128}; G = H_q / H_kv
- * in {1, 2, 4, 8}; split over the prefix by n_splits; out, q and ws 16-byte
- * aligned.
+ * as bf16, accumulation and softmax are fp32; D from 1 to 128 (64 and 128
+ * as they are, others padded to 32, 64 or 128 with zeros); G = H_q / H_kv
+ * in {1, 2, 4, 8}; split over the prefix by n_splits; out, q, the caches and
+ * ws 16-byte aligned.
  * fp32 cache: q and out fp32, every product in fp32 (v_mfma_f32_32x32x2_f32,
- * the kernel of skv_flash_fwd); D in {16, 32, 64, 128}, any G; n_splits and
- * the workspace are not used.
+ * the kernel of skv_flash_fwd); D from 1 to 128, any G; n_splits and the
+ * workspace are not used.
  */
 int skv_prefill_attn(void* out, const void* q, const void* k_cache, const void* v_cache,
                      const int32_t* start, const int32_t* n_new, int B, int C, int H_q,
@@ -296,7 +302,9 @@ int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
  *   M = row max of S, L = sum exp(S - M), out = softmax(S) V.
  * q, k, v, out: [B, N, H, D] fp32 (the reference's [B*N, H*D] buffers),
  * 16-byte aligned; L, M: [B, N, H] fp32, or NULL to skip them.
- * D in {16, 32, 64, 128}. Products on v_mfma_f32_32x32x2_f32 (fp32).
+ * D from 1 to 128 (the reference's default flash_attn_max_head_dim;
+ * gpu_types.py:93): the kernels run at D padded to a multiple of 16, with
+ * zeros past D. Products on v_mfma_f32_32x32x2_f32 (fp32).
  */
 int skv_flash_fwd(float* out, float* L, float* M, const float* q, const float* k, const float* v,
                   int B, int N, int H, int D, float scale, skv_stream_t stream);
@@ -315,7 +323,7 @@ size_t skv_flash_bwd_workspace_bytes(int B, int N, int H);
  * q, k, v, o, dout, dq, dk, dv: [B, N, H, D] fp32 (the reference's
  * [B*N, H*D] buffers), 16-byte aligned; L, M: [B, N, H] fp32, the forward's
  * softmax sums and row maxima of the scaled scores (the reference's L and M
- * buffers). The outputs must not overlap the inputs. D in {16, 32, 64, 128}.
+ * buffers). The outputs must not overlap the inputs. D from 1 to 128.
  * Products run on v_mfma_f32_32x32x2_f32 (fp32); no atomics, so results are
  * bitwise reproducible.
  */

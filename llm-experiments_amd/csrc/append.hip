@@ -8,7 +8,10 @@
 // moves 16 bytes per tensor per iteration (a whole E = H_kv*D row is 1-8 KB),
 // and after a workgroup barrier lane 0 advances lens[b]; no other workgroup
 // touches lens[b], so the position update is race free and the whole decode
-// step stays on the device.
+// step stays on the device. The reference takes any head_dim
+// (gpu_kv_cache.py:55-64 checks only > 0): rows whose E is not a multiple of
+// 8 elements (not 16-byte aligned in every dtype) move one element per lane
+// and iteration instead.
 #include "skv_common.h"
 
 namespace skv {
@@ -35,12 +38,24 @@ struct In16<uint16_t> {
   }
 };
 
-// Copy (TI == TC) keeps the input bits; fp32 -> bf16 rounds to nearest even;
-// bf16 -> fp32 is exact.
+// One element in the cache's type: fp32 -> bf16 rounds to nearest even,
+// bf16 -> fp32 is exact, equal types copy the bits.
 template <typename TC, typename TI>
+__device__ __forceinline__ TC convert_elem(TI x) {
+  if constexpr (sizeof(TC) == sizeof(TI)) return x;
+  else if constexpr (sizeof(TC) == 2) return f32_to_bf16(x);
+  else return bf16_to_f32(x);
+}
+
+// Copy (TI == TC) keeps the input bits; fp32 -> bf16 rounds to nearest even;
+// bf16 -> fp32 is exact. VEC: n is a multiple of 8 and both rows are 16-byte
+// aligned (16-byte vectors); otherwise one element per lane and iteration.
+template <typename TC, typename TI, bool VEC>
 __device__ __forceinline__ void copy_row(TC* __restrict__ dst, const TI* __restrict__ src, int n,
                                          int tid, int nthreads) {
-  if constexpr (sizeof(TC) == sizeof(TI)) {
+  if constexpr (!VEC) {
+    for (int i = tid; i < n; i += nthreads) dst[i] = convert_elem<TC, TI>(src[i]);
+  } else if constexpr (sizeof(TC) == sizeof(TI)) {
     // same type: move raw 16-byte vectors
     const uint4* s = reinterpret_cast<const uint4*>(src);
     uint4* d = reinterpret_cast<uint4*>(dst);
@@ -60,7 +75,7 @@ __device__ __forceinline__ void copy_row(TC* __restrict__ dst, const TI* __restr
   }
 }
 
-template <typename TC, typename TI, bool PAGED>
+template <typename TC, typename TI, bool PAGED, bool VEC>
 __global__ __launch_bounds__(256) void k_append_one(TC* __restrict__ kc, TC* __restrict__ vc,
                                                     const TI* __restrict__ kn,
                                                     const TI* __restrict__ vn,
@@ -81,8 +96,8 @@ __global__ __launch_bounds__(256) void k_append_one(TC* __restrict__ kc, TC* __r
     row = (size_t)b * T_cap + pos;
   }
   const size_t src = (size_t)b * E;
-  copy_row<TC, TI>(kc + row * E, kn + src, E, threadIdx.x, blockDim.x);
-  copy_row<TC, TI>(vc + row * E, vn + src, E, threadIdx.x, blockDim.x);
+  copy_row<TC, TI, VEC>(kc + row * E, kn + src, E, threadIdx.x, blockDim.x);
+  copy_row<TC, TI, VEC>(vc + row * E, vn + src, E, threadIdx.x, blockDim.x);
   __syncthreads();  // every lane has read lens[b] before it moves
   if (threadIdx.x == 0) lens[b] = pos + 1;
 }
@@ -137,6 +152,28 @@ __global__ __launch_bounds__(256) void k_append_chunk(TC* __restrict__ kc, TC* _
   copy_vec<TC, TI>(vc + dst, vn + src);
 }
 
+// Chunk append of rows whose E is not a multiple of 8: grid (tiles of C * E
+// threads, B), one element of K and one of V per thread.
+template <typename TC, typename TI>
+__global__ __launch_bounds__(256) void k_append_chunk_elem(TC* __restrict__ kc,
+                                                           TC* __restrict__ vc,
+                                                           const TI* __restrict__ kn,
+                                                           const TI* __restrict__ vn,
+                                                           const int32_t* __restrict__ lens,
+                                                           const int32_t* __restrict__ n_new,
+                                                           int C, int E, int T_cap) {
+  const int b = blockIdx.y;
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  const int r = g / E, e = g - r * E;
+  const int n = n_new ? min(n_new[b], C) : C;
+  const int pos = lens[b] + r;
+  if (r >= n || pos < 0 || pos >= T_cap) return;
+  const size_t dst = ((size_t)b * T_cap + pos) * E + e;
+  const size_t src = ((size_t)b * C + r) * E + e;
+  kc[dst] = convert_elem<TC, TI>(kn[src]);
+  vc[dst] = convert_elem<TC, TI>(vn[src]);
+}
+
 __global__ void k_advance(int32_t* __restrict__ lens, const int32_t* __restrict__ n_new,
                           int n_const, int B, int T_cap) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -144,6 +181,8 @@ __global__ void k_advance(int32_t* __restrict__ lens, const int32_t* __restrict_
   const int n = n_new ? n_new[b] : n_const;
   lens[b] = min(lens[b] + n, T_cap);
 }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int log2_exact(int x) {
   if (x <= 0 || (x & (x - 1))) return -1;
@@ -157,9 +196,18 @@ int launch_append_one(void* kc, void* vc, const void* kn, const void* vn, int32_
                       const int32_t* bt, int max_blocks, int bs_shift, int B, int E, int T_cap,
                       int cache_dt, int in_dt, hipStream_t s) {
   dim3 grid(B), block(256);
+  const bool vec = E % 8 == 0 && aligned16(kc) && aligned16(vc) && aligned16(kn) && aligned16(vn);
 #define SKV_APPEND_CASE(TC, TI)                                                                   \
-  hipLaunchKernelGGL((k_append_one<TC, TI, PAGED>), grid, block, 0, s, (TC*)kc, (TC*)vc,          \
-                     (const TI*)kn, (const TI*)vn, lens, bt, max_blocks, bs_shift, E, T_cap)
+  do {                                                                                            \
+    if (vec)                                                                                      \
+      hipLaunchKernelGGL((k_append_one<TC, TI, PAGED, true>), grid, block, 0, s, (TC*)kc,         \
+                         (TC*)vc, (const TI*)kn, (const TI*)vn, lens, bt, max_blocks, bs_shift, E, \
+                         T_cap);                                                                  \
+    else                                                                                          \
+      hipLaunchKernelGGL((k_append_one<TC, TI, PAGED, false>), grid, block, 0, s, (TC*)kc,        \
+                         (TC*)vc, (const TI*)kn, (const TI*)vn, lens, bt, max_blocks, bs_shift, E, \
+                         T_cap);                                                                  \
+  } while (0)
   if (cache_dt == SKV_F32 && in_dt == SKV_F32) SKV_APPEND_CASE(float, float);
   else if (cache_dt == SKV_F32 && in_dt == SKV_BF16) SKV_APPEND_CASE(float, uint16_t);
   else if (cache_dt == SKV_BF16 && in_dt == SKV_F32) SKV_APPEND_CASE(uint16_t, float);
@@ -183,7 +231,6 @@ extern "C" int skv_append(void* k_cache, void* v_cache, const void* k_new, const
   SKV_REQUIRE(B > 0 && H_kv > 0 && D > 0 && T_cap > 0, SKV_E_INVALID,
               "skv_append: dims must be > 0 (B=%d H_kv=%d D=%d T_cap=%d)", B, H_kv, D, T_cap);
   SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(in_dt), SKV_E_INVALID, "skv_append: bad dtype");
-  SKV_REQUIRE(D % 8 == 0, SKV_E_UNSUPPORTED, "skv_append: D=%d must be a multiple of 8", D);
   return launch_append_one<false>(k_cache, v_cache, k_new, v_new, lens, nullptr, 0, 0, B,
                                   H_kv * D, T_cap, cache_dt, in_dt, (hipStream_t)stream);
 }
@@ -200,7 +247,6 @@ extern "C" int skv_append_paged(void* k_pool, void* v_pool, const void* k_new, c
   SKV_REQUIRE(shift >= 0, SKV_E_INVALID, "skv_append_paged: block_size=%d not a power of two",
               block_size);
   SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(in_dt), SKV_E_INVALID, "skv_append_paged: bad dtype");
-  SKV_REQUIRE(D % 8 == 0, SKV_E_UNSUPPORTED, "skv_append_paged: D=%d must be a multiple of 8", D);
   return launch_append_one<true>(k_pool, v_pool, k_new, v_new, lens, block_table, max_blocks,
                                  shift, B, H_kv * D, 0, cache_dt, in_dt, (hipStream_t)stream);
 }
@@ -214,15 +260,25 @@ extern "C" int skv_append_chunk(void* k_cache, void* v_cache, const void* k_new,
   SKV_REQUIRE(B > 0 && C > 0 && H_kv > 0 && D > 0 && T_cap > 0, SKV_E_INVALID,
               "skv_append_chunk: dims must be > 0");
   SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(in_dt), SKV_E_INVALID, "skv_append_chunk: bad dtype");
-  SKV_REQUIRE(D % 8 == 0, SKV_E_UNSUPPORTED, "skv_append_chunk: D=%d must be a multiple of 8", D);
   const int E = H_kv * D;
   SKV_REQUIRE((size_t)C * E < (1u << 31), SKV_E_UNSUPPORTED, "skv_append_chunk: chunk too large");
-  const int V = in_dt == SKV_BF16 ? 8 : 4;  // elements per 16-byte input vector
+  // 16-byte vectors when every row is 16-byte aligned in both dtypes
+  const bool vec = E % 8 == 0 && aligned16(k_cache) && aligned16(v_cache) && aligned16(k_new) &&
+                   aligned16(v_new);
+  const int V = vec ? (in_dt == SKV_BF16 ? 8 : 4) : 1;  // elements per thread
   dim3 grid((unsigned)(((size_t)C * (E / V) + 255) / 256), B), block(256);
   hipStream_t s = (hipStream_t)stream;
-#define SKV_CHUNK_CASE(TC, TI)                                                                \
-  hipLaunchKernelGGL((k_append_chunk<TC, TI>), grid, block, 0, s, (TC*)k_cache, (TC*)v_cache, \
-                     (const TI*)k_new, (const TI*)v_new, lens, n_new, C, E, T_cap)
+#define SKV_CHUNK_CASE(TC, TI)                                                                  \
+  do {                                                                                          \
+    if (vec)                                                                                    \
+      hipLaunchKernelGGL((k_append_chunk<TC, TI>), grid, block, 0, s, (TC*)k_cache,             \
+                         (TC*)v_cache, (const TI*)k_new, (const TI*)v_new, lens, n_new, C, E,   \
+                         T_cap);                                                                \
+    else                                                                                        \
+      hipLaunchKernelGGL((k_append_chunk_elem<TC, TI>), grid, block, 0, s, (TC*)k_cache,        \
+                         (TC*)v_cache, (const TI*)k_new, (const TI*)v_new, lens, n_new, C, E,   \
+                         T_cap);                                                                \
+  } while (0)
   if (cache_dt == SKV_F32 && in_dt == SKV_F32) SKV_CHUNK_CASE(float, float);
   else if (cache_dt == SKV_F32 && in_dt == SKV_BF16) SKV_CHUNK_CASE(float, uint16_t);
   else if (cache_dt == SKV_BF16 && in_dt == SKV_F32) SKV_CHUNK_CASE(uint16_t, float);

@@ -59,6 +59,7 @@ struct FbwdArgs {
   float* dv;
   float* delta;  // [B, N, H] row deltas Dl, written by k_fbwd_dq
   int N, H, BH, n_blocks;
+  int D;  // head dim (the padded size is the kernel's template D)
   float scale, sl2;  // scale and scale * log2(e)
 };
 
@@ -71,9 +72,48 @@ __device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Element offset of row n of head h in batch b of a [B, N, H, D] tensor.
-template <int D>
-__device__ __forceinline__ size_t row_off(int b, int n, int N, int H, int h) {
+__device__ __forceinline__ size_t row_off(int b, int n, int N, int H, int h, int D) {
   return ((size_t)(b * N + n) * H + h) * D;
+}
+
+// Head dims: the kernels run on the head dim padded to DP, a multiple of 16
+// (two 8-element k groups per row fragment, whole float4 LDS stores). MODE
+// 0: D == DP (16, 32, 64, 128), 16-byte vectors throughout; MODE 1: D < DP
+// with D % 4 == 0 (float4 loads, groups past D read as zeros); MODE 2: any
+// other D (element loads). Padded elements are zeros in every operand that
+// is contracted over d, and the output rows they produce are never stored,
+// so results equal the unpadded computation.
+// Four consecutive elements c..c+3 of a row with D elements, zeros past D.
+template <int MODE>
+__device__ __forceinline__ f32x4 load4m(const float* row, int c, int D) {
+  if constexpr (MODE == 0) {
+    return *reinterpret_cast<const f32x4*>(row + c);
+  } else if constexpr (MODE == 1) {
+    const bool ok = c < D;  // D % 4 == 0: the group lies wholly inside or past D
+    const f32x4 x = *reinterpret_cast<const f32x4*>(row + (ok ? c : 0));
+    return ok ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+  } else {
+    f32x4 x;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const bool ok = c + t < D;
+      const float v = row[ok ? c + t : 0];
+      x[t] = ok ? v : 0.f;
+    }
+    return x;
+  }
+}
+
+// Stores the elements c..c+3 of y that lie inside a row of D elements.
+template <int MODE>
+__device__ __forceinline__ void store4m(float* row, int c, int D, const f32x4& y) {
+  if constexpr (MODE == 2) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      if (c + t < D) row[c + t] = y[t];
+  } else {
+    if (c < D) *reinterpret_cast<f32x4*>(row + c) = y;
+  }
 }
 
 // 64 rows x D of two tensors, global -> registers -> LDS (row stride D + 4
@@ -81,7 +121,7 @@ __device__ __forceinline__ size_t row_off(int b, int n, int N, int H, int h) {
 // distinct banks). Rows at or beyond N repeat row N - 1: every product that
 // involves them is masked out by a select, never by a multiply, so their
 // values cannot leak (and no load sits behind a branch).
-template <int D>
+template <int D, int MODE>
 struct Stage {
   static constexpr int SP = D + 4;
   static constexpr int C4 = D / 4;                  // float4 per row
@@ -91,15 +131,16 @@ struct Stage {
 
   // rows row0 .. row0+63 of two tensors whose row t starts at t0 + t * rs
   // (and t1 + t * rs), rows clamped to n_rows - 1
+  // (Dr: the real head dim, elements of a row past it read as zeros)
   __device__ __forceinline__ void load(const float* t0, const float* t1, int row0, int n_rows,
-                                       size_t rs) {
+                                       size_t rs, int Dr) {
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
       const int e = threadIdx.x + kThreads * u;
       const int n = min(row0 + e / C4, n_rows - 1);
-      const size_t off = (size_t)n * rs + 4 * (e % C4);
-      r0[u] = *reinterpret_cast<const f32x4*>(t0 + off);
-      r1[u] = *reinterpret_cast<const f32x4*>(t1 + off);
+      const size_t off = (size_t)n * rs;
+      r0[u] = load4m<MODE>(t0 + off, 4 * (e % C4), Dr);
+      r1[u] = load4m<MODE>(t1 + off, 4 * (e % C4), Dr);
     }
   }
   __device__ __forceinline__ void store(float* s0, float* s1) const {
@@ -120,11 +161,12 @@ struct Stage {
 // of one XCD (w % 8 = (b*H + h) % 8 when B*H is a multiple of 8).
 
 // dQ and the row deltas; rank 0 = the last query block (the most keys).
-template <int D>
+template <int D, int MODE>
 __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   constexpr int G = D / 8;             // 16-byte pairs of a row fragment
   constexpr int DT = (D + 31) / 32;    // 32-row tiles of dQ^T
-  constexpr int SP = Stage<D>::SP;
+  constexpr int SP = Stage<D, MODE>::SP;
+  const int RS = MODE == 0 ? D : a.D;  // the real head dim: row stride, last valid column + 1
   __shared__ __attribute__((aligned(16))) float sK[kCols * SP];
   __shared__ __attribute__((aligned(16))) float sV[kCols * SP];
 
@@ -137,7 +179,7 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   const int qrow = blk * kRows + wave * 32 + c;
   const bool qok = qrow < N;
   const int qr = qok ? qrow : N - 1;
-  const size_t qoff = row_off<D>(b, qr, N, H, h);
+  const size_t qoff = row_off(b, qr, N, H, h, RS);
 
   // this lane's query: Q and dO fragments (d = 8g + 4hf + t), and Dl. A lane
   // past N works on row N - 1 and masks all of its keys (qlim = -1).
@@ -146,9 +188,9 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int d0 = 8 * g + 4 * hf;
-    qf[g] = *reinterpret_cast<const f32x4*>(a.q + qoff + d0);
-    df[g] = *reinterpret_cast<const f32x4*>(a.dout + qoff + d0);
-    const f32x4 od = *reinterpret_cast<const f32x4*>(a.o + qoff + d0);
+    qf[g] = load4m<MODE>(a.q + qoff, d0, RS);
+    df[g] = load4m<MODE>(a.dout + qoff, d0, RS);
+    const f32x4 od = load4m<MODE>(a.o + qoff, d0, RS);
     dl += df[g].x * od.x + df[g].y * od.y + df[g].z * od.z + df[g].w * od.w;
   }
   dl += __shfl_xor(dl, 32);
@@ -166,16 +208,16 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   // the wave's last query (-1: the wave has none)
   const int wq_last = blk * kRows + wave * 32 < N ? min(blk * kRows + wave * 32 + 31, N - 1) : -1;
   const int steps = q_last / kCols + 1;
-  const size_t rs = (size_t)H * D;
-  const float* kh = a.k + row_off<D>(b, 0, N, H, h);
-  const float* vh = a.v + row_off<D>(b, 0, N, H, h);
-  Stage<D> st;
-  st.load(kh, vh, 0, N, rs);
+  const size_t rs = (size_t)H * RS;
+  const float* kh = a.k + row_off(b, 0, N, H, h, RS);
+  const float* vh = a.v + row_off(b, 0, N, H, h, RS);
+  Stage<D, MODE> st;
+  st.load(kh, vh, 0, N, rs, RS);
   for (int j = 0; j < steps; ++j) {
     __syncthreads();
     st.store(sK, sV);
     __syncthreads();
-    if (j + 1 < steps) st.load(kh, vh, (j + 1) * kCols, N, rs);
+    if (j + 1 < steps) st.load(kh, vh, (j + 1) * kCols, N, rs, RS);
 #pragma unroll
     for (int sub = 0; sub < kCols / 32; ++sub) {
       const int key0 = j * kCols + sub * 32;
@@ -209,8 +251,8 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int dcol = dt * 32 + c;
-        const bool dok = (D % 32 == 0) || dcol < D;
-        const float* kc = sK + (sub * 32 + 4 * hf) * SP + (dok ? dcol : D - 1);
+        const bool dok = (MODE == 0 && D % 32 == 0) || dcol < RS;
+        const float* kc = sK + (sub * 32 + 4 * hf) * SP + (dok ? dcol : RS - 1);
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
 #pragma unroll
@@ -229,22 +271,21 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const int d0 = dt * 32 + 8 * qq + 4 * hf;
-        if (d0 < D) {
-          const f32x4 y = {acc[dt][4 * qq] * a.scale, acc[dt][4 * qq + 1] * a.scale,
-                           acc[dt][4 * qq + 2] * a.scale, acc[dt][4 * qq + 3] * a.scale};
-          *reinterpret_cast<f32x4*>(a.dq + qoff + d0) = y;
-        }
+        const f32x4 y = {acc[dt][4 * qq] * a.scale, acc[dt][4 * qq + 1] * a.scale,
+                         acc[dt][4 * qq + 2] * a.scale, acc[dt][4 * qq + 3] * a.scale};
+        store4m<MODE>(a.dq + qoff, d0, RS, y);
       }
     }
   }
 }
 
 // dK and dV; rank 0 = key block 0 (the most queries).
-template <int D>
+template <int D, int MODE>
 __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
   constexpr int G = D / 8;
   constexpr int DT = (D + 31) / 32;
-  constexpr int SP = Stage<D>::SP;
+  constexpr int SP = Stage<D, MODE>::SP;
+  const int RS = MODE == 0 ? D : a.D;  // the real head dim
   __shared__ __attribute__((aligned(16))) float sQ[kCols * SP];
   __shared__ __attribute__((aligned(16))) float sD[kCols * SP];  // dO
   __shared__ __attribute__((aligned(16))) float sM2[kCols];
@@ -259,14 +300,14 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
   const int c = lane & 31, hf = lane >> 5;
   const int wk0 = blk * kRows + wave * 32;  // the wave's first key
   const int krow = wk0 + c;  // a key past N is masked for every query (query < N <= krow)
-  const size_t koff = row_off<D>(b, min(krow, N - 1), N, H, h);
+  const size_t koff = row_off(b, min(krow, N - 1), N, H, h, RS);
 
   f32x4 kf[G], vf[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int d0 = 8 * g + 4 * hf;
-    kf[g] = *reinterpret_cast<const f32x4*>(a.k + koff + d0);
-    vf[g] = *reinterpret_cast<const f32x4*>(a.v + koff + d0);
+    kf[g] = load4m<MODE>(a.k + koff, d0, RS);
+    vf[g] = load4m<MODE>(a.v + koff, d0, RS);
   }
   f32x16 dva[DT], dka[DT];
 #pragma unroll
@@ -277,7 +318,7 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
 
   const int j0 = (blk * kRows) / kCols;  // first step holding a query >= the block's first key
   const int steps = (N + kCols - 1) / kCols;
-  Stage<D> st;
+  Stage<D, MODE> st;
   // statistics of query j * kCols + threadIdx.x (threads < kCols), clamped
   float m2 = 0.f, il = 0.f, dl = 0.f;
 #define SKV_FB_STATS(J)                                                          \
@@ -288,11 +329,11 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
     il = 1.f / a.L[sr_];                                                         \
     dl = a.delta[sr_];                                                           \
   }
-  const size_t rs = (size_t)H * D;
-  const float* qh = a.q + row_off<D>(b, 0, N, H, h);
-  const float* dh = a.dout + row_off<D>(b, 0, N, H, h);
+  const size_t rs = (size_t)H * RS;
+  const float* qh = a.q + row_off(b, 0, N, H, h, RS);
+  const float* dh = a.dout + row_off(b, 0, N, H, h, RS);
   if (j0 < steps) {
-    st.load(qh, dh, j0 * kCols, N, rs);
+    st.load(qh, dh, j0 * kCols, N, rs, RS);
     SKV_FB_STATS(j0)
   }
   for (int j = j0; j < steps; ++j) {
@@ -305,7 +346,7 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
     }
     __syncthreads();
     if (j + 1 < steps) {
-      st.load(qh, dh, (j + 1) * kCols, N, rs);
+      st.load(qh, dh, (j + 1) * kCols, N, rs, RS);
       SKV_FB_STATS(j + 1)
     }
 #pragma unroll
@@ -350,8 +391,8 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int dcol = dt * 32 + c;
-        const bool dok = (D % 32 == 0) || dcol < D;
-        const int at = (sub * 32 + 4 * hf) * SP + (dok ? dcol : D - 1);
+        const bool dok = (MODE == 0 && D % 32 == 0) || dcol < RS;
+        const int at = (sub * 32 + 4 * hf) * SP + (dok ? dcol : RS - 1);
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
 #pragma unroll
@@ -373,8 +414,8 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = wk0 + 8 * (r / 4) + 4 * hf + (r % 4);
-      if (key < N && ((D % 32 == 0) || d < D)) {
-        const size_t off = row_off<D>(b, key, N, H, h) + d;
+      if (key < N && ((MODE == 0 && D % 32 == 0) || d < RS)) {
+        const size_t off = row_off(b, key, N, H, h, RS) + d;
         a.dk[off] = dka[dt][r] * a.scale;
         a.dv[off] = dva[dt][r];
       }
@@ -396,6 +437,7 @@ struct FfwdArgs {
   float* L;              // [B, C, Hq] softmax sums (may be NULL)
   float* M;              // [B, C, Hq] row maxima of the scaled scores (may be NULL)
   int C, Hq, Hkv, T_cap, BH, n_blocks;
+  int D;  // head dim (the padded size is the kernel's template D)
   float sl2;  // scale * log2(e)
 };
 
@@ -405,11 +447,12 @@ struct FfwdArgs {
 // running max moves only when a piece's max exceeds it by more than 8 (log2
 // units), so O and l are rescaled on few pieces; the true maximum is kept
 // beside it for M and the final L.
-template <int D>
+template <int D, int MODE>
 __global__ __launch_bounds__(kThreads) void k_flash_fwd(FfwdArgs a) {
   constexpr int G8 = D / 8;
   constexpr int DT = (D + 31) / 32;
-  constexpr int SP = Stage<D>::SP;
+  constexpr int SP = Stage<D, MODE>::SP;
+  const int RS = MODE == 0 ? D : a.D;  // the real head dim
   __shared__ __attribute__((aligned(16))) float sK[kCols * SP];
   __shared__ __attribute__((aligned(16))) float sV[kCols * SP];
 
@@ -425,11 +468,11 @@ __global__ __launch_bounds__(kThreads) void k_flash_fwd(FfwdArgs a) {
   const int qi = blk * kRows + wave * 32 + c;  // this lane's query (row of the chunk)
   const bool qok = qi < n;
   const int qlim = qok ? P + qi : -1;          // keys <= qlim are unmasked
-  const size_t qoff = (((size_t)b * C + min(qi, max(n, 1) - 1)) * Hq + h) * D;
+  const size_t qoff = (((size_t)b * C + min(qi, max(n, 1) - 1)) * Hq + h) * RS;
 
   f32x4 qf[G8];
 #pragma unroll
-  for (int g = 0; g < G8; ++g) qf[g] = *reinterpret_cast<const f32x4*>(a.q + qoff + 8 * g + 4 * hf);
+  for (int g = 0; g < G8; ++g) qf[g] = load4m<MODE>(a.q + qoff, 8 * g + 4 * hf, RS);
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
@@ -440,16 +483,16 @@ __global__ __launch_bounds__(kThreads) void k_flash_fwd(FfwdArgs a) {
   const int steps = blk * kRows < n ? (P + blk_q + kCols - 1) / kCols : 0;
   const int wq_last = blk * kRows + wave * 32 < n ? P + min(blk * kRows + wave * 32 + 31, n - 1)
                                                   : -1;
-  const size_t rs = (size_t)a.Hkv * D;
-  const float* kh = a.k + ((size_t)b * a.T_cap * a.Hkv + hk) * D;
-  const float* vh = a.v + ((size_t)b * a.T_cap * a.Hkv + hk) * D;
-  Stage<D> st;
-  if (steps > 0) st.load(kh, vh, 0, kv_end, rs);
+  const size_t rs = (size_t)a.Hkv * RS;
+  const float* kh = a.k + ((size_t)b * a.T_cap * a.Hkv + hk) * RS;
+  const float* vh = a.v + ((size_t)b * a.T_cap * a.Hkv + hk) * RS;
+  Stage<D, MODE> st;
+  if (steps > 0) st.load(kh, vh, 0, kv_end, rs, RS);
   for (int j = 0; j < steps; ++j) {
     __syncthreads();
     st.store(sK, sV);
     __syncthreads();
-    if (j + 1 < steps) st.load(kh, vh, (j + 1) * kCols, kv_end, rs);
+    if (j + 1 < steps) st.load(kh, vh, (j + 1) * kCols, kv_end, rs, RS);
 #pragma unroll
     for (int sub = 0; sub < kCols / 32; ++sub) {
       const int key0 = j * kCols + sub * 32;
@@ -493,8 +536,8 @@ __global__ __launch_bounds__(kThreads) void k_flash_fwd(FfwdArgs a) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int dcol = dt * 32 + c;
-        const bool dok = (D % 32 == 0) || dcol < D;
-        const float* vc = sV + (sub * 32 + 4 * hf) * SP + (dok ? dcol : D - 1);
+        const bool dok = (MODE == 0 && D % 32 == 0) || dcol < RS;
+        const float* vc = sV + (sub * 32 + 4 * hf) * SP + (dok ? dcol : RS - 1);
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
 #pragma unroll
@@ -515,11 +558,9 @@ __global__ __launch_bounds__(kThreads) void k_flash_fwd(FfwdArgs a) {
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * hf;
-      if (d0 < D) {
-        const f32x4 y = {acc[dt][4 * qq] * inv, acc[dt][4 * qq + 1] * inv,
-                         acc[dt][4 * qq + 2] * inv, acc[dt][4 * qq + 3] * inv};
-        *reinterpret_cast<f32x4*>(a.out + orow * D + d0) = y;
-      }
+      const f32x4 y = {acc[dt][4 * qq] * inv, acc[dt][4 * qq + 1] * inv,
+                       acc[dt][4 * qq + 2] * inv, acc[dt][4 * qq + 3] * inv};
+      store4m<MODE>(a.out + orow * RS, d0, RS, y);
     }
   }
   if (hf == 0 && qok) {
@@ -529,6 +570,21 @@ __global__ __launch_bounds__(kThreads) void k_flash_fwd(FfwdArgs a) {
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Padded head dim (a multiple of 16, at most 128) and load mode of a head dim.
+struct FlashShape {
+  int DP, mode;
+};
+FlashShape flash_shape(int D) {
+  const int DP = (D + 15) / 16 * 16;
+  return {DP, D == DP ? 0 : (D % 4 == 0 ? 1 : 2)};
+}
+
+// Expands X(DP, MODE) for every kernel shape.
+#define SKV_FLASH_SHAPES(X)                                                           \
+  X(16, 0) X(16, 1) X(16, 2) X(32, 0) X(32, 1) X(32, 2) X(48, 0) X(48, 1) X(48, 2)    \
+  X(64, 0) X(64, 1) X(64, 2) X(80, 0) X(80, 1) X(80, 2) X(96, 0) X(96, 1) X(96, 2)    \
+  X(112, 0) X(112, 1) X(112, 2) X(128, 0) X(128, 1) X(128, 2)
 
 }  // namespace
 }  // namespace skv
@@ -549,8 +605,7 @@ extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, co
               "%s: null pointer argument", fn);
   SKV_REQUIRE(B > 0 && N > 0 && H > 0 && D > 0, SKV_E_INVALID,
               "%s: dims must be > 0 (B=%d N=%d H=%d D=%d)", fn, B, N, H, D);
-  SKV_REQUIRE(D == 16 || D == 32 || D == 64 || D == 128, SKV_E_UNSUPPORTED,
-              "%s: head_dim %d (supported: 16, 32, 64, 128)", fn, D);
+  SKV_REQUIRE(D <= 128, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 128)", fn, D);
   SKV_REQUIRE(scale > 0.f, SKV_E_INVALID, "%s: scale must be > 0", fn);
   SKV_REQUIRE(aligned16(dq) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) &&
                   aligned16(dout),
@@ -563,7 +618,7 @@ extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, co
   a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.L = L; a.M = M;
   a.dq = dq; a.dk = dk; a.dv = dv;
   a.delta = static_cast<float*>(ws);
-  a.N = N; a.H = H;
+  a.N = N; a.H = H; a.D = D;
   a.n_blocks = (N + kRows - 1) / kRows;
   a.scale = scale;
   a.sl2 = scale * LOG2E;
@@ -571,14 +626,15 @@ extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, co
   a.BH = B * H;
   SKV_REQUIRE((long)a.n_blocks * a.BH < (1L << 31), SKV_E_UNSUPPORTED, "%s: grid too large", fn);
   const dim3 grid((unsigned)(a.n_blocks * a.BH));
-#define SKV_FB(DD)                                                                 \
-  if (D == DD) {                                                                   \
-    hipLaunchKernelGGL((k_fbwd_dq<DD>), grid, dim3(kThreads), 0, s, a);            \
+  const FlashShape fs = flash_shape(D);
+#define SKV_FB(DD, MM)                                                             \
+  if (fs.DP == DD && fs.mode == MM) {                                              \
+    hipLaunchKernelGGL((k_fbwd_dq<DD, MM>), grid, dim3(kThreads), 0, s, a);        \
     int rc = check_launch(fn);                                                     \
     if (rc) return rc;                                                             \
-    hipLaunchKernelGGL((k_fbwd_dkv<DD>), grid, dim3(kThreads), 0, s, a);           \
+    hipLaunchKernelGGL((k_fbwd_dkv<DD, MM>), grid, dim3(kThreads), 0, s, a);       \
   }
-  SKV_FB(16) SKV_FB(32) SKV_FB(64) SKV_FB(128)
+  SKV_FLASH_SHAPES(SKV_FB)
 #undef SKV_FB
   return check_launch(fn);
 }
@@ -591,22 +647,23 @@ namespace skv {
 int attn_fwd_f32(float* out, float* L, float* M, const float* q, const float* k, const float* v,
                  const int32_t* start, const int32_t* n_new, int B, int C, int Hq, int Hkv, int D,
                  int T_cap, float scale, hipStream_t s, const char* fn) {
-  SKV_REQUIRE(D == 16 || D == 32 || D == 64 || D == 128, SKV_E_UNSUPPORTED,
-              "%s: head_dim %d (supported: 16, 32, 64, 128)", fn, D);
+  SKV_REQUIRE(D >= 1 && D <= 128, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 128)",
+              fn, D);
   SKV_REQUIRE(aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v), SKV_E_INVALID,
               "%s: q, k, v and out must be 16-byte aligned", fn);
   FfwdArgs a;
   a.q = q; a.k = k; a.v = v; a.start = start; a.n_new = n_new;
   a.out = out; a.L = L; a.M = M;
-  a.C = C; a.Hq = Hq; a.Hkv = Hkv; a.T_cap = T_cap;
+  a.C = C; a.Hq = Hq; a.Hkv = Hkv; a.T_cap = T_cap; a.D = D;
   a.BH = B * Hq;
   a.n_blocks = (C + kRows - 1) / kRows;
   a.sl2 = scale * LOG2E;
   SKV_REQUIRE((long)a.n_blocks * a.BH < (1L << 31), SKV_E_UNSUPPORTED, "%s: grid too large", fn);
   const dim3 grid((unsigned)(a.n_blocks * a.BH));
-#define SKV_FF(DD) \
-  if (D == DD) hipLaunchKernelGGL((k_flash_fwd<DD>), grid, dim3(kThreads), 0, s, a);
-  SKV_FF(16) SKV_FF(32) SKV_FF(64) SKV_FF(128)
+  const FlashShape fs = flash_shape(D);
+#define SKV_FF(DD, MM) \
+  if (fs.DP == DD && fs.mode == MM) hipLaunchKernelGGL((k_flash_fwd<DD, MM>), grid, dim3(kThreads), 0, s, a);
+  SKV_FLASH_SHAPES(SKV_FF)
 #undef SKV_FF
   return check_launch(fn);
 }

@@ -27,6 +27,11 @@
 //    computed. Grouped-query attention folds the G query heads of a kv
 //    head into the rows (row = query * G + head), so K/V are read once per
 //    group.
+//  * Head dims other than 64 and 128 run the same kernel on the head dim
+//    padded to DP (32, 64 or 128): K/V tiles go through registers into the
+//    same LDS layout, zero-filled past the head dim, and the queries past it
+//    are zeros, so QK^T is unchanged and the padded rows of O^T are never
+//    stored.
 //  * Long prefixes are split into n_splits token ranges (split-K, so that
 //    about one workgroup runs per CU); partials (m, l, o[D]) are merged by a
 //    second pass. The query tiles of one (sequence, kv head, split) are laid
@@ -65,6 +70,7 @@ struct PrefillArgs {
   float* ws_o;   // [n_splits][B][C][Hq][D]
   float* ws_ml;  // [n_splits][B][C][Hq][2]
   int B;
+  int D;         // head dim: the row stride of q, out and the caches
 };
 
 // K and V tiles live in LDS row-major, [kBN tokens][D] bf16, two stages
@@ -87,7 +93,8 @@ struct alignas(16) Smem {
 template <int D>
 __device__ __forceinline__ int swz_key(int row) {
   if constexpr (D == 128) return 4 * (row & 3) + ((row >> 2) & 3);
-  else return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
+  else if constexpr (D == 64) return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
+  else return (row >> 2) & 3;  // D = 32: four chunks per row, four rows per bank sweep
 }
 template <int D>
 __device__ __forceinline__ int swz(int row, int chunk) {  // element offset of a 16-B chunk
@@ -114,10 +121,15 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const uint16_t* p) {
 // DMA writes) has completed.
 __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
-template <int D, int G>
+// LV = 0: D is the real head dim (64 or 128) and tiles move by LDS DMA.
+// LV = 8 or 1: D is the padded head dim, a.D the real one; tiles move
+// through registers, 16-byte loads (a.D % 8 == 0) or element loads.
+template <int D, int G, int LV>
 __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) {
   constexpr int KB = D / 16;  // k-blocks of the QK^T product
   constexpr int DB = D / 32;  // 32-row d blocks of O^T
+  constexpr bool GEN = LV != 0;
+  const int RS = GEN ? a.D : D;  // row stride of q, out and the cache rows
   __shared__ Smem<D> sm;
 
   // ---- which (sequence, kv head, split, query tile) this workgroup is ----
@@ -158,12 +170,21 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
     qrow[qb] = r;
     const bool ok = r < R;
     const int i = r / G, h = hk * G + r % G;
-    const size_t qoff = (((size_t)b * a.C + i) * a.Hq + h) * D;
+    const size_t qoff = (((size_t)b * a.C + i) * a.Hq + h) * RS;
     const size_t qsafe = ok ? qoff : 0;  // rows past the chunk read row 0 and are zeroed
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       float v[8];
-      load8_f32(a.q, qsafe + kb * 16 + g * 8, a.q_dt, v);
+      if constexpr (GEN) {  // element loads at clamped offsets, zeros past the head dim
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int e = kb * 16 + g * 8 + j;
+          const float x = load_elem(a.q, e < RS ? qsafe + e : 0, a.q_dt);
+          v[j] = e < RS ? x : 0.f;
+        }
+      } else {
+        load8_f32(a.q, qsafe + kb * 16 + g * 8, a.q_dt, v);
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) qf[qb][kb][j] = (__bf16)(ok ? v[j] : 0.f);
     }
@@ -179,9 +200,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
     for (int db = 0; db < DB; ++db) o[qb][db] = f32x16{};
   }
 
-  const size_t row_stride = (size_t)a.Hkv * D;  // elements between consecutive tokens
-  const uint16_t* kbase = a.k + ((size_t)b * a.T_cap * a.Hkv + hk) * D;
-  const uint16_t* vbase = a.v + ((size_t)b * a.T_cap * a.Hkv + hk) * D;
+  const size_t row_stride = (size_t)a.Hkv * RS;  // elements between consecutive tokens
+  const uint16_t* kbase = a.k + ((size_t)b * a.T_cap * a.Hkv + hk) * RS;
+  const uint16_t* vbase = a.v + ((size_t)b * a.T_cap * a.Hkv + hk) * RS;
 
   // Tiles go from HBM straight into LDS (global_load_lds_dwordx4: each lane
   // moves 16 bytes, a wavefront fills 1 KB of LDS in lane order), so no
@@ -191,9 +212,54 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
   // the last one is fetched too and never read.
   constexpr int RPK = 1024 / (D * 2);          // token rows per 1 KB
   constexpr int KPT = kBN * D * 2 / 1024;      // 1 KB pieces per tile and tensor
-  static_assert(KPT % kWaves == 0, "tile pieces must split over the wavefronts");
+  static_assert(GEN || KPT % kWaves == 0, "tile pieces must split over the wavefronts");
+  // Register-staged tiles (GEN): 16-byte chunk c of a tile is token row
+  // c / (D/8), logical chunk c % (D/8), at the same swizzled LDS position as
+  // the DMA form; chunks past the head dim are zeros.
+  constexpr int NCH = kBN * D / 8;                             // chunks per tile and tensor
+  constexpr int CPT = (NCH + kWaves * 64 - 1) / (kWaves * 64);  // chunks per thread
+  uint4 rk[GEN ? CPT : 1], rv[GEN ? CPT : 1];
+  auto reg_tile_load = [&](int T0) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = min(tid + u * kWaves * 64, NCH - 1);  // threads past NCH repeat the last chunk
+      const int row = c / (D / 8), lch = c % (D / 8);
+      const size_t rofs = (size_t)min(T0 + row, kv_end - 1) * row_stride;
+      if constexpr (LV == 8) {
+        const bool ok = lch * 8 < RS;  // RS % 8 == 0: the chunk is wholly inside or past D
+        const uint4 zk = *reinterpret_cast<const uint4*>(kbase + rofs + (ok ? lch * 8 : 0));
+        const uint4 zv = *reinterpret_cast<const uint4*>(vbase + rofs + (ok ? lch * 8 : 0));
+        rk[u] = ok ? zk : make_uint4(0, 0, 0, 0);
+        rv[u] = ok ? zv : make_uint4(0, 0, 0, 0);
+      } else {
+        uint32_t wk[4], wv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int e0 = lch * 8 + 2 * j;
+          const uint32_t k0 = kbase[rofs + (e0 < RS ? e0 : 0)];
+          const uint32_t k1 = kbase[rofs + (e0 + 1 < RS ? e0 + 1 : 0)];
+          const uint32_t v0 = vbase[rofs + (e0 < RS ? e0 : 0)];
+          const uint32_t v1 = vbase[rofs + (e0 + 1 < RS ? e0 + 1 : 0)];
+          wk[j] = (e0 < RS ? k0 : 0u) | ((e0 + 1 < RS ? k1 : 0u) << 16);
+          wv[j] = (e0 < RS ? v0 : 0u) | ((e0 + 1 < RS ? v1 : 0u) << 16);
+        }
+        rk[u] = make_uint4(wk[0], wk[1], wk[2], wk[3]);
+        rv[u] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+      }
+    }
+  };
+  auto reg_tile_store = [&](int ST) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = tid + u * kWaves * 64;
+      if (c >= NCH) continue;
+      const int row = c / (D / 8), lch = c % (D / 8);
+      *reinterpret_cast<uint4*>(&sm.k[ST][swz<D>(row, lch)]) = rk[u];
+      *reinterpret_cast<uint4*>(&sm.v[ST][swz<D>(row, lch)]) = rv[u];
+    }
+  };
 #define SKV_DMA_TILE(T0, ST)                                                                 \
-  {                                                                                          \
+  if constexpr (!GEN) {                                                                      \
     _Pragma("unroll") for (int c = 0; c < KPT / kWaves; ++c) {                               \
       const int piece = wave * (KPT / kWaves) + c;                                           \
       const int row = piece * RPK + lane / (D / 8);                                          \
@@ -206,7 +272,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
   }
 
   const int n_tiles = s1 > s0 ? (s1 - s0 + kBN - 1) / kBN : 0;
-  if (n_tiles > 0) SKV_DMA_TILE(s0, 0);
+  if constexpr (GEN) {
+    if (n_tiles > 0) {
+      reg_tile_load(s0);
+      reg_tile_store(0);
+    }
+  } else {
+    if (n_tiles > 0) SKV_DMA_TILE(s0, 0);
+  }
   wait_all_memory();
   __syncthreads();
 
@@ -218,7 +291,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
   auto tile = [&](auto stage, int it) {
     constexpr int st = decltype(stage)::value;
     const int t0 = s0 + it * kBN;
-    SKV_DMA_TILE(t0 + kBN, st ^ 1);
+    // the next tile: DMA into the other stage, or (GEN) loads into registers
+    // now and their LDS stores after this tile's products
+    if constexpr (GEN) reg_tile_load(t0 + kBN);
+    else SKV_DMA_TILE(t0 + kBN, st ^ 1);
 
     // S^T for the whole 64-token tile first (two independent accumulator
     // chains per query block), then one online-softmax update, then PV.
@@ -324,6 +400,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
         }
     }
 
+    if constexpr (GEN) reg_tile_store(st ^ 1);
     // the next tile's DMA has landed in LDS before anyone reads it
     wait_all_memory();
     __syncthreads();
@@ -350,9 +427,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            store_elem(a.out, orow * D + db * 32 + r4 * 8 + g * 4 + e, a.out_dt,
-                       o[qb][db][r4 * 4 + e] * inv);
+          for (int e = 0; e < 4; ++e) {
+            const int d = db * 32 + r4 * 8 + g * 4 + e;
+            if (!GEN || d < RS) store_elem(a.out, orow * RS + d, a.out_dt, o[qb][db][r4 * 4 + e] * inv);
+          }
     } else {
       const size_t prow = (size_t)split * a.B * a.C * a.Hq + orow;
       float* dst = a.ws_o + prow * D;
@@ -390,8 +468,10 @@ __device__ __forceinline__ void store4(void* out, size_t i, int dt, const float 
 // thread per 4 consecutive d of a row, 16-byte partial loads, 32-bit index
 // arithmetic. (One thread per element with 64-bit divisions took 31 us on
 // C4's 55 MB, 1.7 TB/s, measured on MI355X.) Rows i >= n_new[b] are zeros.
-// Splits that saw no token of a row (m = -inf, l = 0) drop out.
-template <int D>
+// Splits that saw no token of a row (m = -inf, l = 0) drop out. The partials
+// have the kernel's (padded) row stride D; GEN: outputs have the real head
+// dim a.D, stored element by element.
+template <int D, bool GEN>
 __global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a) {
   constexpr int V = D / 4;  // threads per row
   const int b = blockIdx.y;
@@ -423,7 +503,13 @@ __global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = o[e] / L;
   }
-  store4(a.out, row * D + d, a.out_dt, o);
+  if constexpr (GEN) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (d + e < a.D) store_elem(a.out, row * a.D + d + e, a.out_dt, o[e]);
+  } else {
+    store4(a.out, row * D + d, a.out_dt, o);
+  }
 }
 
 // Zero-fill of rows i >= n_new[b] when there is no merge pass.
@@ -440,6 +526,13 @@ __global__ __launch_bounds__(256) void k_prefill_zero_tail(PrefillArgs a, int D)
 }
 
 int n_query_tiles(int C, int G) { return (C * G + kBM - 1) / kBM; }
+
+// Head dim the bf16 kernel runs at: 64 and 128 as they are, others (up to
+// 128) padded to the next of 32, 64, 128.
+int kernel_dim(int D) {
+  if (D == 64 || D == 128 || D > 128) return D;
+  return D <= 32 ? 32 : D <= 64 ? 64 : 128;
+}
 
 bool dt_ok(int dt) { return dt == SKV_F32 || dt == SKV_BF16; }
 
@@ -467,7 +560,8 @@ extern "C" int skv_prefill_plan(int B, int C, int H_q, int H_kv, int max_kv_end,
 
 extern "C" size_t skv_prefill_workspace_bytes(int B, int C, int H_q, int D, int n_splits) {
   if (B <= 0 || C <= 0 || H_q <= 0 || D <= 0 || n_splits <= 1) return 0;
-  return (size_t)n_splits * B * C * H_q * (size_t)(D + 2) * sizeof(float);
+  // partials at the kernel's (padded) head dim
+  return (size_t)n_splits * B * C * H_q * (size_t)(kernel_dim(D) + 2) * sizeof(float);
 }
 
 extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
@@ -492,9 +586,12 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
                         static_cast<const float*>(k_cache), static_cast<const float*>(v_cache),
                         start, n_new, B, C, H_q, H_kv, D, T_cap, scale, (hipStream_t)stream, fn);
   }
-  SKV_REQUIRE(D == 64 || D == 128, SKV_E_UNSUPPORTED, "%s: D=%d (supported: 64, 128)", fn, D);
-  SKV_REQUIRE((((uintptr_t)out | (uintptr_t)q | (uintptr_t)ws) & 15) == 0, SKV_E_INVALID,
-              "%s: out, q and ws must be 16-byte aligned", fn);
+  SKV_REQUIRE(D >= 1 && D <= 128, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 128)",
+              fn, D);
+  SKV_REQUIRE((((uintptr_t)out | (uintptr_t)q | (uintptr_t)ws | (uintptr_t)k_cache |
+                (uintptr_t)v_cache) & 15) == 0,
+              SKV_E_INVALID, "%s: out, q, the caches and ws must be 16-byte aligned", fn);
+  const int DK = kernel_dim(D);  // the kernel's (padded) head dim
   SKV_REQUIRE((size_t)C * H_q * D < (1u << 31), SKV_E_UNSUPPORTED, "%s: chunk too large", fn);
   const int G = H_q / H_kv;
   SKV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, SKV_E_UNSUPPORTED,
@@ -518,26 +615,34 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
   a.n_splits = n_splits;
   a.n_groups = B * H_kv * n_splits;
   a.B = B;
+  a.D = D;
   a.ws_o = static_cast<float*>(ws);
-  a.ws_ml = n_splits > 1 ? a.ws_o + (size_t)n_splits * B * C * H_q * D : nullptr;
+  a.ws_ml = n_splits > 1 ? a.ws_o + (size_t)n_splits * B * C * H_q * DK : nullptr;
   const long blocks = (long)((a.n_groups + kXCD - 1) / kXCD) * kXCD * a.n_qt;
   SKV_REQUIRE(blocks < (1L << 31), SKV_E_UNSUPPORTED, "%s: grid too large", fn);
   hipStream_t s = (hipStream_t)stream;
-#define SKV_PF(DD, GG)                                                                        \
-  if (D == DD && G == GG)                                                                     \
-    hipLaunchKernelGGL((k_prefill_mfma<DD, GG>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, \
-                       s, a);
-  SKV_PF(64, 1) SKV_PF(64, 2) SKV_PF(64, 4) SKV_PF(64, 8)
-  SKV_PF(128, 1) SKV_PF(128, 2) SKV_PF(128, 4) SKV_PF(128, 8)
+  // LV: 0 = LDS DMA at the exact head dim; 8 = 16-byte register loads; 1 = element loads
+  const int LV = DK == D ? 0 : (D % 8 == 0 ? 8 : 1);
+#define SKV_PF(DD, GG, LL)                                                                    \
+  if (DK == DD && G == GG && LV == LL)                                                        \
+    hipLaunchKernelGGL((k_prefill_mfma<DD, GG, LL>), dim3((unsigned)blocks), dim3(kWaves * 64), \
+                       0, s, a);
+#define SKV_PF4(DD, LL) SKV_PF(DD, 1, LL) SKV_PF(DD, 2, LL) SKV_PF(DD, 4, LL) SKV_PF(DD, 8, LL)
+  SKV_PF4(64, 0) SKV_PF4(128, 0)
+  SKV_PF4(32, 8) SKV_PF4(32, 1) SKV_PF4(64, 8) SKV_PF4(64, 1) SKV_PF4(128, 8) SKV_PF4(128, 1)
+#undef SKV_PF4
 #undef SKV_PF
   int rc = check_launch(fn);
   if (rc) return rc;
   const size_t elems = (size_t)B * C * H_q * D;
   const unsigned mblocks = (unsigned)((elems + 255) / 256);
   if (n_splits > 1) {
-    const dim3 mgrid((unsigned)(((size_t)C * H_q * (D / 4) + 255) / 256), (unsigned)B);
-    if (D == 64) hipLaunchKernelGGL(k_prefill_merge<64>, mgrid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(k_prefill_merge<128>, mgrid, dim3(256), 0, s, a);
+    const dim3 mgrid((unsigned)(((size_t)C * H_q * (DK / 4) + 255) / 256), (unsigned)B);
+    if (LV == 0 && D == 64) hipLaunchKernelGGL((k_prefill_merge<64, false>), mgrid, dim3(256), 0, s, a);
+    else if (LV == 0) hipLaunchKernelGGL((k_prefill_merge<128, false>), mgrid, dim3(256), 0, s, a);
+    else if (DK == 32) hipLaunchKernelGGL((k_prefill_merge<32, true>), mgrid, dim3(256), 0, s, a);
+    else if (DK == 64) hipLaunchKernelGGL((k_prefill_merge<64, true>), mgrid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_prefill_merge<128, true>), mgrid, dim3(256), 0, s, a);
   } else if (n_new)
     hipLaunchKernelGGL(k_prefill_zero_tail, dim3(mblocks), dim3(256), 0, s, a, D);
   return check_launch(fn);

@@ -72,8 +72,6 @@ def kv_cache_create(ctx: GPUContext, config: KVCacheConfig) -> KVCache:
         raise ValueError(f"n_heads ({config.n_heads}) must be a multiple of n_kv_heads ({n_kv})")
     if config.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError(f"dtype must be torch.float32 or torch.bfloat16, got {config.dtype}")
-    if config.head_dim % 8 != 0:
-        raise ValueError(f"head_dim must be a multiple of 8, got {config.head_dim}")
 
     e_kv = n_kv * config.head_dim
     B = config.batch_size

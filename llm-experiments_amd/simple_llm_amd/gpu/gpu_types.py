@@ -30,8 +30,8 @@ class GPUConfig:
     max_workgroups_per_dim: int = 2**31 - 1
     attention_workgroup_size: int = 256
     flash_attn_max_head_dim: int = 128
-    flash_attn_br: int = 64
-    flash_attn_bc: int = 64
+    flash_attn_br: int = 32
+    flash_attn_bc: int = 32
     decode_chunk_tokens: int = 0  # 0: choose per call (skv_decode_plan)
 
 

@@ -97,7 +97,8 @@ def test_entry_points_reject_bad_arguments():
                                  a["T"], a["scale"], a["chunk"], a["n"], fake,
                                  kw.get("ws", ws), 0, 0, 0, None)
 
-    assert dec(D=96) == _lib.SKV_E_UNSUPPORTED
+    assert dec(D=300) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 256
+    assert dec(D=0) == _lib.SKV_E_INVALID
     assert dec(Hq=6, Hkv=4) == _lib.SKV_E_INVALID
     assert dec(chunk=100) == _lib.SKV_E_INVALID  # not a multiple of 16
     assert dec(ws=ws - 1) == _lib.SKV_E_WORKSPACE
@@ -140,7 +141,7 @@ def test_flash_bwd_rejects_bad_arguments():
                                None)
 
     assert call() == _lib.SKV_E_WORKSPACE
-    assert call(D=48, ws_bytes=need) == _lib.SKV_E_UNSUPPORTED
+    assert call(D=136, ws_bytes=need) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 128
     assert call(D=256, ws_bytes=need) == _lib.SKV_E_UNSUPPORTED
     assert call(ptr=None, ws_bytes=need) == _lib.SKV_E_INVALID
     assert call(ptr=fake + 4, ws_bytes=need) == _lib.SKV_E_INVALID  # not 16-byte aligned
@@ -156,7 +157,7 @@ def test_flash_fwd_rejects_bad_arguments():
     def call(D=64, ptr=fake, scale=0.125, n=100):
         return L.skv_flash_fwd(ptr, None, None, fake, fake, fake, 2, n, 3, D, scale, None)
 
-    assert call(D=48) == _lib.SKV_E_UNSUPPORTED
+    assert call(D=129) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 128
     assert call(D=256) == _lib.SKV_E_UNSUPPORTED
     assert call(ptr=None) == _lib.SKV_E_INVALID
     assert call(ptr=fake + 4) == _lib.SKV_E_INVALID  # not 16-byte aligned
@@ -172,7 +173,7 @@ def test_prefill_rejects_bad_arguments():
         return L.skv_prefill_attn(out, fake, fake, fake, fake, None, 2, 16, Hq, 4, D, 1024, 0.125,
                                   ns, ws, ws_bytes, 1, 1, 1, None)
 
-    assert call(D=96) == _lib.SKV_E_UNSUPPORTED
+    assert call(D=136) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 128
     assert call(out=fake + 8) == _lib.SKV_E_INVALID  # bf16 path: 16-byte alignment
     assert b"16-byte aligned" in L.skv_last_error()
     assert call(ns=2, ws=fake + 4, ws_bytes=1 << 30) == _lib.SKV_E_INVALID
