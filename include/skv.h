@@ -139,6 +139,26 @@ int skv_decode_attn(void* out, const void* q, const void* k_cache,
                     int n_chunks_max, void* ws, size_t ws_bytes, int cache_dt,
                     int q_dt, int out_dt, skv_stream_t stream);
 
+/*
+ * skv_decode_attn without a workspace argument: an entry point that
+ * allocates nothing, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It has no counterpart in the reference. The split-K partials
+ * live in a file-scope device array of SKV_DECODE_NOALLOC_MAX_BYTES (64 MiB)
+ * that each GPU the library runs on holds until the process ends; a plan
+ * whose skv_decode_workspace_bytes exceeds it is rejected with
+ * SKV_E_WORKSPACE. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams, or threads) race and must not be
+ * issued. Arguments and results are those of skv_decode_attn (same kernels:
+ * results are bitwise equal for the same plan).
+ */
+#define SKV_DECODE_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+int skv_decode_attn_noalloc(void* out, const void* q, const void* k_cache,
+                            const void* v_cache, const int32_t* lens, int B, int H_q,
+                            int H_kv, int D, int T_cap, float scale, int chunk_tokens,
+                            int n_chunks_max, int cache_dt, int q_dt, int out_dt,
+                            skv_stream_t stream);
+
 /* Paged variant of skv_decode_attn (extension; block_size a power of two). */
 int skv_decode_attn_paged(void* out, const void* q, const void* k_pool,
                           const void* v_pool, const int32_t* lens,

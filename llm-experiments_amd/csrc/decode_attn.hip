@@ -2,6 +2,9 @@
 // (pass-1 kernels tuned per shape), the merge pass for every head dim, and
 // the C entry points. Kernel design: decode_kernels.h; pass 1 for any other
 // head dim: decode_attn_generic.hip.
+#include <atomic>
+#include <mutex>
+
 #include "decode_kernels.h"
 
 namespace skv {
@@ -162,6 +165,21 @@ int dispatch_partial(const DecodeArgs& a, int D, int G, hipStream_t s) {
                : dec::launch_partial_generic(a, G, sizeof(TC) == 2, s);
 }
 
+// Workspace layout of a call: fp32 partials o [Hq][n_slots][D], then (m, l)
+// [Hq][n_slots][2], then B + 1 int64 prefix sums; each part starts 16-byte
+// aligned (odd head dims would misalign the (m, l) pairs and the int64s).
+struct WsLayout {
+  size_t o_floats, ml_floats, bytes;
+};
+WsLayout ws_layout(int B, int Hq, int D, int n_chunks_max) {
+  const size_t parts = (size_t)B * Hq * n_chunks_max;
+  WsLayout w;
+  w.o_floats = (parts * D + 3) / 4 * 4;
+  w.ml_floats = (parts * 2 + 3) / 4 * 4;
+  w.bytes = (w.o_floats + w.ml_floats) * sizeof(float) + (size_t)(B + 1) * sizeof(long long);
+  return w;
+}
+
 // Padded head dim of the masked kernels: a power of two in [32, 256].
 int padded_dim(int D) {
   int p = 32;
@@ -183,10 +201,12 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
                   const int32_t* bt, int max_blocks, int block_size, int B, int Hq, int Hkv,
                   int D, int T_cap, float scale, int chunk, int n_chunks_max, void* ws,
                   size_t ws_bytes, int cache_dt, int q_dt, int out_dt, hipStream_t s,
-                  const void* new_k = nullptr, const void* new_v = nullptr, int in_dt = 0) {
+                  const void* new_k = nullptr, const void* new_v = nullptr, int in_dt = 0,
+                  const char* name = nullptr) {
   const bool app = new_k != nullptr;
-  const char* fn = app ? (PAGED ? "skv_append_decode_attn_paged" : "skv_append_decode_attn")
-                       : (PAGED ? "skv_decode_attn_paged" : "skv_decode_attn");
+  const char* fn = name ? name
+                        : app ? (PAGED ? "skv_append_decode_attn_paged" : "skv_append_decode_attn")
+                              : (PAGED ? "skv_decode_attn_paged" : "skv_decode_attn");
   SKV_REQUIRE(!app || (new_v && dt_ok(in_dt)), SKV_E_INVALID,
               "%s: new_v missing or bad input dtype", fn);
   SKV_REQUIRE(out && q && k && v && lens && ws, SKV_E_INVALID, "%s: null pointer argument", fn);
@@ -230,10 +250,10 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   a.S = kMaxRows / a.hw;
   SKV_REQUIRE(Hkv / a.hw <= 65535, SKV_E_UNSUPPORTED, "%s: H_kv=%d exceeds the grid limit", fn,
               Hkv);
-  const size_t parts = (size_t)Hq * a.n_slots;
+  const WsLayout wl = ws_layout(B, Hq, D, n_chunks_max);
   a.ws_o = static_cast<float*>(ws);
-  a.ws_ml = a.ws_o + parts * D;
-  a.cum = reinterpret_cast<long long*>(a.ws_ml + parts * 2);
+  a.ws_ml = a.ws_o + wl.o_floats;
+  a.cum = reinterpret_cast<long long*>(a.ws_ml + wl.ml_floats);
   a.new_k = new_k;
   a.new_v = new_v;
   a.in_dt = in_dt;
@@ -256,6 +276,43 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   else SKV_MERGE(256, true);
 #undef SKV_MERGE
   return check_launch(fn);
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of skv_decode_attn_noalloc: the split-K workspace in a file-scope
+// device array, kScratchBytes per GPU for the life of the process. Host code
+// never uses the array's name as an address (on the host it is only a
+// handle): the device address comes from hipGetSymbolAddress, queried once
+// per device with that device current, and kept here.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = SKV_DECODE_NOALLOC_MAX_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of this GPU's scratch (the current device's).
+int scratch_ptr(void** out, const char* fn) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(SKV_E_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(SKV_E_UNSUPPORTED, "%s: device %d beyond the %d this library serves", fn, dev,
+                     kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // `dev` is the current device
+      if (e != hipSuccess || p == nullptr)
+        return set_error(SKV_E_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                         hipGetErrorString(e));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return SKV_OK;
 }
 
 }  // namespace
@@ -311,9 +368,8 @@ extern "C" int skv_decode_plan(int B, int H_q, int H_kv, int max_len, long long 
 
 extern "C" size_t skv_decode_workspace_bytes(int B, int H_q, int D, int n_chunks_max) {
   if (B <= 0 || H_q <= 0 || D <= 0 || n_chunks_max <= 0) return 0;
-  const size_t parts = (size_t)B * H_q * n_chunks_max;
   // partials (o[D], m, l) per (query head, slot), then B + 1 int64 prefix sums
-  return parts * (size_t)(D + 2) * sizeof(float) + (size_t)(B + 1) * sizeof(long long);
+  return ws_layout(B, H_q, D, n_chunks_max).bytes;
 }
 
 extern "C" int skv_decode_attn(void* out, const void* q, const void* k_cache, const void* v_cache,
@@ -363,4 +419,26 @@ extern "C" int skv_append_decode_attn_paged(void* out, const void* q, void* k_po
   return decode_common<true>(out, q, k_pool, v_pool, lens, block_table, max_blocks, block_size, B,
                              H_q, H_kv, D, 0, scale, chunk_tokens, n_chunks_max, ws, ws_bytes,
                              cache_dt, q_dt, out_dt, (hipStream_t)stream, new_k, new_v, in_dt);
+}
+
+extern "C" int skv_decode_attn_noalloc(void* out, const void* q, const void* k_cache,
+                                       const void* v_cache, const int32_t* lens, int B, int H_q,
+                                       int H_kv, int D, int T_cap, float scale, int chunk_tokens,
+                                       int n_chunks_max, int cache_dt, int q_dt, int out_dt,
+                                       skv_stream_t stream) {
+  const char* fn = "skv_decode_attn_noalloc";
+  if (B > 0 && H_q > 0 && D > 0 && n_chunks_max > 0) {
+    const size_t need = skv_decode_workspace_bytes(B, H_q, D, n_chunks_max);
+    SKV_REQUIRE(need <= kScratchBytes, SKV_E_WORKSPACE,
+                "%s: this plan needs %zu bytes of split-K scratch, above the %zu-byte maximum "
+                "(call skv_decode_attn with a workspace instead)",
+                fn, need, kScratchBytes);
+  }
+  void* ws = nullptr;
+  const int rc = scratch_ptr(&ws, fn);
+  if (rc) return rc;
+  return decode_common<false>(out, q, k_cache, v_cache, lens, nullptr, 0, 0, B, H_q, H_kv, D,
+                              T_cap, scale, chunk_tokens, n_chunks_max, ws, kScratchBytes,
+                              cache_dt, q_dt, out_dt, (hipStream_t)stream, nullptr, nullptr, 0,
+                              fn);
 }

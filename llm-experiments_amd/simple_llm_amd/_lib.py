@@ -65,6 +65,8 @@ _SIGNATURES = {
                                           _I, _F, _I, _I, _P, _Z, _I, _I, _I, _I, _P]),
     "skv_decode_attn_paged": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I,
                                    _I, _P, _Z, _I, _I, _I, _P]),
+    "skv_decode_attn_noalloc": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _I,
+                                     _I, _P]),
 }
 
 _lib = None
