@@ -255,18 +255,32 @@ int skv_layernorm(float* y, const float* x, const float* gamma, const float* bet
  * [N / split_cols][M][split_cols] output (q, k, v of a fused projection as
  * three contiguous [M, d] blocks). K must be a multiple of 4. Sums run in a
  * fixed order, so results are reproducible run to run.
- * ws (may be NULL) of skv_linear_workspace_bytes(M, N, K) bytes lets a
- * narrow projection (few 16-column tiles) split K over more workgroups and
- * finish in a second kernel; the split sums in a different fixed order, so
- * its bits differ from the unsplit result within fp32 rounding. Calls that
- * share ws must be stream ordered. */
+ * M <= 64 (a decode step's rows): a weight-streaming kernel. ws (may be
+ * NULL) of skv_linear_workspace_bytes(M, N, K) bytes lets a narrow
+ * projection (few 16-column tiles) split K over more workgroups and finish
+ * in a second kernel; the split sums in a different fixed order, so its bits
+ * differ from the unsplit result within fp32 rounding.
+ * M > 64 (a prompt's prefill): a tiled MFMA GEMM (128 x 128 tiles of
+ * v_mfma_f32_32x32x2_f32); with LayerNorm, ws of
+ * skv_linear_workspace_bytes(M, N, K) bytes holds the row statistics,
+ * computed once (without it every column tile computes its rows' own).
+ * Calls that share ws must be stream ordered. */
 int skv_linear(float* y, const float* x, const float* w_t, const float* bias,
                const float* residual, const float* ln_gamma, const float* ln_beta, float ln_eps,
                int M, int N, int K, int activation, int split_cols, void* ws, size_t ws_bytes,
                skv_stream_t stream);
 
-/* Workspace skv_linear can use for these sizes (0: it never splits them). */
+/* Workspace skv_linear can use for these sizes: the split-K partials of a
+ * narrow projection of at most 64 rows (0: it never splits them), or, for
+ * more than 64 rows, M * 2 floats of LayerNorm row statistics. */
 size_t skv_linear_workspace_bytes(int M, int N, int K);
+
+/* y[m, :] = x[rows[m], :] for m < M, x [n_rows, d] (rows clamped into
+ * [0, n_rows)); y and x must not overlap. The prefill's last prompt row of
+ * each sequence goes to the logits projection this way (the reference's
+ * generate_text takes logits[0, -1], generate.py:52). */
+int skv_gather_rows(float* y, const float* x, const int32_t* rows, int M, int d, int n_rows,
+                    skv_stream_t stream);
 
 /* Workspace of skv_argmax: per-slice candidates, 0 bytes when N <= 2048
  * (ws may then be NULL); calls that share it must be stream ordered. */

@@ -15,8 +15,8 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(HERE, "libskv.so")
 
 SOURCES = ["skv_api.hip", "append.hip", "decode_attn.hip", "decode_attn_generic.hip",
-           "decode_attn_generic_paged.hip", "prefill_attn.hip", "model_ops.hip", "sample.hip",
-           "flash_fp32.hip", "bpe_tokenizer.cpp"]
+           "decode_attn_generic_paged.hip", "prefill_attn.hip", "model_ops.hip", "gemm.hip",
+           "sample.hip", "flash_fp32.hip", "bpe_tokenizer.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

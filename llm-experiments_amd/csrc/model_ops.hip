@@ -494,10 +494,29 @@ __global__ void k_next_tokens(int32_t* __restrict__ ids, int32_t* __restrict__ s
   if (p >= 0 && p < seq_cap) seq[(size_t)b * seq_cap + p] = t;
 }
 
+// y[m, :] = x[rows[m], :]; rows are clamped into [0, n_rows).
+__global__ __launch_bounds__(256) void k_gather_rows(float* __restrict__ y,
+                                                     const float* __restrict__ x,
+                                                     const int32_t* __restrict__ rows, int d,
+                                                     int n_rows) {
+  const int m = blockIdx.x;
+  const size_t r = (size_t)min(max(rows[m], 0), n_rows - 1);
+  for (int j = threadIdx.x; j < d; j += blockDim.x) y[(size_t)m * d + j] = x[r * d + j];
+}
+
 }  // namespace
 }  // namespace skv
 
 using namespace skv;
+
+extern "C" int skv_gather_rows(float* y, const float* x, const int32_t* rows, int M, int d,
+                               int n_rows, skv_stream_t stream) {
+  SKV_REQUIRE(y && x && rows, SKV_E_INVALID, "skv_gather_rows: null pointer argument");
+  SKV_REQUIRE(M > 0 && d > 0 && n_rows > 0, SKV_E_INVALID, "skv_gather_rows: dims must be > 0");
+  hipLaunchKernelGGL(k_gather_rows, dim3(M), dim3(256), 0, (hipStream_t)stream, y, x, rows, d,
+                     n_rows);
+  return check_launch("skv_gather_rows");
+}
 
 extern "C" int skv_embed(float* x, const int32_t* ids, const int32_t* pos, const float* embedding,
                          const float* pos_table, int M, int d, int vocab, int ctx,
@@ -523,6 +542,8 @@ extern "C" int skv_layernorm(float* y, const float* x, const float* gamma, const
 
 extern "C" size_t skv_linear_workspace_bytes(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
+  // the GEMM path (more than one 64-row tile): LayerNorm row statistics
+  if (M > kLinRowsPerBlock) return (size_t)M * 2 * sizeof(float);
   const int S = linear_splits(M, N, K);
   return S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
 }
@@ -539,8 +560,13 @@ extern "C" int skv_linear(float* y, const float* x, const float* w_t, const floa
               "skv_linear: N=%d is not a multiple of split_cols=%d", N, split_cols);
   SKV_REQUIRE((ln_gamma == nullptr) == (ln_beta == nullptr), SKV_E_INVALID,
               "skv_linear: LayerNorm needs both gamma and beta");
-  SKV_REQUIRE((M + kLinRowsPerBlock - 1) / kLinRowsPerBlock <= 65535, SKV_E_UNSUPPORTED,
-              "skv_linear: M=%d too large", M);
+  // Many rows (a prompt's prefill): the tiled GEMM, bound by the products
+  // rather than by the weight stream.
+  if (M > kLinRowsPerBlock) {
+    const bool room = ws != nullptr && ws_bytes >= (size_t)M * 2 * sizeof(float);
+    return gemm_linear(y, x, w_t, bias, residual, ln_gamma, ln_beta, ln_eps, M, N, K, activation,
+                       split_cols, room ? static_cast<float*>(ws) : nullptr, (hipStream_t)stream);
+  }
   const int ksteps = (K + 15) / 16;
   // split K when the caller gave room for the partials
   int S = linear_splits(M, N, K);

@@ -199,6 +199,13 @@ int check_launch(const char* what);
 int attn_fwd_f32(float* out, float* L, float* M, const float* q, const float* k, const float* v,
                  const int32_t* start, const int32_t* n_new, int B, int C, int Hq, int Hkv, int D,
                  int T_cap, float scale, hipStream_t s, const char* fn);
+
+// skv_linear over more than 64 rows: the tiled MFMA GEMM (gemm.hip). stats:
+// M * 2 floats of workspace, used when ln_gamma is set.
+int gemm_linear(float* y, const float* x, const float* w_t, const float* bias,
+                const float* residual, const float* ln_gamma, const float* ln_beta, float ln_eps,
+                int M, int N, int K, int activation, int split_cols, float* stats,
+                hipStream_t s);
 }  // namespace skv
 
 #define SKV_REQUIRE(cond, code, ...)                          \

@@ -57,6 +57,7 @@ _SIGNATURES = {
     "skv_bpe_train": (_I, [_P, _Z, _I, _P, _I, ctypes.POINTER(_I)]),
     "skv_bpe_encode": (_I, [_P, _Z, _P, _I, _P, ctypes.POINTER(_Z)]),
     "skv_next_tokens": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "skv_gather_rows": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "skv_decode_attn": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _Z,
                              _I, _I, _I, _P]),
     "skv_append_decode_attn": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I,

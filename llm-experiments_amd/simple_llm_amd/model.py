@@ -1,30 +1,42 @@
-"""The reference model's decode path on the KV cache, on gfx950.
+"""The reference model's generate path on the KV cache, on gfx950.
 
 Drop-in for the caller side of the hot path:
   TransformerModelParams   simple-llm/src/common_backend.py:4-11
   LayerParams field names  simple-llm/src/jax_backend.py:36-55
   forward                  simple-llm/src/jax_backend.py:143-148 (logits of every
-                           position; here computed step by step on the cache)
+                           position: one multi-token prefill over the cache)
   generate_text            simple-llm/src/generate.py:8-71 (same signature)
 
 The model is the reference's JAX model (pre-LN blocks, bias-free attention
 projections, tanh GELU MLP, tied logits, positional table of
-jax_backend.py:25-33). One decode step runs every sequence's next token
-through all layers as HIP kernels of libskv.so: embedding + position,
-fused q/k/v projection (the LayerNorm before it folded into its reads), the
-cache append and decode attention in one call (skv_append_decode_attn), output
-projection with residual, MLP (LayerNorm folded in, GELU, residual), tied
-logits and the next token: skv_argmax when greedy (temperature 0, the
-reference's jnp.argmax branch, jax_backend.py:466-469), otherwise skv_sample
-(repetition penalty, temperature, min-p, top-k, top-p, then a draw).
-PyTorch only owns the memory.
+jax_backend.py:25-33). Generation runs in two phases, all HIP kernels of
+libskv.so:
+  * prefill: every prompt (a ragged batch) goes through all layers at once:
+    embedding + position of every prompt row, the fused q/k/v projection as
+    a tiled MFMA GEMM (LayerNorm applied as the rows are staged), the chunk
+    append into the cache (skv_append_chunk) and causal attention over it
+    (skv_prefill_attn: the fp32 MFMA kernel for an fp32 cache, the bf16 one
+    for a bf16 cache), output projection and MLP as GEMMs; then the logits of
+    each sequence's last prompt row only;
+  * decode: one token per sequence and step: embedding + position, fused
+    q/k/v projection (LayerNorm folded into its reads), the cache append and
+    decode attention in one call (skv_append_decode_attn), output projection
+    with residual, MLP (LayerNorm folded in, GELU, residual), tied logits and
+    the next token, replayed as one HIP graph.
+The next token is skv_argmax when greedy (temperature 0, the reference's
+jnp.argmax branch, jax_backend.py:466-469), otherwise skv_sample (repetition
+penalty, temperature, min-p, top-k, top-p, then a draw). PyTorch only owns
+the memory.
 
 Differences from the reference's generate_text, both documented choices:
-  * tokens attend their cached prefix at their absolute positions; the
-    reference re-runs a left-padded window of context_size per token, which
-    shifts positions while the window is not full (its tokens are therefore
-    not a parity target; parity is checked on the logits of the final
-    sequence, teacher forced);
+  * while the sequence is shorter than context_size, tokens attend their
+    cached prefix at their absolute positions; the reference re-runs a
+    left-padded window of context_size per token, which shifts positions
+    while the window is not full (its tokens are therefore not a parity
+    target; parity is checked on the logits of the final sequence, teacher
+    forced). From context_size tokens on, generate_text does what the
+    reference does: one full-window forward of the last context_size tokens
+    per token (a prefill at positions 0..context_size-1);
   * the draw's uniform comes from splitmix64 of (seed, row, position), so a
     captured step replays deterministically; the reference's jax.random
     stream is not reproduced, only its filtered distribution.
@@ -40,6 +52,7 @@ import torch
 
 from . import _lib
 from .gpu import gpu
+from .gpu.gpu_kv_cache import _prefill_workspace
 from .gpu.gpu_types import GPUContext, KVCache
 
 LAYER_FIELDS = ("attn_wq", "attn_wk", "attn_wv", "attn_wo", "ff_w1", "ff_b1", "ff_w2",
@@ -116,6 +129,31 @@ class _Buffers:
         self.lin_ws = torch.empty(max(lin, 4), dtype=torch.uint8, device=dev)
 
 
+class _PrefillBuffers:
+    """Activations of a prefill of B sequences x C prompt rows (device, fp32).
+
+    Rows are laid out [B, C]: row b*C + i is position start[b] + i of
+    sequence b, valid for i < n_new[b] (the padding rows of shorter prompts
+    run through the projections too, and their attention output is zero)."""
+
+    def __init__(self, dev, B, C, d, mlp):
+        M = B * C
+        self.B, self.C = B, C
+        self.ids = torch.zeros(M, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(M, dtype=torch.int32, device=dev)
+        self.n_new = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.last = torch.zeros(B, dtype=torch.int32, device=dev)  # each sequence's last row
+        self.x = torch.zeros((M, d), device=dev)
+        self.qkv = torch.zeros((3, M, d), device=dev)
+        self.attn = torch.zeros((M, d), device=dev)
+        self.ff = torch.zeros((M, mlp), device=dev)
+        self.x_last = torch.zeros((B, d), device=dev)
+        L = _lib.lib()
+        lin = max(L.skv_linear_workspace_bytes(M, n, k)
+                  for n, k in ((3 * d, d), (d, d), (mlp, d), (d, mlp)))
+        self.lin_ws = torch.empty(max(lin, 4), dtype=torch.uint8, device=dev)
+
+
 class TransformerModel:
     """The reference model's weights on the device, laid out for the decode
     kernels: every matrix transposed to [out, in] (rows read contiguously by
@@ -174,6 +212,13 @@ class TransformerModel:
             self._bufs[B] = _Buffers(self.ctx.device, B, tm.embedding_dim, self.mlp_dim,
                                      tm.vocab_size)
         return self._bufs[B]
+
+    def prefill_buffers(self, B: int, C: int) -> _PrefillBuffers:
+        key = ("prefill", B, C)
+        if key not in self._bufs:
+            self._bufs[key] = _PrefillBuffers(self.ctx.device, B, C, self.tm_params.embedding_dim,
+                                              self.mlp_dim)
+        return self._bufs[key]
 
     # -- one decode step -----------------------------------------------------
 
@@ -250,31 +295,146 @@ class TransformerModel:
 
     # -- many steps ----------------------------------------------------------
 
+    # -- prefill ---------------------------------------------------------------
+
+    def prefill(self, cache: KVCache, tokens: np.ndarray, n_new: Optional[np.ndarray] = None,
+                all_logits: bool = False) -> torch.Tensor:
+        """Run C prompt tokens of every sequence through all layers at once,
+        appending their K/V to the cache after each sequence's current fill.
+
+        tokens: host int array [B, C]; n_new: valid tokens per sequence (<= C,
+        default C), the rest of a row is padding. Returns the logits of each
+        sequence's last new token, [B, V] (the decode buffer, reused by the
+        next call), or with all_logits those of every row, [B, C, V] (a new
+        tensor). The fills advance by n_new."""
+        tm = self.tm_params
+        B = cache.batch_size
+        if cache.n_kv_heads != cache.n_heads or cache.paged:
+            raise ValueError("the model path uses a contiguous multi-head cache")
+        tokens = np.asarray(tokens, np.int64)
+        if tokens.ndim != 2 or tokens.shape[0] != B or tokens.shape[1] <= 0:
+            raise ValueError(f"tokens must be [batch_size={B}, C] with C >= 1")
+        C = int(tokens.shape[1])
+        n_host = (np.full(B, C, np.int64) if n_new is None
+                  else np.asarray(n_new, np.int64).reshape(B))
+        if (n_host < 0).any() or (n_host > C).any():
+            raise ValueError(f"n_new entries must lie in [0, {C}]")
+        if tokens.size and (tokens.min() < 0 or tokens.max() >= tm.vocab_size):
+            raise ValueError("token out of the vocabulary")
+        start = cache.layers[0].host_lens.copy()
+        if int((start + n_host).max()) > cache.max_seq_len:
+            raise ValueError(f"Cache is full: a prefill of {int(n_host.max())} tokens after "
+                             f"{int(start.max())}, max_seq_len={cache.max_seq_len}")
+        pb = self.prefill_buffers(B, C)
+        d, H, D, T = tm.embedding_dim, tm.n_heads, self.head_dim, cache.max_seq_len
+        M = B * C
+        pos = start[:, None] + np.arange(C)[None, :]
+        pb.ids.copy_(torch.from_numpy(tokens.reshape(-1).astype(np.int32)))
+        pb.pos.copy_(torch.from_numpy(np.minimum(pos, T - 1).reshape(-1).astype(np.int32)))
+        pb.n_new.copy_(torch.from_numpy(n_host.astype(np.int32)))
+        pb.last.copy_(torch.from_numpy(
+            (np.arange(B) * C + np.maximum(n_host - 1, 0)).astype(np.int32)))
+        L = _lib.lib()
+        s = _lib.stream_handle(self.ctx.device)
+        chk = _lib.check
+        cdt = _lib.dtype_code(cache.dtype)
+        scale = 1.0 / float(np.sqrt(D))
+        x, qkv, attn, ff = pb.x.data_ptr(), pb.qkv.data_ptr(), pb.attn.data_ptr(), pb.ff.data_ptr()
+        q_ptr, k_ptr, v_ptr = qkv, qkv + M * d * 4, qkv + 2 * M * d * 4
+        ws, wn = pb.lin_ws.data_ptr(), pb.lin_ws.numel()
+        n_ptr = pb.n_new.data_ptr()
+        ns = ctypes.c_int()
+        chk(L.skv_prefill_plan(B, C, H, H, max(int((start + n_host).max()), 1), ctypes.byref(ns)),
+            "skv_prefill_plan")
+        need = L.skv_prefill_workspace_bytes(B, C, H, D, ns.value)
+        pws = _prefill_workspace(self.ctx, need)
+        pws_ptr = pws.data_ptr() if pws is not None else None
+        pws_n = pws.numel() if pws is not None else 0
+        chk(L.skv_embed(x, pb.ids.data_ptr(), pb.pos.data_ptr(), self.emb.data_ptr(),
+                        self.pe.data_ptr(), M, d, tm.vocab_size, self.pe.shape[0], s), "skv_embed")
+        for lw, layer in zip(self.layers, cache.layers):
+            kc, vc = layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr()
+            lens = layer.lens.data_ptr()
+            # q, k, v = LN1(x) . [Wq Wk Wv] over every prompt row: [3][B, C, H, D]
+            chk(L.skv_linear(qkv, x, lw["wqkv_t"].data_ptr(), None, None, lw["g1"].data_ptr(),
+                             lw["be1"].data_ptr(), 1e-5, M, 3 * d, d, 0, d, ws, wn, s),
+                "skv_linear")
+            # the chunk's k, v at each sequence's fill, then causal attention of
+            # its queries over prefix + chunk; then the fill moves past the chunk
+            chk(L.skv_append_chunk(kc, vc, k_ptr, v_ptr, lens, n_ptr, B, C, H, D, T, cdt,
+                                   _lib.F32, s), "skv_append_chunk")
+            chk(L.skv_prefill_attn(attn, q_ptr, kc, vc, lens, n_ptr, B, C, H, H, D, T, scale,
+                                   ns.value, pws_ptr, pws_n, cdt, _lib.F32, _lib.F32, s),
+                "skv_prefill_attn")
+            chk(L.skv_advance(lens, n_ptr, C, B, T, s), "skv_advance")
+            # x += attn . Wo; ff = gelu(LN2(x) . W1 + b1); x += ff . W2 + b2
+            chk(L.skv_linear(x, attn, lw["wo_t"].data_ptr(), None, x, None, None, 0.0, M, d, d, 0,
+                             0, ws, wn, s), "skv_linear")
+            chk(L.skv_linear(ff, x, lw["w1_t"].data_ptr(), lw["b1"].data_ptr(), None,
+                             lw["g2"].data_ptr(), lw["be2"].data_ptr(), 1e-5, M, self.mlp_dim, d,
+                             1, 0, ws, wn, s), "skv_linear")
+            chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, None, None, 0.0,
+                             M, d, self.mlp_dim, 0, 0, ws, wn, s), "skv_linear")
+        for layer in cache.layers:
+            layer.host_lens = np.minimum(start + n_host, T)
+        if all_logits:
+            out = torch.empty((B, C, tm.vocab_size), device=self.ctx.device)
+            lws = torch.empty(max(L.skv_linear_workspace_bytes(M, tm.vocab_size, d), 4),
+                              dtype=torch.uint8, device=self.ctx.device)
+            chk(L.skv_linear(out.data_ptr(), x, self.emb.data_ptr(), None, None, None, None, 0.0,
+                             M, tm.vocab_size, d, 0, 0, lws.data_ptr(), lws.numel(), s),
+                "skv_linear")
+            return out
+        # the logits of each sequence's last new row (generate.py:52 takes logits[0, -1])
+        bf = self.buffers(B)
+        chk(L.skv_gather_rows(pb.x_last.data_ptr(), x, pb.last.data_ptr(), B, d, M, s),
+            "skv_gather_rows")
+        chk(L.skv_linear(bf.logits.data_ptr(), pb.x_last.data_ptr(), self.emb.data_ptr(), None,
+                         None, None, None, 0.0, B, tm.vocab_size, d, 0, 0, bf.lin_ws.data_ptr(),
+                         bf.lin_ws.numel(), s), "skv_linear")
+        return bf.logits
+
+    # -- logits of whole sequences ------------------------------------------
+
     def forward(self, tokens: np.ndarray) -> np.ndarray:
         """Logits of every position of [B, T] token ids (T <= context_size),
-        computed step by step on a fresh cache: row t equals the reference's
-        forward (jax_backend.py:143-148) at position t. Returns float32 host
-        array [B, T, V]."""
+        as the reference's forward (jax_backend.py:143-148): one prefill of
+        all T tokens on a fresh cache. Returns float32 host array [B, T, V]."""
+        tokens = np.asarray(tokens, np.int32)
+        B, T = tokens.shape
+        if T > self.tm_params.context_size:
+            raise ValueError("sequence longer than context_size")
+        cache = self.new_cache(B)
+        return self.prefill(cache, tokens, all_logits=True).cpu().numpy()
+
+    def forward_decode(self, tokens: np.ndarray, n_prefill: int = 0) -> np.ndarray:
+        """forward() computed through the decode step instead: the first
+        n_prefill tokens as one prefill (logits of every row), then one cached
+        decode step per token. Returns float32 host array [B, T, V]."""
         tokens = np.asarray(tokens, np.int32)
         B, T = tokens.shape
         if T > self.tm_params.context_size:
             raise ValueError("sequence longer than context_size")
         cache = self.new_cache(B)
         out = np.zeros((B, T, self.tm_params.vocab_size), np.float32)
+        if n_prefill > 0:
+            out[:, :n_prefill] = self.prefill(cache, tokens[:, :n_prefill],
+                                              all_logits=True).cpu().numpy()
         ids = torch.from_numpy(tokens).to(self.ctx.device)
-        for t in range(T):
+        for t in range(n_prefill, T):
             out[:, t] = self.forward_step(cache, ids[:, t].contiguous()).cpu().numpy()
         return out
 
 
 class Generator:
-    """Greedy generation of a batch of (possibly ragged) prompts on the device.
+    """Generation of a batch of (possibly ragged) prompts on the device.
 
-    Every step feeds each sequence its next prompt token while it is inside
-    its prompt and its previous argmax afterwards (skv_next_tokens), so the
-    loop never waits for the host. With use_graph the step is captured once
-    into a HIP graph (torch.cuda.CUDAGraph over the library's launches) and
-    replayed.
+    run() prefills every prompt at once (TransformerModel.prefill: the
+    logits of each prompt's last token give its first new token), then
+    decodes one token per sequence and step, feeding each sequence its
+    previous token (skv_next_tokens), so the loop never waits for the host.
+    With use_graph the decode step is captured once into a HIP graph
+    (torch.cuda.CUDAGraph over the library's launches) and replayed.
     """
 
     def __init__(self, model: TransformerModel, prompts: Sequence[Sequence[int]],
@@ -295,51 +455,52 @@ class Generator:
             raise ValueError("total_len shorter than a prompt")
         if int(tot.max()) > tm.context_size:
             raise ValueError(f"total length {int(tot.max())} exceeds context_size "
-                             f"{tm.context_size} (the cache does not slide)")
+                             f"{tm.context_size} (the cache does not slide; generate_text "
+                             f"continues past it with full-window forwards)")
         for p in prompts:
             if min(p) < 0 or max(p) >= tm.vocab_size:
                 raise ValueError("prompt token out of the vocabulary")
+        if temperature < 0 or top_k < 0 or min_p < 0 or repetition_penalty <= 0 \
+                or repetition_window < 0:
+            raise ValueError("bad sampling parameters")
+        if tm.vocab_size > 65536 and (temperature != 0.0 or repetition_penalty != 1.0):
+            raise ValueError("device sampling supports vocab_size <= 65536")
         dev = model.ctx.device
         self.B, self.plen, self.tot = B, plen, tot
         Pm = int(plen.max())
         pr = np.zeros((B, Pm), np.int32)
         for b, p in enumerate(prompts):
             pr[b, :len(p)] = p
+        self.prompt_host = pr
         self.prompt = torch.from_numpy(pr).to(dev)
         self.prompt_len = torch.from_numpy(plen).to(dev)
         self.seq = torch.zeros((B, tm.context_size), dtype=torch.int32, device=dev)
         self.cache = model.new_cache(B)
         self.bufs = model.buffers(B)
-        self.steps = int(tot.max()) - 1  # position p's step produces token p + 1
+        # decode steps after the prefill: the step at position p produces token p + 1
+        self.steps = max(int((tot - 1 - plen).max()), 0)
         self.use_graph = use_graph
         self.graph = None
-        if temperature < 0 or top_k < 0 or min_p < 0 or repetition_penalty <= 0 \
-                or repetition_window < 0:
-            raise ValueError("bad sampling parameters")
-        if tm.vocab_size > 65536 and (temperature != 0.0 or repetition_penalty != 1.0):
-            raise ValueError("device sampling supports vocab_size <= 65536")
         self.sampling = (float(temperature), int(top_k), float(top_p), float(min_p),
                          float(repetition_penalty), int(repetition_window))
         self.seed = int(seed) & ((1 << 64) - 1)
         # greedy without a penalty takes the multi-workgroup argmax
         self.greedy = temperature == 0.0 and repetition_penalty == 1.0
+        self.reset()
 
     def reset(self) -> None:
-        """Rewind to before the first step (empty cache, no tokens), keeping
-        the captured graph, so run() can be repeated."""
+        """Rewind to before the prefill (empty cache, only the prompts in the
+        token buffer), keeping the captured graph, so run() can be repeated."""
         self.cache.current_len = 0
         self.seq.zero_()
+        self.seq[:, :self.prompt.shape[1]].copy_(self.prompt)
         self.bufs.argmax.zero_()
 
-    def _one_step(self):
+    def _pick(self) -> None:
+        """Next token of every sequence from the logits buffer into argmax."""
         L = _lib.lib()
         m, c, bf = self.model, self.cache, self.bufs
         s = _lib.stream_handle(m.ctx.device)
-        _lib.check(L.skv_next_tokens(bf.ids.data_ptr(), self.seq.data_ptr(), bf.argmax.data_ptr(),
-                                     self.prompt.data_ptr(), self.prompt_len.data_ptr(),
-                                     c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
-                                     self.seq.shape[1], s), "skv_next_tokens")
-        m._launch_step(c, bf)
         if self.greedy:
             _lib.check(L.skv_argmax(bf.argmax.data_ptr(), bf.logits.data_ptr(), self.B,
                                     m.tm_params.vocab_size, bf.arg_ws.data_ptr(),
@@ -355,8 +516,27 @@ class Generator:
                                     m.tm_params.vocab_size, T, k, p, mp, pen, win, self.seed,
                                     s), "skv_sample")
 
+    def _one_step(self):
+        L = _lib.lib()
+        m, c, bf = self.model, self.cache, self.bufs
+        s = _lib.stream_handle(m.ctx.device)
+        _lib.check(L.skv_next_tokens(bf.ids.data_ptr(), self.seq.data_ptr(), bf.argmax.data_ptr(),
+                                     self.prompt.data_ptr(), self.prompt_len.data_ptr(),
+                                     c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
+                                     self.seq.shape[1], s), "skv_next_tokens")
+        m._launch_step(c, bf)
+        self._pick()
+
+    def prefill(self) -> None:
+        """Every prompt through the model at once; the first new token of
+        each sequence goes to the argmax buffer."""
+        self.model.prefill(self.cache, self.prompt_host, self.plen)
+        self._pick()
+
     def run(self) -> List[List[int]]:
-        """Run all steps; returns every sequence's tokens (prompt + output)."""
+        """Prefill, then all decode steps; returns every sequence's tokens
+        (prompt + output)."""
+        self.prefill()
         steps = self.steps
         if steps > 0:
             if self.use_graph:
@@ -373,7 +553,7 @@ class Generator:
             else:
                 for _ in range(steps):
                     self._one_step()
-        # record the last argmax at its position (the final token)
+        # record the last new token at its position
         L = _lib.lib()
         s = _lib.stream_handle(self.model.ctx.device)
         _lib.check(L.skv_next_tokens(self.bufs.ids.data_ptr(), self.seq.data_ptr(),
@@ -388,6 +568,47 @@ class Generator:
         return [seq[b, :int(self.tot[b])].tolist() for b in range(self.B)]
 
 
+class _WindowDecoder:
+    """Next tokens past context_size, as the reference's generate_text makes
+    them (generate.py:29-69): each from a full forward of the last
+    context_size tokens at positions 0..context_size-1 (one prefill on a
+    one-sequence cache, logits of its last row), then greedy or sample_token
+    over the tokens so far."""
+
+    def __init__(self, model: TransformerModel, max_len: int, sampling, seed: int):
+        tm = model.tm_params
+        self.model = model
+        self.ctx_len = tm.context_size
+        self.cache = model.new_cache(1)
+        self.bufs = model.buffers(1)
+        self.seq = torch.zeros((1, max(max_len, 1)), dtype=torch.int32, device=model.ctx.device)
+        self.lens = torch.zeros(1, dtype=torch.int32, device=model.ctx.device)
+        self.sampling = sampling
+        self.seed = seed
+        self.greedy = sampling[0] == 0.0 and sampling[4] == 1.0
+
+    def next_token(self, tokens: List[int]) -> int:
+        m, bf = self.model, self.bufs
+        L = _lib.lib()
+        s = _lib.stream_handle(m.ctx.device)
+        self.cache.current_len = 0
+        m.prefill(self.cache, np.asarray([tokens[-self.ctx_len:]], np.int64))
+        if self.greedy:
+            _lib.check(L.skv_argmax(bf.argmax.data_ptr(), bf.logits.data_ptr(), 1,
+                                    m.tm_params.vocab_size, bf.arg_ws.data_ptr(),
+                                    bf.arg_ws.numel(), s), "skv_argmax")
+        else:
+            n = len(tokens)
+            self.seq[0, :n].copy_(torch.tensor(tokens, dtype=torch.int32))
+            self.lens.fill_(n)
+            T, k, p, mp, pen, win = self.sampling
+            _lib.check(L.skv_sample(bf.argmax.data_ptr(), None, bf.logits.data_ptr(),
+                                    self.seq.data_ptr(), self.seq.shape[1], self.lens.data_ptr(),
+                                    1, m.tm_params.vocab_size, T, k, p, mp, pen, win, self.seed,
+                                    s), "skv_sample")
+        return int(bf.argmax[0].item())
+
+
 def generate_text(model: TransformerModel, prompt_tokens, max_tokens=100, temperature=1.0,
                   top_k=0, top_p=1.0, min_p=0.0, repetition_penalty=1.0, repetition_window=64,
                   use_graph: bool = True, seed: int = 42):
@@ -396,22 +617,45 @@ def generate_text(model: TransformerModel, prompt_tokens, max_tokens=100, temper
     ints. temperature = 0 is greedy; otherwise each token is drawn on the
     device from sample_token's filtered distribution (jax_backend.py:413-515)
     with a uniform keyed by (seed, position) -- the reference's jax.random
-    stream itself is not reproduced. The prompt plus the output must fit in
-    context_size (the cache does not slide)."""
+    stream itself is not reproduced. Up to context_size tokens the prompt is
+    prefilled and the rest decoded on the cache; past it, every token comes
+    from a full forward of the last context_size tokens, the reference's
+    sliding window (generate.py:30-33)."""
     prompt = [int(t) for t in prompt_tokens]
     if max_tokens <= 0:
         return prompt
-    g = Generator(model, [prompt], len(prompt) + int(max_tokens), use_graph=use_graph,
-                  temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p,
-                  repetition_penalty=repetition_penalty, repetition_window=repetition_window,
-                  seed=seed)
-    return g.run()[0]
+    tm = model.tm_params
+    if not prompt:
+        raise ValueError("every prompt needs at least one token")
+    if min(prompt) < 0 or max(prompt) >= tm.vocab_size:
+        raise ValueError("prompt token out of the vocabulary")
+    total = len(prompt) + int(max_tokens)
+    sampling = dict(temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p,
+                    repetition_penalty=repetition_penalty, repetition_window=repetition_window,
+                    seed=seed)
+    if len(prompt) < tm.context_size:
+        g = Generator(model, [prompt], min(total, tm.context_size), use_graph=use_graph,
+                      **sampling)
+        tokens = g.run()[0]
+        if len(tokens) == total:
+            return tokens
+        win = _WindowDecoder(model, total, g.sampling, g.seed)
+    else:
+        Generator(model, [prompt[:1]], 1, **sampling)  # the same argument checks
+        tokens = list(prompt)
+        win = _WindowDecoder(model, total, (float(temperature), int(top_k), float(top_p),
+                                            float(min_p), float(repetition_penalty),
+                                            int(repetition_window)),
+                             int(seed) & ((1 << 64) - 1))
+    while len(tokens) < total:
+        tokens.append(win.next_token(tokens))
+    return tokens
 
 
 def generate_batch(model: TransformerModel, prompts: Sequence[Sequence[int]], total_len,
                    use_graph: bool = True, **sampling) -> List[List[int]]:
     """Generation of a ragged batch until each sequence holds total_len
-    tokens (an int or one per sequence); greedy unless sampling parameters
-    (temperature, top_k, top_p, min_p, repetition_penalty, repetition_window,
-    seed) are given."""
+    tokens (an int or one per sequence, at most context_size); greedy unless
+    sampling parameters (temperature, top_k, top_p, min_p, repetition_penalty,
+    repetition_window, seed) are given."""
     return Generator(model, prompts, total_len, use_graph=use_graph, **sampling).run()

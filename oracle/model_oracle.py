@@ -72,11 +72,12 @@ def _f64(params):
             np.asarray(params["pos_encoding"], np.float64), layers)
 
 
-def forward(params: dict, tokens: np.ndarray, n_heads: int) -> np.ndarray:
+def forward(params: dict, tokens: np.ndarray, n_heads: int, last: int | None = None) -> np.ndarray:
     """Full causal forward of [B, T] token ids -> logits [B, T, V] (float64).
 
     params: {"embedding": [V, d], "pos_encoding": [ctx, d], "layers": [dict of
-    LAYER_FIELDS]} with the reference's shapes (W as [in, out]).
+    LAYER_FIELDS]} with the reference's shapes (W as [in, out]). last: only
+    the logits of the last `last` positions, [B, last, V] (the same rows).
     """
     E, PE, layers = _f64(params)
     tokens = np.asarray(tokens)
@@ -99,6 +100,8 @@ def forward(params: dict, tokens: np.ndarray, n_heads: int) -> np.ndarray:
         h = layer_norm(x, lp["ln_gamma2"], lp["ln_beta2"])
         f = gelu_tanh(h @ lp["ff_w1"] + lp["ff_b1"])
         x = x + f @ lp["ff_w2"] + lp["ff_b2"]
+    if last is not None:
+        x = x[:, T - last:]
     return x @ E.T
 
 
