@@ -194,8 +194,31 @@ def cpu_baseline(args, k_dev, v_dev, q_all, k_all, v_all):
     }
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _with_cpu_model(cpu):
+    if cpu is not None:
+        cpu = dict(cpu)
+        cpu.setdefault("cpu_model", cpu_model())
+    return cpu
+
+
 def _record(metric, value, unit, steps, warmup, ms_per_step, dtype, config, roofline, cpu,
             **extra):
+    cpu = _with_cpu_model(cpu)
+    for k in list(extra):
+        if k.startswith("cpu") and isinstance(extra[k], dict):
+            extra[k] = _with_cpu_model(extra[k])
     rec = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps,
            "warmup": warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic",
@@ -245,8 +268,10 @@ def _time_reference_generate(params, prompt, n_heads, context, budget_s, max_tok
 
 
 def _model_workload(args, ctx, tm, prompts, total_len, label, kv_dtypes):
-    """Greedy generation of `prompts` to `total_len` tokens with HIP-graph
-    replay; per KV dtype, the mean of 3 timed runs after a warm-up run."""
+    """Greedy generation of `prompts` to `total_len` tokens: one prefill of
+    every prompt, then the decode steps with HIP-graph replay; per KV dtype,
+    the mean of 3 timed runs after a warm-up run, and the prefill alone over
+    3 more runs."""
     import numpy as np
     import torch
 
@@ -268,11 +293,20 @@ def _model_workload(args, ctx, tm, prompts, total_len, label, kv_dtypes):
             torch.cuda.synchronize()
             times.append(time.perf_counter() - t0)
         assert out2 == out, "graph replays must reproduce the first run"
+        pre = []
+        for _ in range(3):
+            g.reset()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            g.prefill()
+            torch.cuda.synchronize()
+            pre.append(time.perf_counter() - t0)
         gen = sum(total_len - len(p) for p in prompts)
+        run_s, pre_s = float(np.mean(times)), float(np.mean(pre))
         runs[str(kvd).replace("torch.", "")] = {
-            "run_s": float(np.mean(times)), "steps": g.steps,
-            "generated_tokens": gen, "tokens_per_s": gen / float(np.mean(times)),
-            "step_us": float(np.mean(times)) / g.steps * 1e6}
+            "run_s": run_s, "prefill_s": pre_s, "prompt_tokens": int(sum(len(p) for p in prompts)),
+            "steps": g.steps, "generated_tokens": gen, "tokens_per_s": gen / run_s,
+            "step_us": (run_s - pre_s) / max(g.steps, 1) * 1e6}
     d, L, V = tm.embedding_dim, tm.n_layers, tm.vocab_size
     weight_bytes = 4 * (V * d + L * (4 * d * d + 2 * d * model.mlp_dim + model.mlp_dim + 7 * d))
     return params, model, runs, weight_bytes
@@ -310,7 +344,9 @@ def run_c1(args, ctx):
         "fp32",
         {"workload": "C1 tiny LM: 4 layers, d 256, 4 heads x 64, MLP 1024, vocab 256, context "
                      "256, fp32 weights and KV, 64-token prompt + 192 greedy tokens, batch 1; "
-                     "prompt fed token by token through the same cached step (HIP graph)",
+                     "the prompt prefilled in one multi-token pass (its logits give the first "
+                     "token), then 191 cached decode steps replayed from one HIP graph; value "
+                     "= generated tokens / whole run (prefill included)",
          "batch": 1, "prompt": 64, "generated": 192},
         {"bound": "launch latency", "note": "12.8 MB of weights per token; ~40 launches per "
                                             "step replayed from one HIP graph",
@@ -360,8 +396,10 @@ def run_c3(args, ctx):
         r32["step_us"] / 1e3, "fp32",
         {"workload": "C3 GPT-2-small shape: 12 layers, d 768, 12 heads x 64, vocab 50304, "
                      "context 1024, batch 16, prompts U[32,512], greedy to 1024 tokens, fp32 "
-                     "weights; value = generated tokens/s with the fp32 KV cache (bf16 KV in "
-                     "runs)", "batch": 16, "prompt_lens": plen.tolist()},
+                     "weights; the prompts prefilled in one ragged multi-token pass, then the "
+                     "cached decode steps (HIP graph); value = generated tokens / whole run "
+                     "(prefill included) with the fp32 KV cache (bf16 KV in runs)",
+         "batch": 16, "prompt_lens": plen.tolist()},
         {"bound": "hbm", "achieved": roof["float32"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": roof["float32"] / HBM_PEAK_GBS, "traffic": None,
          "note": "per step: all weights + mean K/V prefix of 16 sequences, over step time",
@@ -742,6 +780,23 @@ def main():
     assert cache.layers[0].lens.cpu().tolist() == [FILL + args.steps] * B
 
     chunk, n_chunks = gpu.decode_plan(ctx, B, H, H, max_len)
+    # the same K steps again with an event pair per call (outside the timed
+    # region above, whose single pair carries no per-call markers): the
+    # spread of the call time over the run
+    cache.current_len = FILL
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for i, (e0, e1) in enumerate(evs):
+        e0.record()
+        step(i)
+        e1.record()
+    torch.cuda.synchronize()
+    per = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+    per_call = {"events": "one pair per call, a second pass over the same steps",
+                "mean_us": float(per.mean()), "median_us": float(np.median(per)),
+                "min_us": float(per.min()), "max_us": float(per.max()),
+                "first5_us": [round(float(x), 1) for x in per[:5]]}
     prefill = None if args.no_prefill else time_prefill(ctx, cache, reps=10)
     cpu = None
     if not args.no_cpu_baseline:
@@ -781,8 +836,9 @@ def main():
             "mean_call_us": mean_s * 1e6,
             "split_k": {"chunk_tokens": chunk, "n_chunks": n_chunks},
             "algorithmic_bytes_per_call": bytes_per_call,
+            "per_call": per_call,
         },
-        "cpu_baseline": cpu,
+        "cpu_baseline": _with_cpu_model(cpu),
         "prefill": prefill,
     }
     print(json.dumps(rec), flush=True)

@@ -55,7 +55,9 @@ def kv_cache_create(ctx: GPUContext, config: KVCacheConfig) -> KVCache:
     caches are [batch_size * max_seq_len, n_kv_heads * head_dim] per tensor;
     paged caches are a pool [n_blocks * block_size, n_kv_heads * head_dim]
     whose page table starts as the identity mapping (sequence b owns pages
-    b*max_blocks .. b*max_blocks + max_blocks - 1) when the pool is big enough.
+    b*max_blocks .. b*max_blocks + max_blocks - 1) when the pool is big
+    enough; a smaller pool has no table until kv_cache_set_block_table
+    installs one (appends and attention raise ValueError before that).
     """
     if config.batch_size <= 0:
         raise ValueError(f"batch_size must be > 0, got {config.batch_size}")
@@ -84,10 +86,9 @@ def kv_cache_create(ctx: GPUContext, config: KVCacheConfig) -> KVCache:
         max_blocks = -(-config.max_seq_len // bs)
         n_blocks = config.n_blocks or B * max_blocks
         rows = n_blocks * bs
-        ident = torch.arange(B * max_blocks, dtype=torch.int32).reshape(B, max_blocks)
-        if n_blocks < B * max_blocks:
-            ident = ident % n_blocks  # placeholder: caller installs a real table
-        block_table = ident.to(ctx.device)
+        if n_blocks >= B * max_blocks:
+            block_table = torch.arange(B * max_blocks, dtype=torch.int32).reshape(
+                B, max_blocks).to(ctx.device)
     else:
         rows = B * config.max_seq_len
 
@@ -135,6 +136,19 @@ def kv_cache_set_block_table(cache: KVCache, block_table: torch.Tensor) -> None:
 def _check_layer(cache: KVCache, layer_idx: int) -> None:
     if layer_idx < 0 or layer_idx >= len(cache.layers):
         raise ValueError(f"layer_idx {layer_idx} out of range [0, {len(cache.layers)})")
+    if cache.paged and cache.block_table is None:
+        raise ValueError("the paged cache has no block table yet: its pool is smaller than "
+                         "batch_size * ceil(max_seq_len / block_size) pages, so install one "
+                         "with kv_cache_set_block_table first")
+
+
+def _check_max_len(max_len: int, fills: np.ndarray) -> None:
+    # the split-K grid covers batch_size * max_len tokens of the flat token
+    # stream; a fill beyond it would come back as NaN rows
+    top = int(fills.max()) if fills.size else 0
+    if max_len < top:
+        raise ValueError(f"max_len={max_len} is below the longest fill {top}: the attention "
+                         f"plan would not cover every filled position")
 
 
 def _check_tensor(t: torch.Tensor, name: str, device: torch.device) -> None:
@@ -259,6 +273,7 @@ def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.T
     (default: the host mirror's maximum), used to size the split-K grid; the
     chunk size follows the batch's total fill (host mirror).
     """
+    _check_layer(cache, layer_idx)
     layer = cache.layers[layer_idx]
     dev = layer.lens.device
     _check_tensor(q, "q_new", dev)
@@ -269,6 +284,7 @@ def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.T
                          f"{cache.batch_size * e_q} elements")
     if max_len is None:
         max_len = int(layer.host_lens.max())
+    _check_max_len(max_len, layer.host_lens)
     total = int(np.minimum(layer.host_lens, max_len).sum())
     chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
                                   total)
@@ -332,6 +348,7 @@ def kv_cache_append_attend(ctx: GPUContext, cache: KVCache, layer_idx: int, new_
         max_len = int(after.max())
         total = int(after.sum())
     else:
+        _check_max_len(max_len, after)
         total = int(np.minimum(after, max_len).sum())
     chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
                                   total)

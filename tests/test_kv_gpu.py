@@ -325,15 +325,30 @@ def test_decode_empty_sequence_and_plan_overflow(gpu_ctx):
     assert not got[0].any()
     want = ko.decode_attention(q, k, v, lens)
     assert rel_err(got[1:], want[1:]) < FP32_TOL
-    # a plan sized for max_len=256: its workgroups cover B * 256 = 768 tokens
-    # of the flat token stream [0 | 300 | 1024]. Sequence 1 (tokens 0-299)
-    # fits and is exact although longer than max_len; sequence 2 runs past
-    # the planned grid and is flagged with NaN, never read out of bounds.
-    gpu_ctx.config.decode_chunk_tokens = 256
-    try:
-        got = _decode(gpu, gpu_ctx, cache, q, max_len=256)
-    finally:
-        gpu_ctx.config.decode_chunk_tokens = 0
+    # the Python API rejects a max_len below the fills before any GPU work
+    with pytest.raises(ValueError, match="max_len=256 is below the longest fill 1024"):
+        _decode(gpu, gpu_ctx, cache, q, max_len=256)
+    # the C ABI with a plan sized for max_len=256: its workgroups cover
+    # B * 256 = 768 tokens of the flat token stream [0 | 300 | 1024].
+    # Sequence 1 (tokens 0-299) fits and is exact although longer than
+    # max_len; sequence 2 runs past the planned grid and is flagged with NaN,
+    # never read out of bounds.
+    import ctypes
+    from simple_llm_amd import _lib
+    L = _lib.lib()
+    chunk, nch = ctypes.c_int(), ctypes.c_int()
+    _lib.check(L.skv_decode_plan(B, H, H, 256, 0, 256, ctypes.byref(chunk), ctypes.byref(nch)),
+               "plan")
+    need = L.skv_decode_workspace_bytes(B, H, D, nch.value)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    qd = to_dev(q)
+    out = torch.empty_like(qd)
+    layer = cache.layers[0]
+    _lib.check(L.skv_decode_attn(out.data_ptr(), qd.data_ptr(), layer.k_cache.buffer.data_ptr(),
+                                 layer.v_cache.buffer.data_ptr(), layer.lens.data_ptr(), B, H, H,
+                                 D, T, float(D ** -0.5), chunk.value, nch.value, ws.data_ptr(),
+                                 need, 0, 0, 0, _lib.stream_handle()), "decode")
+    got = out.cpu().numpy()
     assert not got[0].any()
     assert rel_err(got[1:2], want[1:2]) < FP32_TOL
     assert np.isnan(got[2]).all()
@@ -555,3 +570,57 @@ def test_append_attend_equals_append_then_attend(gpu_ctx, B, T, Hq, Hkv, D, cdt,
         assert rel_err(b_, a_) < 1e-6, step
         want = ko.decode_attention(q, kw, vw, fills)
         assert rel_err(b_, want) < 1e-4, step
+
+
+@pytest.mark.parametrize("variant", ["bench", "retiring"])
+def test_c2_full_run_every_step_matches_c_oracle(gpu_ctx, variant):
+    """C2 as the bench runs it (fp32 cache [8, 8, 2048, 64], start lengths
+    U[1, 2047] from seed 0, 256 steps of append + attention through
+    kv_cache_append_attend). Every step's output is checked against
+    oracle/c/kv_attn_ref.c over a host mirror of the cache updated by the
+    append rule, and the fills against that rule exactly. With seed 0 no
+    sequence reaches 2048 within 256 steps (the longest starts at 1742), so
+    the "retiring" variant starts four of the sequences at 2047, 1998, 1900
+    and 1793: they reach 2048 at steps 1, 50, 148 and 255 and then retire (no
+    append; their output stays attention over the full cache)."""
+    banner(f"C2 full run ({variant}): 256 steps vs C oracle")
+    from oracle import c_oracle
+    gpu = _gpu()
+    B, H, T, Dh, steps = 8, 8, 2048, 64, 256
+    lens0 = np.random.default_rng(0).integers(1, 2048, B).astype(np.int64)
+    if variant == "retiring":
+        lens0[::2] = [2047, 1998, 1900, 1793]
+    cache = gpu.kv_cache_create(gpu_ctx, gpu.KVCacheConfig(B, T, 1, H, Dh))
+    layer = cache.layers[0]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    layer.k_cache.buffer.copy_(torch.randn(layer.k_cache.buffer.shape, generator=g,
+                                           device="cuda"))
+    layer.v_cache.buffer.copy_(torch.randn(layer.v_cache.buffer.shape, generator=g,
+                                           device="cuda"))
+    layer.lens.copy_(torch.from_numpy(lens0.astype(np.int32)))
+    layer.host_lens = lens0.copy()
+    kc = layer.k_cache.buffer.cpu().numpy().reshape(B, T, H, Dh).copy()
+    vc = layer.v_cache.buffer.cpu().numpy().reshape(B, T, H, Dh).copy()
+    q_all = torch.randn((steps, B, H, Dh), generator=g, device="cuda")
+    k_all = torch.randn((steps, B, H, Dh), generator=g, device="cuda")
+    v_all = torch.randn((steps, B, H, Dh), generator=g, device="cuda")
+    qs, ks, vs = q_all.cpu().numpy(), k_all.cpu().numpy(), v_all.cpu().numpy()
+    out = torch.empty((B, H, Dh), device="cuda")
+    lens = lens0.astype(np.int32).copy()
+    worst = 0.0
+    for n in range(steps):
+        fills = gpu.kv_cache_append_attend(gpu_ctx, cache, 0, k_all[n], v_all[n], q_all[n], out,
+                                           max_len=min(int(lens0.max()) + steps, T))
+        for b in range(B):
+            if lens[b] < T:
+                kc[b, lens[b]], vc[b, lens[b]] = ks[n, b], vs[n, b]
+                lens[b] += 1
+        np.testing.assert_array_equal(fills, lens)
+        want = c_oracle.decode_attn(qs[n], kc, vc, lens, cache_bf16=False)
+        err = rel_err(out.cpu().numpy(), want)
+        worst = max(worst, err)
+        assert err < FP32_TOL, (n, err)
+    np.testing.assert_array_equal(layer.lens.cpu().numpy(), lens)
+    retired = int((lens == T).sum())
+    print(f"worst rel_err over {steps} steps = {worst:.3e}; sequences retired: {retired}")
+    assert retired == (0 if variant == "bench" else 4)

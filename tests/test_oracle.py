@@ -106,6 +106,55 @@ def test_append_ragged_and_bf16():
     assert not kc[2].any()
 
 
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_append_chunk_offsets_clamp_and_no_wrap(dtype):
+    """append_chunk against two independent statements of the chunk rule:
+    (1) the reference's flat offsets (cache_offset) over a [B*T_cap, E] buffer
+    pre-filled with a sentinel: row i < n_new[b] lands at position lens[b]+i
+    while that is < T_cap, and every other element keeps the sentinel (so no
+    row spills into the next sequence's positions); (2) the same rows fed one
+    token at a time through append() with the sequences that have no row
+    left masked out. Ragged n_new (0, partial, full C, beyond T_cap)."""
+    B, T, H, D, C = 4, 10, 2, 4, 6
+    lens = np.array([0, 7, 3, 10])
+    n_new = np.array([6, 6, 0, 2])  # 7+6 runs past T_cap: rows 7..9 only
+    k = rng.standard_normal((B, C, H, D)).astype(np.float32)
+    v = rng.standard_normal((B, C, H, D)).astype(np.float32)
+    sentinel = np.float32(-777.0)
+    kc = np.full((B, T, H, D), sentinel, np.float32)
+    vc = np.full_like(kc, sentinel)
+    ko.append_chunk(kc, vc, k, v, lens, n_new, dtype=dtype)
+    want_k = np.full(B * T * H * D, sentinel, np.float32)
+    want_v = np.full_like(want_k, sentinel)
+    kr, vr = ko.storage_round(k, dtype), ko.storage_round(v, dtype)
+    for b in range(B):
+        for i in range(n_new[b]):
+            t = lens[b] + i
+            if t >= T:
+                continue
+            for h in range(H):
+                for d in range(D):
+                    off = ko.cache_offset(b, t, h, d, T, H, D)
+                    want_k[off], want_v[off] = kr[b, i, h, d], vr[b, i, h, d]
+    np.testing.assert_array_equal(kc.reshape(-1), want_k)
+    np.testing.assert_array_equal(vc.reshape(-1), want_v)
+    # (2) token by token through append()
+    k1 = np.full((B, T, H, D), sentinel, np.float32)
+    v1 = np.full_like(k1, sentinel)
+    cur = lens.copy()
+    for i in range(C):
+        live = i < n_new
+        step_lens = np.where(live, cur, T)  # a sequence without a row i: "full", skipped
+        out = ko.append(k1, v1, k[:, i], v[:, i], step_lens, dtype=dtype)
+        cur = np.where(live, out, cur)
+    np.testing.assert_array_equal(k1, kc)
+    np.testing.assert_array_equal(v1, vc)
+    # a planted off-by-one (rows written one position late) is caught
+    bad = np.full((B, T, H, D), sentinel, np.float32)
+    ko.append_chunk(bad, bad.copy(), k, v, lens + 1, n_new, dtype=dtype)
+    assert not np.array_equal(bad, kc)
+
+
 def test_paged_gather_matches_direct_scatter():
     B, H, D, bs, max_blocks = 3, 2, 8, 4, 5
     n_blocks = B * max_blocks
