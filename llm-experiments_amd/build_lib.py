@@ -15,7 +15,8 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(HERE, "libskv.so")
 
 SOURCES = ["skv_api.hip", "append.hip", "decode_attn.hip", "decode_attn_generic.hip",
-           "decode_attn_generic_paged.hip", "prefill_attn.hip", "model_ops.hip", "gemm.hip",
+           "decode_attn_generic_paged.hip", "decode_gqa_mfma.hip",
+           "prefill_attn.hip", "model_ops.hip", "gemm.hip",
            "sample.hip", "flash_fp32.hip", "bpe_tokenizer.cpp"]
 
 HIPCC_FLAGS = [

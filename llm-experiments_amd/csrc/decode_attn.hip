@@ -149,10 +149,13 @@ void launch_partial(const DecodeArgs& a, hipStream_t s) {
   launch_partial_t<TC, D, G, TPG, PAGED, PF, 1, false>(a, s);
 }
 
-// Pass 1 of D = 64 or 128 (this file) or of any other D <= 256 (the masked
-// kernels of decode_attn_generic.hip).
+// Pass 1: grouped queries over a bf16 cache on the matrix cores
+// (decode_gqa_mfma.hip), else D = 64 or 128 (this file) or any other D <= 256
+// (the masked kernels of decode_attn_generic.hip).
 template <typename TC, bool PAGED>
 int dispatch_partial(const DecodeArgs& a, int D, int G, hipStream_t s) {
+  if (dec::gqa_mfma_eligible(a, G, sizeof(TC) == 2, PAGED))
+    return dec::launch_partial_gqa(a, G, PAGED, s);
 #define SKV_DEC(DD, GG)                                    \
   if (D == DD && G == GG) {                                \
     launch_partial<TC, DD, GG, PAGED>(a, s);               \

@@ -86,6 +86,12 @@ struct DecodeArgs {
 int launch_partial_generic(const DecodeArgs& a, int G, bool bf16_cache, hipStream_t s);
 int launch_partial_generic_paged(const DecodeArgs& a, int G, bool bf16_cache, hipStream_t s);
 
+// Pass 1 on the matrix cores for grouped queries (decode_gqa_mfma.hip):
+// bf16 caches, head dim 64 or 128, G in {2, 4, 8}, pages of >= 16 tokens or
+// a contiguous capacity that is a multiple of 16.
+bool gqa_mfma_eligible(const DecodeArgs& a, int G, bool bf16_cache, bool paged);
+int launch_partial_gqa(const DecodeArgs& a, int G, bool paged, hipStream_t s);
+
 // Kv heads per workgroup: the largest divisor of H_kv that is <= 16.
 inline int heads_per_group(int Hkv) {
   for (int hw = kMaxRows; hw > 1; --hw)
@@ -206,7 +212,7 @@ struct FragSel<TC, EPL, VG, true> {
 // sums (and the total at [B]) for the merge pass.
 __device__ void locate(const DecodeArgs& a, long long first, bool write_cum, int* b_out,
                        int* off_out) {
-  __shared__ long long s_wave[4];  // wavefront totals of one round (blockDim <= 256)
+  __shared__ long long s_wave[16];  // wavefront totals of one round (blockDim <= 1024)
   __shared__ int s_b, s_off;
   const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wv = tid >> 6;
   const int nwaves = (nt + 63) >> 6;
