@@ -460,7 +460,8 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
     byts = float(np.mean([algorithmic_bytes(f, h_q=Hq, h_kv=Hkv, d=Dh, s_kv=s_kv, s_q=4, s_o=4)
                           for f in fills]))
     mean_s = ev0.elapsed_time(ev1) * 1e-3 / steps
-    chunk, n_chunks = gpu.decode_plan(ctx, B, Hq, Hkv, max_len, int(lens0.sum()))
+    chunk, n_chunks = gpu.decode_plan(ctx, B, Hq, Hkv, max_len, int(lens0.sum()),
+                                      head_dim=cache.head_dim, dtype=cache.dtype)
     roof = {"kernel": "append + decode attention (k_decode_partial + k_decode_merge)", "bound": "hbm",
             "achieved": byts / mean_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": byts / mean_s / 1e9 / HBM_PEAK_GBS, "traffic": None,
@@ -779,7 +780,7 @@ def main():
     achieved = bytes_per_call / mean_s / 1e9
     assert cache.layers[0].lens.cpu().tolist() == [FILL + args.steps] * B
 
-    chunk, n_chunks = gpu.decode_plan(ctx, B, H, H, max_len)
+    chunk, n_chunks = gpu.decode_plan(ctx, B, H, H, max_len, head_dim=D, dtype=cache.dtype)
     # the same K steps again with an event pair per call (outside the timed
     # region above, whose single pair carries no per-call markers): the
     # spread of the call time over the run

@@ -100,16 +100,23 @@ int skv_advance(int32_t* lens, const int32_t* n_new, int n_const, int B, int T_c
  * Given the longest sequence the call may see (max_len) and the filled
  * tokens of the whole batch (total_len; <= 0 means B * max_len), picks
  * chunk_tokens (tokens of the flat token stream -- every sequence's filled
- * tokens end to end -- per workgroup) for about two busy workgroups per CU
- * (512), or one per CU (256) when H_q == H_kv and that still gives chunks
- * of at least 256 tokens; and n_chunks_max = ceil(max_len / chunk_tokens) + 1
- * partial slots per sequence: B * (n_chunks_max - 1) workgroups cover
- * B * max_len tokens, and the spare slot holds the piece of a sequence that
- * starts inside a workgroup's range. H_q must be a multiple of H_kv.
- * chunk_hint > 0 forces that chunk size (rounded up to a multiple of 16).
+ * tokens end to end -- per workgroup) for the pass-1 kernel a call with
+ * this head_dim and cache_dtype runs: grouped queries (H_q / H_kv in
+ * {2, 4, 8}) over a bf16 cache with head_dim 64 or 128 run on the matrix
+ * cores, one busy workgroup per CU for about 90% of the CUs (HBM streams
+ * faster with fewer streams than CUs); the other kernels get about two busy
+ * workgroups per CU (512), or one per CU (256) when H_q == H_kv and that
+ * still gives chunks of at least 256 tokens. n_chunks_max =
+ * ceil(max_len / chunk_tokens) + 1 partial slots per sequence: B *
+ * (n_chunks_max - 1) workgroups cover B * max_len tokens, and the spare slot
+ * holds the piece of a sequence that starts inside a workgroup's range.
+ * H_q must be a multiple of H_kv. chunk_hint > 0 forces that chunk size
+ * (rounded up to a multiple of 16). Any plan is valid for any call with
+ * these B, H_q and max_len; head_dim and cache_dtype only tune it.
  */
-int skv_decode_plan(int B, int H_q, int H_kv, int max_len, long long total_len, int chunk_hint,
-                    int* chunk_tokens /* host */, int* n_chunks_max /* host */);
+int skv_decode_plan(int B, int H_q, int H_kv, int head_dim, int cache_dtype, int max_len,
+                    long long total_len, int chunk_hint, int* chunk_tokens /* host */,
+                    int* n_chunks_max /* host */);
 
 /* Bytes of workspace skv_decode_attn needs for this plan: fp32 partials
  * (o[D], m, l) per (query head, slot), then B + 1 int64 prefix sums. */

@@ -2,6 +2,7 @@
 // (pass-1 kernels tuned per shape), the merge pass for every head dim, and
 // the C entry points. Kernel design: decode_kernels.h; pass 1 for any other
 // head dim: decode_attn_generic.hip.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -323,8 +324,9 @@ int scratch_ptr(void** out, const char* fn) {
 
 using namespace skv;
 
-extern "C" int skv_decode_plan(int B, int H_q, int H_kv, int max_len, long long total_len,
-                               int chunk_hint, int* chunk_tokens, int* n_chunks_max) {
+extern "C" int skv_decode_plan(int B, int H_q, int H_kv, int head_dim, int cache_dtype,
+                               int max_len, long long total_len, int chunk_hint, int* chunk_tokens,
+                               int* n_chunks_max) {
   SKV_REQUIRE(chunk_tokens && n_chunks_max, SKV_E_INVALID, "skv_decode_plan: null output");
   SKV_REQUIRE(B > 0 && H_q > 0 && H_kv > 0 && max_len > 0, SKV_E_INVALID,
               "skv_decode_plan: dims must be > 0 (B=%d H_q=%d H_kv=%d max_len=%d)", B, H_q, H_kv,
@@ -332,8 +334,25 @@ extern "C" int skv_decode_plan(int B, int H_q, int H_kv, int max_len, long long 
   SKV_REQUIRE(H_q % H_kv == 0, SKV_E_INVALID,
               "skv_decode_plan: H_q=%d is not a multiple of H_kv=%d", H_q, H_kv);
   int chunk;
+  const long long tot = total_len > 0 ? total_len : (long long)B * max_len;
+  const int G = H_q / H_kv;
   if (chunk_hint > 0) {
     chunk = (int)(((long)chunk_hint + 15) / 16 * 16);
+  } else if (cache_dtype == SKV_BF16 && (head_dim == 64 || head_dim == 128) &&
+             (G == 2 || G == 4 || G == 8)) {
+    // The matrix-core GQA kernel (decode_gqa_mfma.hip): one workgroup of 8
+    // wavefronts per CU, kv heads in groups of up to 8. It is bound by HBM,
+    // which served fewer concurrent streams than CUs faster: C5 (132K
+    // tokens, 8 kv heads) 101.7 us per call at 230 workgroups of 576 tokens,
+    // 104.0 us at 243 of 544; past 256 (512 tokens: 258) a second round of
+    // workgroups costs 45%.
+    int hw = 1;
+    while (hw < 8 && H_kv % (hw * 2) == 0) hw *= 2;
+    const long long groups = H_kv / hw;
+    const long long target = kNumCUs * 9 / 10;
+    long long per = (tot * groups + target - 1) / target;
+    per = (per + 15) / 16 * 16;
+    chunk = (int)std::min<long long>(std::max<long long>(per, 32), 8192);
   } else {
     // About 512 busy workgroups per call: two per CU on MI355X's 256 CUs.
     // Grids that leave some CUs one workgroup more than others (e.g. 336
@@ -346,9 +365,9 @@ extern "C" int skv_decode_plan(int B, int H_q, int H_kv, int max_len, long long 
     // work per byte, and one workgroup per CU with twice the chunk streams
     // faster once chunks are long: C4 161.6 -> 159.5 us per call (256 ->
     // 512 tokens), as a plain non-temporal read of K and V does (87.3% ->
-    // 89.5% of 8 TB/s). With G = 4 (C5) the per-wavefront exp and dot work
-    // needs the second workgroup: 119 -> 159 us per call at one per CU.
-    const long long tot = total_len > 0 ? total_len : (long long)B * max_len;
+    // 89.5% of 8 TB/s). With grouped queries the VALU kernels' per-wavefront
+    // exp and dot work needs the second workgroup (C5: 119 -> 159 us per
+    // call at one per CU).
     const long long groups = H_kv / heads_per_group(H_kv);
     long long target = 2 * kNumCUs;
     if (H_q == H_kv && (tot * groups + kNumCUs - 1) / kNumCUs >= 256) target = kNumCUs;

@@ -5,44 +5,48 @@
 // (decode_kernels.h): workgroup w owns tokens [w*chunk, (w+1)*chunk) of the
 // flat token stream, cut into pieces at sequence boundaries, and writes one
 // partial (m, l, o[D]) per (piece, query head) at slot w + b. What differs is
-// how a wavefront consumes a piece. With G query heads per kv head the VALU
-// kernels spend ~36 wavefront instructions per (token, kv head) on the q.k
-// dots, the p.V updates and their cross-lane sums; here both products run
-// on v_mfma_f32_16x16x32_bf16 and the VALU is left with the softmax itself
-// (~3 instructions per token and kv head), so the pass is bound by HBM.
+// how a piece is consumed. With G query heads per kv head the VALU kernels
+// spend ~36 wavefront instructions per (token, kv head) on the q.k dots, the
+// p.V updates and their cross-lane sums; here both products run on MFMA and
+// the VALU is left with the softmax itself (~4 instructions per token and
+// kv head), so the pass is bound by HBM.
 //
-// One wavefront serves one kv head and G query heads, in steps of 32 tokens
-// (two 16-token tiles):
-//  * S = K q^T: operand A is the K tile straight from HBM (lane l holds row
-//    l%16, 8 consecutive elements per k-block), operand B is the query:
-//    column c < G holds head c, column G + c holds head c again, and the k
-//    dimension is [D elements of q_hi ; D elements of q_lo], q_hi =
-//    bf16(q * scale * log2 e), q_lo = bf16(that - q_hi), against [K | K].
-//    The split makes q.k exact to ~2^-17 relative (K is bf16 already), and
-//    the duplicated columns give both column c and G + c the full score of
-//    head c, bit for bit.
-//  * Online softmax per column, lanes of column c holding 8 of the step's
-//    32 scores. The running max is kept lazily: the accumulator is rescaled
-//    only when a step's max exceeds it by more than 8 (log2 units), so p =
-//    exp2(s - m) <= 256; (m, l, o) stay consistent, the merge is exact.
-//  * O^T += V^T P: operand B is P, column c < G holding bf16(p) and column
-//    G + c holding bf16(p - bf16(p)) of head c (so p too is split to ~2^-17);
-//    the token order of its k slots is the order in which the S lanes hold
-//    the scores, so P needs no shuffle. Operand A is V^T, which needs 8
-//    tokens of one element per lane: the V tile is staged in LDS and read
-//    with ds_read_b64_tr_b16. At the end column c + G is added to column c.
-//  * Memory: each step's K and V loads are issued (16-byte non-temporal
-//    loads, 16 KB per wavefront for D = 128) before the previous step is
-//    consumed, into a second register set, so every wavefront keeps a step
-//    in flight. V rows go to LDS after the products of the previous step
-//    (a wavefront's LDS operations execute in order, so no barrier).
-//  * Tiles are aligned to 16 tokens of the sequence, so a tile lies inside
-//    one page (block_size >= 16) and its rows are one base plus a lane
-//    offset. Tokens outside the piece are masked (score -inf); V rows past
-//    the sequence's fill are zeroed, so uninitialised pool memory cannot
-//    turn 0 * garbage into NaN. A fused append's token is taken from the
-//    input in the step that holds it, rounded to bf16 and written to the
-//    cache by the lanes that hold it.
+// Memory: a workgroup of 8 wavefronts serves hw kv heads (hw = 8 for C5's
+// 8 kv heads) and moves its tokens through LDS in stages of 16*S tokens x hw
+// heads, K then V (S = 8 / hw token substreams; 32 KB per tensor at D =
+// 128). The cache rows of consecutive heads of a token are adjacent, so a
+// stage is read as contiguous 1 KB pieces (16-byte non-temporal loads),
+// two stages in flight in registers while the previous one is consumed
+// from LDS. (A first form
+// in which each wavefront read only its own head's 256-byte rows, 2 KB
+// apart, streamed at 65% of 8 TB/s on C5; the VALU kernels, which read 1 KB
+// contiguous per instruction, reach 85% on C4.) Each 16-byte chunk of a row
+// is stored at position chunk ^ swz(token), which puts both read patterns
+// below on distinct LDS banks.
+//
+// Compute: wavefront (hl, sub) takes kv head hl and tokens [16 sub, 16 sub
+// + 16) of each stage, for its G query heads:
+//  * S = K q^T (v_mfma_f32_16x16x32_bf16): operand A is the K tile (lane l
+//    holds row l%16, 8 elements per k-block), operand B the query: column
+//    c < G holds head c, column G + c head c again, and the k dimension is
+//    [D elements of q_hi ; D elements of q_lo], q_hi = bf16(q * scale *
+//    log2 e), q_lo = bf16(that - q_hi), against [K | K]. The split makes q.k
+//    exact to ~2^-17 relative (K is bf16 already); the duplicated columns
+//    give columns c and G + c the same score, bit for bit.
+//  * Online softmax per column, each lane holding 4 of the 16 scores. The
+//    running max moves lazily: only when a stage's max passes it by more
+//    than 8 (log2 units), so p = exp2(s - m) <= 256; (m, l, o) stay
+//    consistent and the merge is exact.
+//  * O^T += V^T P (v_mfma_f32_16x16x16_bf16): operand B is P, column c < G
+//    holding bf16(p) and column G + c bf16(p - bf16(p)) of head c, in the
+//    token order in which the score lanes hold them (no shuffle); operand A
+//    is V^T, 4 tokens of one element per lane, read with ds_read_b64_tr_b16.
+//    At the end column G + c is added to column c.
+// Tokens outside the piece are masked (score -inf); rows past its end are
+// loaded from its last row, so no page past the fill is touched and no
+// uninitialised memory meets a zero weight (0 * NaN). A fused append's rows
+// are stored to the cache (rounded to bf16) at the start of the piece, and
+// the stores complete before any wavefront loads the stage holding them.
 // No atomics: results are bitwise reproducible, and a paged cache gives the
 // bits of the same rows in a contiguous one.
 #include "decode_kernels.h"
@@ -52,28 +56,34 @@ namespace dec {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kStep = 32;      // tokens per wavefront step (two 16-token tiles)
-constexpr float kLazy = 8.f;   // rescale when the max grows by more than this (log2 units)
-constexpr int kWaves = 8;      // wavefronts per workgroup
+constexpr int kWaves = 8;     // wavefronts per workgroup
+constexpr int kSub = 16;      // tokens per wavefront and stage (one MFMA tile)
+constexpr float kLazy = 8.f;  // rescale when the max grows by more than this (log2 units)
 
 template <int D>
 struct Gq {
-  static constexpr int KB = D / 32;       // 32-element k-blocks of a K row
-  static constexpr int CPR = D / 8;       // 16-byte chunks per row
-  static constexpr int RPI = 64 / CPR;    // V rows per wavefront load
-  static constexpr int VL = kStep / RPI;  // V loads per lane and step
-  static constexpr int DB = D / 16;       // 16-row blocks of O^T
-  // LDS bytes per V row: 32 bytes of padding put the rows of a transposed
-  // read (8 rows x 2 chunks per half-wavefront) and of a row store (16 or
-  // 8 chunks) on distinct banks.
-  static constexpr int LROW = 2 * D + 32;
-  static constexpr int TILE = kStep * LROW;  // a wavefront's V tile
+  static constexpr int KB = D / 32;   // 32-element k-blocks of a K row
+  static constexpr int CPR = D / 8;   // 16-byte chunks per row
+  static constexpr int DB = D / 16;   // 16-row blocks of O^T
+  static constexpr int TBYTES = kWaves * kSub * D * 2;  // one tensor's rows of a stage
+  static constexpr int SBYTES = 2 * TBYTES;             // a stage: K, then V
+  static constexpr int NI = TBYTES / (kWaves * 1024);   // 1 KB pieces per wavefront and tensor
 };
+
+// Physical 16-byte chunk position of logical chunk lc in the row of stage
+// token t is lc ^ swz(t). At D = 128 (a row is the 256 bytes of one bank
+// sweep): the K operand reads take one chunk of 16 consecutive tokens'
+// rows (swz injective on t % 16), the transposed V reads two adjacent
+// chunks of 8 consecutive tokens' rows (swz / 2 injective on t % 8).
+template <int D>
+__device__ __forceinline__ int swz(int t) {
+  return (2 * (t & 7) + ((t >> 3) & 1)) & (D / 8 - 1);
+}
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives as its slot
 // j the element i%4 of the four 16-bit values addressed by lane 4j + i/4.
@@ -97,7 +107,7 @@ __device__ __forceinline__ u32x4_t load8_bf16(const void* p, size_t i, int dt) {
 // page table), read through the constant address space: a scalar load,
 // waited for on its own counter. A plain load of it compiles to a vector
 // load (the kernel's stores could alias it), and waiting for that vector
-// load waited for every K/V load in flight as well.
+// load waits for every load in flight as well.
 __device__ __forceinline__ int load_uniform(const int32_t* p) {
   return *(const __attribute__((address_space(4))) int32_t*)(p);
 }
@@ -109,21 +119,21 @@ __device__ __forceinline__ float shl_cols(float x) {  // lane i <- lane i + G of
 }
 
 // One piece [start, end) of sequence b for kv head group hg; the partials go
-// to `slot`. smem: the workgroup's V tiles (kWaves * TILE bytes).
+// to `slot`. smem: one stage (SBYTES bytes).
 template <int D, int G, bool PAGED>
 __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, int start, int end,
                                           int slot, char* smem) {
   using Sh = Gq<D>;
-  constexpr int KB = Sh::KB, CPR = Sh::CPR, RPI = Sh::RPI, VL = Sh::VL, DB = Sh::DB;
-  constexpr int LROW = Sh::LROW;
+  constexpr int KB = Sh::KB, CPR = Sh::CPR, DB = Sh::DB, NI = Sh::NI;
+  constexpr int TBYTES = Sh::TBYTES;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hw = a.hw, S = a.S;
-  const int hl = wave % hw, sub = wave / hw;
+  const int hw = a.hw, S = a.S;  // hw * S == kWaves, both powers of two
+  const int lhw = __builtin_ctz(hw);
+  const int hl = wave & (hw - 1), sub = wave >> lhw;
   const int hk = hg * hw + hl;
   const int h = lane >> 4, c = lane & 15;
-  const size_t RS = (size_t)a.Hkv * D;  // elements between consecutive tokens of a kv head
-  char* vt = smem + wave * Sh::TILE;
+  const int TS = kSub * S;  // tokens per stage
 
   // ---- query operand: columns c and G + c hold head c % G; k-block kb < KB
   // takes q_hi, KB + kb takes q_lo, elements 32 kb + 8 h + j ----
@@ -148,130 +158,117 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
   const bool has_new = appends(a, b) && end == clamped_len(a, b);
   const int mend = has_new ? end - 1 : end;  // the appended token's position, if any
   const int T0 = start & ~15;
-  const int nsteps = (end - T0 + kStep - 1) / kStep;
-  const int tlast = (end - 1) & ~15;  // the last tile holding a token of the piece
+  const int nst = (end - T0 + TS - 1) / TS;
+  const int tlast = (end - 1) & ~15;  // the last 16-token tile holding a token of the piece
   const uint16_t* kc = static_cast<const uint16_t*>(a.k);
   const uint16_t* vc = static_cast<const uint16_t*>(a.v);
 
-  // First element of the tile at token T (a multiple of 16, clamped to the
-  // last tile of the piece so no page past the fill is looked up) for this
-  // kv head. All 16 rows of a tile may be read: a page holds whole tiles
-  // (block_size >= 16), and a contiguous cache whole ones too (T_cap % 16 ==
-  // 0, checked by the dispatch). Uniform over the wavefront.
-  auto tile_base = [&](int T) -> const uint16_t* {
-    const int Tt = min(T, tlast);
-    size_t row;
+  // Cache row of token Tt (a multiple of 16, <= tlast); uniform.
+  auto tile_row = [&](int Tt) -> size_t {
     if constexpr (PAGED) {
       const int blk = load_uniform(a.block_table + (size_t)b * a.max_blocks + (Tt >> a.bs_shift));
-      row = ((size_t)blk << a.bs_shift) + (Tt & ((1 << a.bs_shift) - 1));
+      return ((size_t)blk << a.bs_shift) + (Tt & ((1 << a.bs_shift) - 1));
     } else {
-      row = (size_t)b * a.T_cap + Tt;
-    }
-    return reinterpret_cast<const uint16_t*>(0) + (row * a.Hkv + hk) * D;
-  };
-  // lane offsets (elements) from a tile's first element: K operand rows and
-  // V staging rows
-  const uint32_t koff = (uint32_t)(c * RS + 8 * h);
-  const uint32_t voff = (uint32_t)((lane / CPR) * RS + 8 * (lane % CPR));
-  const size_t vstep = (size_t)RPI * RS;  // between the V loads of one lane
-  auto at = [](const uint16_t* cache, const uint16_t* rel, size_t e) {
-    return cache + (rel - reinterpret_cast<const uint16_t*>(0)) + e;
-  };
-
-  // Loads of step k: K rows into kr (MFMA operand layout), V rows into vr
-  // (row u*RPI + lane/CPR of the step, chunk lane%CPR).
-  auto issue_v = [&](int k, u32x4_t (&vr)[VL]) {
-    const int T = T0 + k * kStep;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint16_t* base = tile_base(T + 16 * t);
-#pragma unroll
-      for (int u = 0; u < VL / 2; ++u)
-        vr[t * VL / 2 + u] = stream_load16(at(vc, base, u * vstep) + voff);
-    }
-  };
-  auto issue_k = [&](int k, u32x4_t (&kr)[2][KB]) {
-    const int T = T0 + k * kStep;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint16_t* kp = at(kc, tile_base(T + 16 * t), koff);
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) kr[t][kb] = stream_load16(kp + 32 * kb);
+      return (size_t)b * a.T_cap + Tt;
     }
   };
 
-  // Step k's data has arrived: V rows past the sequence's fill are zeroed
-  // (they may be uninitialised memory), then the rows go to LDS.
-  auto finish = [&](int k, u32x4_t (&vr)[VL]) {
-    const int T = T0 + k * kStep;
-    if (T + kStep > end) {  // uniform: the step reaches past the piece
-#pragma unroll
-      for (int u = 0; u < VL; ++u)
-        if (T + u * RPI + lane / CPR >= end) vr[u] = u32x4_t{0u, 0u, 0u, 0u};
+  // A fused append: the rows of the group's hw heads go to position mend,
+  // stored by threads [0, 2 hw CPR) (K, then V), before any load.
+  if (has_new) {
+    const int nrow = hw * CPR;
+    if (tid < 2 * nrow) {
+      const bool isv = tid >= nrow;
+      const int u = isv ? tid - nrow : tid, hd = u / CPR, ln = u % CPR;
+      const size_t src = ((size_t)b * a.Hkv + hg * hw + hd) * D + 8 * ln;
+      const u32x4_t x = load8_bf16(isv ? a.new_v : a.new_k, src, a.in_dt);
+      const size_t row = tile_row(mend & ~15) + (mend & 15);
+      uint16_t* dst = const_cast<uint16_t*>(isv ? vc : kc) + (row * a.Hkv + hg * hw + hd) * D;
+      *reinterpret_cast<u32x4_t*>(dst + 8 * ln) = x;
     }
+    __builtin_amdgcn_s_waitcnt(0);  // the stores have completed
+    __syncthreads();
+  }
+
+  // Loads of stage k (tokens [T0 + k TS, + TS)) into r: the 16-byte unit
+  // pos of a tensor's stage rows is row pos / CPR = t * hw + hd (stage
+  // token t, head hd of the group), physical chunk pos % CPR; wavefront w
+  // moves the 1 KB pieces [w NI, (w + 1) NI) of K (r[i]) and of V
+  // (r[NI + i]). A piece's rows lie in one 16-token tile (a piece holds 1
+  // to 8 whole tokens), so its page is uniform. Rows at or past the
+  // piece's end are read from its last row.
+  auto load_stage = [&](int k, u32x4_t (&r)[2 * NI]) {
+    const int T = T0 + k * TS;
 #pragma unroll
-    for (int u = 0; u < VL; ++u)
-      *reinterpret_cast<u32x4_t*>(vt + (u * RPI + lane / CPR) * LROW + 16 * (lane % CPR)) = vr[u];
+    for (int i = 0; i < NI; ++i) {
+      const int piece = wave * NI + i;
+      const int pos = piece * 64 + lane;
+      const int ri = pos / CPR;
+      const int t = ri >> lhw, hd = ri & (hw - 1);
+      const int lc = (pos % CPR) ^ swz<D>(t);
+      const int tfirst = __builtin_amdgcn_readfirstlane((piece * 64 / CPR) >> lhw);
+      const int Tt = min(T + (tfirst & ~15), tlast);
+      const size_t trow = tile_row(Tt);
+      const int tok = min(T + t, end - 1);
+      const size_t e = ((trow + (tok - Tt)) * a.Hkv + hg * hw + hd) * D + 8 * lc;
+      r[i] = stream_load16(kc + e);
+      r[NI + i] = stream_load16(vc + e);
+    }
+  };
+  // ... and into the LDS stage, at unit pos
+  auto store_stage = [&](const u32x4_t (&r)[2 * NI]) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      char* p = smem + (wave * NI + i) * 1024 + 16 * lane;
+      *reinterpret_cast<u32x4_t*>(p) = r[i];
+      *reinterpret_cast<u32x4_t*>(p + TBYTES) = r[NI + i];
+    }
   };
 
-  // A fused append's token: the wavefront that reads the piece's last step
-  // stores the input rows (rounded to bf16) at position mend first; before
-  // it issues the loads of that step it waits for its stores to complete,
-  // and then reads the row like any other.
-  const bool writes_new = has_new && (nsteps - 1) % S == sub;
-  if (writes_new) {
-    const size_t nsrc = ((size_t)b * a.Hkv + hk) * D;
-    const int tt = mend & ~15, ln = lane & (CPR - 1);
-    const uint16_t* base = tile_base(tt);
-    if (lane < 2 * CPR) {  // lanes [0, CPR): the K row, [CPR, 2 CPR): the V row
-      const bool isv = lane >= CPR;
-      const u32x4_t x = load8_bf16(isv ? a.new_v : a.new_k, nsrc + 8 * ln, a.in_dt);
-      *reinterpret_cast<u32x4_t*>(const_cast<uint16_t*>(
-          at(isv ? vc : kc, base, (size_t)(mend - tt) * RS + 8 * ln))) = x;
-    }
+  // LDS offsets (within a stage) of this lane's operand reads: the K rows
+  // of stage token 16 sub + c, chunk 4 kb + h; the V rows of stage token
+  // 16 sub + 4h + c/4, elements 16 db + 4 (c%4) .. + 3.
+  int kaddr[KB], vaddr[DB];
+  {
+    const int tk = kSub * sub + c;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+      kaddr[kb] = ((tk * hw + hl) * CPR + ((4 * kb + h) ^ swz<D>(tk))) * 16;
+    const int tv = kSub * sub + 4 * h + (c >> 2);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      vaddr[db] = TBYTES + ((tv * hw + hl) * CPR + ((2 * db + ((c & 3) >> 1)) ^ swz<D>(tv))) * 16 +
+                  8 * (c & 1);
   }
 
   f32x4 o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
-  // transposed-read offset: lane c of group h addresses row 4h + c/4,
-  // elements 4 (c%4) .. +3 of each 16-element block
-  const int rd = (4 * h + (c >> 2)) * LROW + 8 * (c & 3);
   const float lo_f = c >= G ? 1.f : 0.f;
 
-  // Scores of step k (K in kr): lane (h, c) gets column c at tokens
-  // T + 4h + j (s[j]) and T + 16 + 4h + j (s[4 + j]), tokens outside the
-  // piece masked.
-  auto scores = [&](int k, const u32x4_t (&kr)[2][KB], float (&s)[8]) {
-    const int T = T0 + k * kStep;
-    f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+  // This wavefront's 16 tokens of stage k, from the LDS stage.
+  auto compute = [&](int k) {
+    const int T = T0 + k * TS + kSub * sub;  // first token of this wavefront's tile
+    if (T >= end) return;                    // uniform: a tile past the piece is idle
+    const char* st = smem;
+    bf16x8 kf[KB];
 #pragma unroll
-    for (int kb = 0; kb < 2 * KB; ++kb) {
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[0][kb % KB]),
-                                                    qf[kb], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[1][kb % KB]),
-                                                    qf[kb], s1, 0, 0, 0);
-    }
+    for (int kb = 0; kb < KB; ++kb) kf[kb] = *reinterpret_cast<const bf16x8*>(st + kaddr[kb]);
+    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      s[j] = s0[j];
-      s[4 + j] = s1[j];
-    }
-    if (T < start || T + kStep > end) {  // uniform
+    for (int kb = 0; kb < 2 * KB; ++kb)
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb % KB], qf[kb], sc, 0, 0, 0);
+    // lane (h, c) holds column c at tokens T + 4h + j
+    float s[4] = {sc[0], sc[1], sc[2], sc[3]};
+    if (T < start || T + kSub > end) {  // uniform
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int tok = T + (j >> 2) * 16 + 4 * h + (j & 3);
+      for (int j = 0; j < 4; ++j) {
+        const int tok = T + 4 * h + j;
         if (tok < start || tok >= end) s[j] = -INFINITY;
       }
     }
-  };
-
-  // Online softmax and O^T update of step k (V in this wave's tile).
-  auto consume = [&](float (&s)[8]) {
-    float mt = s[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) mt = fmaxf(mt, s[j]);
+    float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     mt = fmaxf(mt, __shfl_xor(mt, 16));
     mt = fmaxf(mt, __shfl_xor(mt, 32));
     // Lazy max: m moves only when some column's max passed it by more than
@@ -279,7 +276,7 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
     // else by 1 (a multiply in place: a branch around it made the compiler
     // copy every accumulator register).
     const float mn = __any(mt > m_run + kLazy) ? fmaxf(m_run, mt) : m_run;
-    const float al = fast_exp2(m_run - mn);  // 0 on the first step, 1 if m stays
+    const float al = fast_exp2(m_run - mn);  // 0 on the first tile, 1 if m stays
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[db] *= al;
     l_run *= al;
@@ -287,58 +284,103 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
     // P operand: bf16(p) in columns c < G, bf16(p - bf16(p)) in columns
     // G + c (y = p - lo_f * bf16(p), lo_f = 1 there, else 0); the columns
     // past 2G see q = 0, p = 1 and are never read.
-    bf16x8 pf;
+    i16x4 pf;
     float ls = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
+    for (int j = 0; j < 4; j += 2) {
       const float p0 = fast_exp2(s[j] - m_run), p1 = fast_exp2(s[j + 1] - m_run);
       ls += p0 + p1;
-      const bf16x2 hb = __builtin_convertvector(float2_t{p0, p1}, bf16x2);
-      const uint32_t hw2 = __builtin_bit_cast(uint32_t, hb);
-      const float y0 = fmaf(-lo_f, __uint_as_float(hw2 << 16), p0);
-      const float y1 = fmaf(-lo_f, __uint_as_float(hw2 & 0xffff0000u), p1);
-      const bf16x2 yb = __builtin_convertvector(float2_t{y0, y1}, bf16x2);
-      pf[j] = yb[0];
-      pf[j + 1] = yb[1];
+      const uint32_t hb =
+          __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{p0, p1}, bf16x2));
+      const float y0 = fmaf(-lo_f, __uint_as_float(hb << 16), p0);
+      const float y1 = fmaf(-lo_f, __uint_as_float(hb & 0xffff0000u), p1);
+      const uint32_t yb =
+          __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{y0, y1}, bf16x2));
+      pf[j] = (short)(yb & 0xffffu);
+      pf[j + 1] = (short)(yb >> 16);
     }
     l_run += ls;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const i16x4 v0 = lds_read_tr16(vt + rd + 32 * db);
-      const i16x4 v1 = lds_read_tr16(vt + rd + 16 * LROW + 32 * db);
-      const bf16x8 va =
-          __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
-      o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf, o[db], 0, 0, 0);
-    }
+    for (int db = 0; db < DB; ++db)
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(lds_read_tr16(st + vaddr[db]), pf, o[db],
+                                                         0, 0, 0);
   };
 
-  // Pipeline over this wavefront's steps sub, sub + S, ...: step k + S is
-  // loaded (K, then V) once step k's scores are formed, so its 16 KB (D =
-  // 128) are in flight while step k is consumed; the only wait of a step is
-  // for those loads, before its V rows go to LDS. (Issuing V of step k + S
-  // before step k's scores left the compiler's wait counting unable to tell
-  // the loop's registers from the prologue's: it waited on step k's K loads
-  // before every V load.)
+  // Two stages in flight, in two register sets: stages k + 1 and k + 2 are
+  // loading while stage k is consumed from LDS; then stage k + 1 goes to
+  // LDS and stage k + 3 is issued into the set it leaves. (Loads straight
+  // into LDS need no registers, but the compiler cannot tell which LDS a
+  // pending one writes and waited for all of them before the first LDS
+  // read of every stage.) The steady-state loop issues its loads without
+  // conditions: the compiler counts outstanding loads per path, and a load
+  // behind a branch made it wait for both sets before every LDS store.
   {
-    u32x4_t kr[2][KB], vr[VL];
-    auto load_step = [&](int k) {
-      if (writes_new && k == nsteps - 1) __builtin_amdgcn_s_waitcnt(0);  // appended rows stored
-      issue_k(k, kr);
-      issue_v(k, vr);
-    };
-    int k = sub;
-    if (k < nsteps) {
-      load_step(k);
-      finish(k, vr);
+    u32x4_t ra[2 * NI], rb[2 * NI];
+    if (nst > 4) {
+      load_stage(0, ra);
+      load_stage(1, rb);
+      store_stage(ra);
+      __syncthreads();
+      load_stage(2, ra);
+      int k = 0;
+      for (; k + 4 < nst; k += 2) {  // stages k + 1 (rb), k + 2 (ra) in flight
+        compute(k);
+        __syncthreads();  // every wavefront is done with stage k
+        store_stage(rb);
+        __syncthreads();
+        load_stage(k + 3, rb);
+        compute(k + 1);
+        __syncthreads();
+        store_stage(ra);
+        __syncthreads();
+        load_stage(k + 4, ra);
+      }
+      // stages k (LDS), k + 1 (rb), k + 2 (ra) and perhaps k + 3 are left
+      const bool four = k + 3 < nst;
+      compute(k);
+      __syncthreads();
+      store_stage(rb);
+      __syncthreads();
+      if (four) load_stage(k + 3, rb);
+      compute(k + 1);
+      __syncthreads();
+      store_stage(ra);
+      __syncthreads();
+      compute(k + 2);
+      if (four) {
+        __syncthreads();
+        store_stage(rb);
+        __syncthreads();
+        compute(k + 3);
+      }
+    } else {  // a short piece: up to 4 stages
+      load_stage(0, ra);
+      if (nst > 1) load_stage(1, rb);
+      store_stage(ra);
+      __syncthreads();
+      compute(0);
+      if (nst > 1) {
+        if (nst > 2) load_stage(2, ra);
+        __syncthreads();
+        store_stage(rb);
+        __syncthreads();
+        compute(1);
+        if (nst > 2) {
+          if (nst > 3) load_stage(3, rb);
+          __syncthreads();
+          store_stage(ra);
+          __syncthreads();
+          compute(2);
+          if (nst > 3) {
+            __syncthreads();
+            store_stage(rb);
+            __syncthreads();
+            compute(3);
+          }
+        }
+      }
     }
-    for (; k < nsteps; k += S) {
-      const int k2 = k + S;
-      float s[8];
-      scores(k, kr, s);
-      if (k2 < nsteps) load_step(k2);
-      consume(s);
-      if (k2 < nsteps) finish(k2, vr);
-    }
+    __syncthreads();  // the stage's space is free for the merge or the next piece
   }
 
   // ---- epilogue: l over the four lane groups; column G + c into column c ----
@@ -361,11 +403,11 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
     return;
   }
 
-  // S > 1: the S substreams of each kv head merge through LDS (the V tiles'
-  // space). Substreams that saw no step drop out through exp2(-inf) = 0.
-  float* mo = reinterpret_cast<float*>(smem);         // [kWaves][G][D]
-  float* mml = mo + kWaves * G * D;                   // [kWaves][G][2]
-  __syncthreads();  // every wavefront is done with its tile
+  // S > 1: the S substreams of each kv head merge through LDS (the stage's
+  // space: every wavefront is past the loop's last barrier). Substreams
+  // that saw no token drop out through exp2(-inf) = 0.
+  float* mo = reinterpret_cast<float*>(smem);  // [kWaves][G][D]
+  float* mml = mo + kWaves * G * D;            // [kWaves][G][2]
   if (c < G) {
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -391,16 +433,16 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
     a.ws_o[pidx * D + d] = O;
     if (d == 0) *reinterpret_cast<float2*>(a.ws_ml + pidx * 2) = make_float2(M, L);
   }
-  __syncthreads();  // the next piece's V tiles overwrite this space
+  __syncthreads();  // the next piece's stages overwrite this space
 }
 
 // Grid (n_wg, H_kv / hw), kWaves wavefronts: wavefront w serves kv head
 // w % hw of the group and token substream w / hw.
 template <int D, int G, bool PAGED>
 __global__ __launch_bounds__(kWaves * 64) void k_decode_gqa(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kWaves * Gq<D>::TILE];
-  static_assert(kWaves * Gq<D>::TILE >= kWaves * 8 * D * 4 + kWaves * 8 * 2 * 4,
-                "the substream merge reuses the V tiles' space");
+  __shared__ __attribute__((aligned(16))) char smem[Gq<D>::SBYTES];
+  static_assert(Gq<D>::SBYTES >= kWaves * 8 * D * 4 + kWaves * 8 * 2 * 4,
+                "the substream merge reuses the stage's space");
   const int w = blockIdx.x, hg = blockIdx.y;
   int b, off;
   locate(a, (long long)w * a.chunk, w == 0 && hg == 0, &b, &off);
@@ -430,7 +472,7 @@ void launch_dg(const DecodeArgs& a, bool paged, hipStream_t s) {
 
 bool gqa_mfma_eligible(const DecodeArgs& a, int G, bool bf16_cache, bool paged) {
   return bf16_cache && (a.D == 64 || a.D == 128) && (G == 2 || G == 4 || G == 8) &&
-         (paged ? a.bs_shift >= 4 : a.T_cap % 16 == 0);
+         (!paged || a.bs_shift >= 4);
 }
 
 int launch_partial_gqa(const DecodeArgs& a0, int G, bool paged, hipStream_t s) {

@@ -35,7 +35,7 @@ _SIGNATURES = {
     "skv_append_paged": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "skv_append_chunk": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "skv_advance": (_I, [_P, _P, _I, _I, _I, _P]),
-    "skv_decode_plan": (_I, [_I, _I, _I, _I, ctypes.c_longlong, _I, ctypes.POINTER(_I),
+    "skv_decode_plan": (_I, [_I, _I, _I, _I, _I, _I, ctypes.c_longlong, _I, ctypes.POINTER(_I),
                                  ctypes.POINTER(_I)]),
     "skv_decode_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "skv_prefill_plan": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(_I)]),

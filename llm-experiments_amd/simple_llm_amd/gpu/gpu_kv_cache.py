@@ -251,13 +251,15 @@ def _workspace(ctx: GPUContext, nbytes: int) -> torch.Tensor:
 
 
 def decode_plan(ctx: GPUContext, batch_size: int, n_heads: int, n_kv_heads: int, max_len: int,
-                total_len: int = 0) -> tuple[int, int]:
+                total_len: int = 0, *, head_dim: int, dtype: torch.dtype) -> tuple[int, int]:
     """(chunk_tokens, n_chunks_max) of the split-K decode for these sizes.
 
-    total_len: filled tokens over the batch (0: batch_size * max_len)."""
+    total_len: filled tokens over the batch (0: batch_size * max_len);
+    head_dim and the cache dtype select the kernel the plan is tuned for."""
     L = _lib.lib()
     c, n = ctypes.c_int(), ctypes.c_int()
-    rc = L.skv_decode_plan(batch_size, n_heads, n_kv_heads, max(int(max_len), 1), int(total_len),
+    rc = L.skv_decode_plan(batch_size, n_heads, n_kv_heads, int(head_dim), _lib.dtype_code(dtype),
+                           max(int(max_len), 1), int(total_len),
                            int(ctx.config.decode_chunk_tokens), ctypes.byref(c), ctypes.byref(n))
     _lib.check(rc, "skv_decode_plan")
     return c.value, n.value
@@ -287,7 +289,7 @@ def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.T
     _check_max_len(max_len, layer.host_lens)
     total = int(np.minimum(layer.host_lens, max_len).sum())
     chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
-                                  total)
+                                  total, head_dim=cache.head_dim, dtype=cache.dtype)
     L = _lib.lib()
     need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
     ws = _workspace(ctx, need)
@@ -351,7 +353,7 @@ def kv_cache_append_attend(ctx: GPUContext, cache: KVCache, layer_idx: int, new_
         _check_max_len(max_len, after)
         total = int(np.minimum(after, max_len).sum())
     chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
-                                  total)
+                                  total, head_dim=cache.head_dim, dtype=cache.dtype)
     L = _lib.lib()
     need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
     ws = _workspace(ctx, need)

@@ -245,8 +245,8 @@ class TransformerModel:
         if key not in self._bufs:
             T = cache.max_seq_len
             chunk, n = gpu.decode_plan(self.ctx, cache.batch_size, cache.n_heads,
-                                       cache.n_kv_heads, T,
-                                       cache.batch_size * T)
+                                       cache.n_kv_heads, T, cache.batch_size * T,
+                                       head_dim=cache.head_dim, dtype=cache.dtype)
             L = _lib.lib()
             need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, n)
             ws = torch.empty(max(need, 1), dtype=torch.uint8, device=self.ctx.device)

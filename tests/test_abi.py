@@ -24,9 +24,9 @@ def test_version():
     assert _lib.lib().skv_version() == 100
 
 
-def _plan(B, Hkv, max_len, hint=0, total=0, Hq=None):
+def _plan(B, Hkv, max_len, hint=0, total=0, Hq=None, D=64, dt=_lib.F32):
     c, n = ctypes.c_int(), ctypes.c_int()
-    rc = _lib.lib().skv_decode_plan(B, Hkv if Hq is None else Hq, Hkv, max_len, total, hint,
+    rc = _lib.lib().skv_decode_plan(B, Hkv if Hq is None else Hq, Hkv, D, dt, max_len, total, hint,
                                     ctypes.byref(c), ctypes.byref(n))
     return rc, c.value, n.value
 
@@ -59,6 +59,34 @@ def test_decode_plan_c4_and_ragged_total():
     # stay at two workgroups per CU, with the 32-token minimum chunk
     assert _plan(8, 8, 2048)[:2] == (0, 32)
     assert _plan(16, 12, 1024)[:2] == (0, 32)
+
+
+@pytest.mark.parametrize("B,Hkv,Hq,L,total", [(64, 8, 32, 8192, 0), (64, 8, 32, 8192, 132154),
+                                                (4, 8, 32, 32768, 128000), (1, 2, 8, 300, 0),
+                                                (16, 16, 32, 1024, 0), (8, 4, 32, 100000, 0)])
+def test_decode_plan_gqa_matrix_core_kernel(B, Hkv, Hq, L, total):
+    """Grouped queries over a bf16 cache with head_dim 64/128 run the MFMA
+    kernel: one busy workgroup per CU for 230 of the 256 CUs, chunks a
+    multiple of 16, every length covered."""
+    rc, chunk, n = _plan(B, Hkv, L, total=total, Hq=Hq, D=128, dt=_lib.BF16)
+    assert rc == 0
+    assert chunk % 16 == 0 and 32 <= chunk <= 8192
+    assert (n - 1) * chunk >= L > (n - 2) * chunk
+    groups = Hkv // min(8, Hkv & -Hkv)
+    tot = total if total > 0 else B * L
+    if 32 < chunk < 8192:
+        assert -(-tot * groups // chunk) <= 230 < -(-tot * groups // (chunk - 16))
+
+
+def test_decode_plan_c5_kernel_choice():
+    # C5 (64 sequences, 32 query / 8 kv heads, lengths summing to 132154):
+    # the bf16 D=128 cache gets 576-token chunks (230 workgroups), the same
+    # shapes over an fp32 cache (VALU kernel) 288-token ones (459)
+    assert _plan(64, 8, 8192, total=132154, Hq=32, D=128, dt=_lib.BF16) == (0, 576, 16)
+    assert _plan(64, 8, 8192, total=132154, Hq=32, D=128, dt=_lib.F32) == (0, 288, 30)
+    # head dims other than 64 and 128 and MHA keep the VALU plans
+    assert _plan(64, 8, 8192, total=132154, Hq=32, D=96, dt=_lib.BF16)[1] == 288
+    assert _plan(4, 16, 32256, D=128, dt=_lib.BF16) == (0, 512, 64)
 
 
 def test_decode_plan_hint_and_errors():

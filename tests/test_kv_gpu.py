@@ -337,8 +337,8 @@ def test_decode_empty_sequence_and_plan_overflow(gpu_ctx):
     from simple_llm_amd import _lib
     L = _lib.lib()
     chunk, nch = ctypes.c_int(), ctypes.c_int()
-    _lib.check(L.skv_decode_plan(B, H, H, 256, 0, 256, ctypes.byref(chunk), ctypes.byref(nch)),
-               "plan")
+    _lib.check(L.skv_decode_plan(B, H, H, D, _lib.F32, 256, 0, 256, ctypes.byref(chunk),
+                                 ctypes.byref(nch)), "plan")
     need = L.skv_decode_workspace_bytes(B, H, D, nch.value)
     ws = torch.empty(need, dtype=torch.uint8, device="cuda")
     qd = to_dev(q)

@@ -40,8 +40,9 @@ def _both(L, _lib, k, v, q, lens, Hq, Hkv, D, dtype):
     kd, vd, qd = dev(k, dtype), dev(v, dtype), dev(q)
     ld = torch.from_numpy(np.asarray(lens, np.int32)).cuda()
     chunk, nch = ctypes.c_int(), ctypes.c_int()
-    _lib.check(L.skv_decode_plan(B, Hq, Hkv, int(max(lens)), int(np.sum(lens)), 0,
-                                 ctypes.byref(chunk), ctypes.byref(nch)), "plan")
+    _lib.check(L.skv_decode_plan(B, Hq, Hkv, D, _lib.dtype_code(dtype), int(max(lens)),
+                                 int(np.sum(lens)), 0, ctypes.byref(chunk), ctypes.byref(nch)),
+               "plan")
     cdt = _lib.dtype_code(dtype)
     s = _lib.stream_handle(qd.device)
     out_n = torch.full_like(qd, float("nan"))
