@@ -64,6 +64,8 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 8;     // wavefronts per workgroup
 constexpr int kSub = 16;      // tokens per wavefront and stage (one MFMA tile)
 constexpr float kLazy = 8.f;  // rescale when the max grows by more than this (log2 units)
+constexpr int kMaxChunk = 8192;                // longest chunk (tokens) the kernel takes
+constexpr int kMaxTiles = kMaxChunk / 16 + 2;  // 16-token tiles a piece can touch
 
 template <int D>
 struct Gq {
@@ -103,15 +105,6 @@ __device__ __forceinline__ u32x4_t load8_bf16(const void* p, size_t i, int dt) {
   return __builtin_bit_cast(u32x4_t, h);
 }
 
-// A wavefront-uniform 32-bit value that no kernel of the call writes (the
-// page table), read through the constant address space: a scalar load,
-// waited for on its own counter. A plain load of it compiles to a vector
-// load (the kernel's stores could alias it), and waiting for that vector
-// load waits for every load in flight as well.
-__device__ __forceinline__ int load_uniform(const int32_t* p) {
-  return *(const __attribute__((address_space(4))) int32_t*)(p);
-}
-
 template <int G>
 __device__ __forceinline__ float shl_cols(float x) {  // lane i <- lane i + G of its 16-lane row
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + G, 0xF, 0xF,
@@ -119,10 +112,10 @@ __device__ __forceinline__ float shl_cols(float x) {  // lane i <- lane i + G of
 }
 
 // One piece [start, end) of sequence b for kv head group hg; the partials go
-// to `slot`. smem: one stage (SBYTES bytes).
+// to `slot`. smem: one stage (SBYTES bytes); s_rows: kMaxTiles cache rows.
 template <int D, int G, bool PAGED>
 __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, int start, int end,
-                                          int slot, char* smem) {
+                                          int slot, char* smem, long long* s_rows) {
   using Sh = Gq<D>;
   constexpr int KB = Sh::KB, CPR = Sh::CPR, DB = Sh::DB, NI = Sh::NI;
   constexpr int TBYTES = Sh::TBYTES;
@@ -163,11 +156,25 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
   const uint16_t* kc = static_cast<const uint16_t*>(a.k);
   const uint16_t* vc = static_cast<const uint16_t*>(a.v);
 
-  // Cache row of token Tt (a multiple of 16, <= tlast); uniform.
+  // Cache rows of the piece's 16-token tiles. Paged: looked up once per
+  // piece into LDS (one vector load per tile, all in flight together), so a
+  // stage's loads do not wait on a page-table read.
+  if constexpr (PAGED) {
+    const int ntiles = (tlast - T0) / 16 + 1;
+    for (int i = tid; i < ntiles; i += kWaves * 64) {
+      const int Tt = T0 + 16 * i;
+      const long long blk = a.block_table[(size_t)b * a.max_blocks + (Tt >> a.bs_shift)];
+      s_rows[i] = (blk << a.bs_shift) + (Tt & ((1 << a.bs_shift) - 1));
+    }
+    __syncthreads();
+  }
+  // Cache row of token Tt (a multiple of 16, in [T0, tlast]); uniform.
   auto tile_row = [&](int Tt) -> size_t {
     if constexpr (PAGED) {
-      const int blk = load_uniform(a.block_table + (size_t)b * a.max_blocks + (Tt >> a.bs_shift));
-      return ((size_t)blk << a.bs_shift) + (Tt & ((1 << a.bs_shift) - 1));
+      const long long r = s_rows[(Tt - T0) >> 4];  // the same for every lane
+      const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)r);
+      const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(r >> 32));
+      return ((size_t)hi << 32) | lo;
     } else {
       return (size_t)b * a.T_cap + Tt;
     }
@@ -197,8 +204,13 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
   // (r[NI + i]). A piece's rows lie in one 16-token tile (a piece holds 1
   // to 8 whole tokens), so its page is uniform. Rows at or past the
   // piece's end are read from its last row.
+  // A wavefront's pieces hold stage tokens [2 S w, 2 S w + 2 S) (16 / hw
+  // tokens per 2 D units), all in one 16-token tile.
+  const int twave = (wave * NI * 64 / CPR) >> lhw;
   auto load_stage = [&](int k, u32x4_t (&r)[2 * NI]) {
     const int T = T0 + k * TS;
+    const int Tt = min(T + (twave & ~15), tlast);
+    const size_t trow = tile_row(Tt);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int piece = wave * NI + i;
@@ -206,9 +218,6 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
       const int ri = pos / CPR;
       const int t = ri >> lhw, hd = ri & (hw - 1);
       const int lc = (pos % CPR) ^ swz<D>(t);
-      const int tfirst = __builtin_amdgcn_readfirstlane((piece * 64 / CPR) >> lhw);
-      const int Tt = min(T + (tfirst & ~15), tlast);
-      const size_t trow = tile_row(Tt);
       const int tok = min(T + t, end - 1);
       const size_t e = ((trow + (tok - Tt)) * a.Hkv + hg * hw + hd) * D + 8 * lc;
       r[i] = stream_load16(kc + e);
@@ -441,6 +450,7 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
 template <int D, int G, bool PAGED>
 __global__ __launch_bounds__(kWaves * 64) void k_decode_gqa(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[Gq<D>::SBYTES];
+  __shared__ long long s_rows[PAGED ? kMaxTiles : 1];
   static_assert(Gq<D>::SBYTES >= kWaves * 8 * D * 4 + kWaves * 8 * 2 * 4,
                 "the substream merge reuses the stage's space");
   const int w = blockIdx.x, hg = blockIdx.y;
@@ -450,7 +460,7 @@ __global__ __launch_bounds__(kWaves * 64) void k_decode_gqa(DecodeArgs a) {
   int budget = a.chunk;
   while (true) {
     const int n = min(clamped_len(a, b) - off, budget);
-    gqa_piece<D, G, PAGED>(a, hg, b, off, off + n, w + b, smem);
+    gqa_piece<D, G, PAGED>(a, hg, b, off, off + n, w + b, smem, s_rows);
     budget -= n;
     if (budget == 0) break;
     do {
@@ -472,7 +482,7 @@ void launch_dg(const DecodeArgs& a, bool paged, hipStream_t s) {
 
 bool gqa_mfma_eligible(const DecodeArgs& a, int G, bool bf16_cache, bool paged) {
   return bf16_cache && (a.D == 64 || a.D == 128) && (G == 2 || G == 4 || G == 8) &&
-         (!paged || a.bs_shift >= 4);
+         (!paged || a.bs_shift >= 4) && a.chunk <= kMaxChunk;
 }
 
 int launch_partial_gqa(const DecodeArgs& a0, int G, bool paged, hipStream_t s) {
