@@ -42,9 +42,10 @@
 //    token order in which the score lanes hold them (no shuffle); operand A
 //    is V^T, 4 tokens of one element per lane, read with ds_read_b64_tr_b16.
 //    At the end column G + c is added to column c.
-// Tokens outside the piece are masked (score -inf); rows past its end are
-// loaded from its last row, so no page past the fill is touched and no
-// uninitialised memory meets a zero weight (0 * NaN). A fused append's rows
+// Tokens outside the piece are masked (score -inf), and their rows are
+// loaded from its first or last row: no page past the fill is touched, no
+// uninitialised memory meets a zero weight (0 * NaN), and the first tile's
+// tokens before the piece (another workgroup's) cost no HBM traffic. A fused append's rows
 // are stored to the cache (rounded to bf16) at the start of the piece, and
 // the stores complete before any wavefront loads the stage holding them.
 // No atomics: results are bitwise reproducible, and a paged cache gives the
@@ -202,8 +203,8 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
   // token t, head hd of the group), physical chunk pos % CPR; wavefront w
   // moves the 1 KB pieces [w NI, (w + 1) NI) of K (r[i]) and of V
   // (r[NI + i]). A piece's rows lie in one 16-token tile (a piece holds 1
-  // to 8 whole tokens), so its page is uniform. Rows at or past the
-  // piece's end are read from its last row.
+  // to 8 whole tokens), so its page is uniform. Rows outside the piece
+  // are read from its first or last row.
   // A wavefront's pieces hold stage tokens [2 S w, 2 S w + 2 S) (16 / hw
   // tokens per 2 D units), all in one 16-token tile.
   const int twave = (wave * NI * 64 / CPR) >> lhw;
@@ -218,7 +219,10 @@ __device__ __forceinline__ void gqa_piece(const DecodeArgs& a, int hg, int b, in
       const int ri = pos / CPR;
       const int t = ri >> lhw, hd = ri & (hw - 1);
       const int lc = (pos % CPR) ^ swz<D>(t);
-      const int tok = min(T + t, end - 1);
+      // rows outside the piece (the first tile's tokens before start, the
+      // last one's past end) reread the piece's first or last row: masked
+      // anyway, and an L2 hit instead of a fetch from HBM
+      const int tok = min(max(T + t, start), end - 1);
       const size_t e = ((trow + (tok - Tt)) * a.Hkv + hg * hw + hd) * D + 8 * lc;
       r[i] = stream_load16(kc + e);
       r[NI + i] = stream_load16(vc + e);
