@@ -462,7 +462,10 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
     mean_s = ev0.elapsed_time(ev1) * 1e-3 / steps
     chunk, n_chunks = gpu.decode_plan(ctx, B, Hq, Hkv, max_len, int(lens0.sum()),
                                       head_dim=cache.head_dim, dtype=cache.dtype)
-    roof = {"kernel": "append + decode attention (k_decode_partial + k_decode_merge)", "bound": "hbm",
+    # grouped queries over a bf16 cache with head_dim 64/128 run the matrix-core pass 1
+    pass1 = ("k_decode_gqa" if Hq > Hkv and Hq // Hkv in (2, 4, 8) and s_kv == 2
+             and Dh in (64, 128) else "k_decode_partial")
+    roof = {"kernel": f"append + decode attention ({pass1} + k_decode_merge)", "bound": "hbm",
             "achieved": byts / mean_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": byts / mean_s / 1e9 / HBM_PEAK_GBS, "traffic": None,
             "mean_call_us": mean_s * 1e6, "algorithmic_bytes_per_call": byts,
