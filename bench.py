@@ -103,10 +103,11 @@ def algorithmic_bytes(lens, h_q=H, h_kv=H, d=D, s_kv=2, s_q=4, s_o=4) -> int:
     return int(sum(2 * h_kv * int(L) * d * s_kv + h_q * d * (s_q + s_o) for L in lens))
 
 
-def measured_traffic():
+def measured_traffic(workload: str = "c4"):
     """HBM bytes per decode-attention call from the committed rocprofv3 PMC
-    summary (profiles/decode_attn_c4_pmc.md), or None if absent."""
-    path = os.path.join(ROOT, "profiles", "decode_attn_c4_pmc.md")
+    summary of the workload (profiles/decode_attn_<workload>_pmc.md), or None
+    if absent."""
+    path = os.path.join(ROOT, "profiles", f"decode_attn_{workload}_pmc.md")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -467,7 +468,7 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
              and Dh in (64, 128) else "k_decode_partial")
     roof = {"kernel": f"append + decode attention ({pass1} + k_decode_merge)", "bound": "hbm",
             "achieved": byts / mean_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": byts / mean_s / 1e9 / HBM_PEAK_GBS, "traffic": None,
+            "frac": byts / mean_s / 1e9 / HBM_PEAK_GBS, "traffic": measured_traffic(label),
             "mean_call_us": mean_s * 1e6, "algorithmic_bytes_per_call": byts,
             "split_k": {"chunk_tokens": chunk, "n_chunks": n_chunks}}
     return wall, active, roof, (q_all, k_all, v_all)
