@@ -103,8 +103,8 @@ int skv_advance(int32_t* lens, const int32_t* n_new, int n_const, int B, int T_c
  * tokens end to end -- per workgroup) for the pass-1 kernel a call with
  * this head_dim and cache_dtype runs: grouped queries (H_q / H_kv in
  * {2, 4, 8}) over a bf16 cache with head_dim 64 or 128 run on the matrix
- * cores, one busy workgroup per CU for about 90% of the CUs (HBM streams
- * faster with fewer streams than CUs); the other kernels get about two busy
+ * cores, one busy workgroup per CU for 7/8 of the CUs (HBM streams faster
+ * with fewer streams than CUs); the other kernels get about two busy
  * workgroups per CU (512), or one per CU (256) when H_q == H_kv and that
  * still gives chunks of at least 256 tokens. n_chunks_max =
  * ceil(max_len / chunk_tokens) + 1 partial slots per sequence: B *

@@ -342,14 +342,15 @@ extern "C" int skv_decode_plan(int B, int H_q, int H_kv, int head_dim, int cache
              (G == 2 || G == 4 || G == 8)) {
     // The matrix-core GQA kernel (decode_gqa_mfma.hip): one workgroup of 8
     // wavefronts per CU, kv heads in groups of up to 8. It is bound by HBM,
-    // which served fewer concurrent streams than CUs faster: C5 (132K
-    // tokens, 8 kv heads) 101.7 us per call at 230 workgroups of 576 tokens,
-    // 104.0 us at 243 of 544; past 256 (512 tokens: 258) a second round of
-    // workgroups costs 45%.
+    // which served fewer concurrent streams than CUs faster. C5 (132K
+    // tokens, 8 kv heads), one process, chunk sizes interleaved over three
+    // rounds: 252 workgroups 97.8 us per call, 231: 96.1-96.6, 219-225:
+    // 95.1-95.5, 208: 95.9, 189: 98.2, 173: 104.3; past 256 (512 tokens:
+    // 258) a second round of workgroups costs 45%.
     int hw = 1;
     while (hw < 8 && H_kv % (hw * 2) == 0) hw *= 2;
     const long long groups = H_kv / hw;
-    const long long target = kNumCUs * 9 / 10;
+    const long long target = kNumCUs * 7 / 8;
     long long per = (tot * groups + target - 1) / target;
     per = (per + 15) / 16 * 16;
     chunk = (int)std::min<long long>(std::max<long long>(per, 32), 8192);

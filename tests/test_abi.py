@@ -66,7 +66,7 @@ def test_decode_plan_c4_and_ragged_total():
                                                 (16, 16, 32, 1024, 0), (8, 4, 32, 100000, 0)])
 def test_decode_plan_gqa_matrix_core_kernel(B, Hkv, Hq, L, total):
     """Grouped queries over a bf16 cache with head_dim 64/128 run the MFMA
-    kernel: one busy workgroup per CU for 230 of the 256 CUs, chunks a
+    kernel: one busy workgroup per CU for 224 of the 256 CUs, chunks a
     multiple of 16, every length covered."""
     rc, chunk, n = _plan(B, Hkv, L, total=total, Hq=Hq, D=128, dt=_lib.BF16)
     assert rc == 0
@@ -75,14 +75,14 @@ def test_decode_plan_gqa_matrix_core_kernel(B, Hkv, Hq, L, total):
     groups = Hkv // min(8, Hkv & -Hkv)
     tot = total if total > 0 else B * L
     if 32 < chunk < 8192:
-        assert -(-tot * groups // chunk) <= 230 < -(-tot * groups // (chunk - 16))
+        assert -(-tot * groups // chunk) <= 224 < -(-tot * groups // (chunk - 16))
 
 
 def test_decode_plan_c5_kernel_choice():
     # C5 (64 sequences, 32 query / 8 kv heads, lengths summing to 132154):
-    # the bf16 D=128 cache gets 576-token chunks (230 workgroups), the same
+    # the bf16 D=128 cache gets 592-token chunks (224 workgroups), the same
     # shapes over an fp32 cache (VALU kernel) 288-token ones (459)
-    assert _plan(64, 8, 8192, total=132154, Hq=32, D=128, dt=_lib.BF16) == (0, 576, 16)
+    assert _plan(64, 8, 8192, total=132154, Hq=32, D=128, dt=_lib.BF16) == (0, 592, 15)
     assert _plan(64, 8, 8192, total=132154, Hq=32, D=128, dt=_lib.F32) == (0, 288, 30)
     # head dims other than 64 and 128 and MHA keep the VALU plans
     assert _plan(64, 8, 8192, total=132154, Hq=32, D=96, dt=_lib.BF16)[1] == 288
