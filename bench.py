@@ -49,6 +49,12 @@ for _p in (ROOT, PKG):
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 PREFILL_C = 512  # C4's chunked prefill: 512 tokens from fill 32256 to 32768
+# Before the warm-up steps, the attention workloads run their own step,
+# untimed, for this long (rewinding the cache between bursts): from idle, an
+# MI355X's clock ramps over the first few milliseconds of load, and with
+# --warmup 5 the first ~20 timed C4 calls ran at 170-176 us against ~152 us
+# after the ramp (profiles/decode_attn_c4_per_step.md).
+SETTLE_S = 0.25
 
 # C4 workload
 B, H, D, T_CAP, FILL = 4, 16, 128, 32768, 32000
@@ -212,6 +218,22 @@ def _with_cpu_model(cpu):
         cpu = dict(cpu)
         cpu.setdefault("cpu_model", cpu_model())
     return cpu
+
+
+def settle(run_burst, reset) -> float:
+    """Run run_burst() (a few of the workload's own steps) untimed, calling
+    reset() before each burst and once after, for SETTLE_S seconds; returns the
+    seconds spent."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SETTLE_S:
+        reset()
+        run_burst()
+        torch.cuda.synchronize()
+    reset()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
 
 
 def _record(metric, value, unit, steps, warmup, ms_per_step, dtype, config, roofline, cpu,
@@ -435,7 +457,8 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
         gpu.kv_cache_append_attend(ctx, cache, 0, k_all[i], v_all[i], q_all[i], out,
                                    max_len=max_len)
 
-    set_lens(lens0)
+    roofline_settle = settle(lambda: [step(i) for i in range(min(steps, 32))],
+                             lambda: set_lens(lens0))
     for i in range(args.warmup):
         step(steps + i)
     torch.cuda.synchronize()
@@ -470,7 +493,8 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
             "achieved": byts / mean_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": byts / mean_s / 1e9 / HBM_PEAK_GBS, "traffic": measured_traffic(label),
             "mean_call_us": mean_s * 1e6, "algorithmic_bytes_per_call": byts,
-            "split_k": {"chunk_tokens": chunk, "n_chunks": n_chunks}}
+            "split_k": {"chunk_tokens": chunk, "n_chunks": n_chunks},
+            "warmup_settle_s": round(roofline_settle, 3)}
     return wall, active, roof, (q_all, k_all, v_all)
 
 
@@ -758,8 +782,9 @@ def main():
         gpu.kv_cache_append_attend(ctx, cache, 0, k_all[i], v_all[i], q_all[i], out,
                                    max_len=max_len)
 
-    # warm-up, then rewind the fill to FILL
-    cache.current_len = FILL
+    # clock settle and warm-up, then rewind the fill to FILL
+    settle_s = settle(lambda: [step(i) for i in range(min(args.steps, 32))],
+                      lambda: setattr(cache, "current_len", FILL))
     for i in range(args.warmup):
         step(args.steps + i)
     torch.cuda.synchronize()
@@ -816,6 +841,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_settle_s": round(settle_s, 3),
         "ms_per_step": wall / args.steps * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
