@@ -264,9 +264,12 @@ int skv_layernorm(float* y, const float* x, const float* gamma, const float* bet
  * fixed order, so results are reproducible run to run.
  * M <= 64 (a decode step's rows): a weight-streaming kernel. ws (may be
  * NULL) of skv_linear_workspace_bytes(M, N, K) bytes lets a narrow
- * projection (few 16-column tiles) split K over more workgroups and finish
- * in a second kernel; the split sums in a different fixed order, so its bits
- * differ from the unsplit result within fp32 rounding.
+ * projection (few 16-column tiles) split K over more workgroups; the split
+ * sums in a different fixed order, so its bits differ from the unsplit
+ * result within fp32 rounding. Without LayerNorm and with M <= 16 the last
+ * workgroup of each tile to finish sums the split (arrival counters kept in
+ * ws): ws must be zero-filled before its first use, and every call leaves
+ * the counters at zero again; with LayerNorm a second kernel sums it.
  * M > 64 (a prompt's prefill): a tiled MFMA GEMM (128 x 128 tiles of
  * v_mfma_f32_32x32x2_f32); with LayerNorm, ws of
  * skv_linear_workspace_bytes(M, N, K) bytes holds the row statistics,
@@ -277,9 +280,33 @@ int skv_linear(float* y, const float* x, const float* w_t, const float* bias,
                int M, int N, int K, int activation, int split_cols, void* ws, size_t ws_bytes,
                skv_stream_t stream);
 
-/* Workspace skv_linear can use for these sizes: the split-K partials of a
- * narrow projection of at most 64 rows (0: it never splits them), or, for
- * more than 64 rows, M * 2 floats of LayerNorm row statistics. */
+/* LayerNorm folded into a projection's weights for skv_linear_folded:
+ * w_fold[n, k] = ln_gamma[k] * w_t[n, k], c1[n] = sum_k w_fold[n, k],
+ * c2[n] = sum_k ln_beta[k] * w_t[n, k] + bias[n] (bias may be NULL), the
+ * sums in double. w_fold [N, K] may not alias w_t; c1, c2 [N]. Run once per
+ * weight set (no counterpart in the reference, which normalizes x and then
+ * multiplies: jax_backend.py:135, 138). */
+int skv_linear_fold_ln(float* w_fold, float* c1, float* c2, const float* w_t,
+                       const float* ln_gamma, const float* ln_beta, const float* bias, int N,
+                       int K, skv_stream_t stream);
+
+/* y = act(LN(x) . w_t^T + bias) + residual, as skv_linear with LayerNorm,
+ * from the folded weights of skv_linear_fold_ln:
+ *   LN(x)[m] . w_t[n] + bias[n] = rstd_m (sum_k (x[m, k] - c_m) w_fold[n, k]
+ *                                 - (mean_m - c_m) c1[n]) + c2[n],
+ * c_m = x[m, 0], so the products start before the row statistics are known.
+ * M <= 16 rows; K = 16 * s * w for some s in {3, 4, 6, 8, 12} and 4 <= w <=
+ * 16 (768, 1024, 3072, ...); otherwise SKV_E_UNSUPPORTED. residual may
+ * equal y, x may not; split_cols as for skv_linear. The rounding differs
+ * from skv_linear's within fp32 accuracy; sums run in a fixed order. */
+int skv_linear_folded(float* y, const float* x, const float* w_fold, const float* c1,
+                      const float* c2, const float* residual, float ln_eps, int M, int N, int K,
+                      int activation, int split_cols, skv_stream_t stream);
+
+/* Workspace skv_linear can use for these sizes: the split-K partials (and
+ * arrival counters) of a narrow projection of at most 64 rows (0: it never
+ * splits them), or, for more than 64 rows, M * 2 floats of LayerNorm row
+ * statistics. Zero-fill it once before the first call. */
 size_t skv_linear_workspace_bytes(int M, int N, int K);
 
 /* y[m, :] = x[rows[m], :] for m < M, x [n_rows, d] (rows clamped into

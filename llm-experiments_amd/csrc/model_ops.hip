@@ -97,6 +97,7 @@ __global__ __launch_bounds__(256) void k_layernorm(float* __restrict__ y, const 
 // ---------------------------------------------------------------------------
 // Linear: y = act(x Wt^T + bias) + res, MFMA fp32
 // ---------------------------------------------------------------------------
+constexpr int kNumCUs = 256;          // compute units of an MI355X
 constexpr int kLinRowsPerBlock = 64;  // 4 tiles of 16 rows
 constexpr int kLinMaxWaves = 16;      // wavefronts per workgroup, splitting K
 
@@ -361,6 +362,415 @@ __global__ __launch_bounds__(STEPS > 4 ? 512 : kLinMaxWaves * 64) void k_linear(
   }
 }
 
+// Wide projections of one row tile (M <= 16 rows, at least 1024 16-column
+// tiles: the tied logits, 16 x 768 -> 50304). k_linear gives each 16-column
+// tile its own workgroup, which reads the whole x block (as many bytes as
+// its weights) and reduces across wavefronts; at 3,144 tiles that halved the
+// useful stream of every CU (154.5 MB in ~45 us, 3.4 TB/s). Here one
+// workgroup per CU stages the x rows once in LDS (LayerNorm applied there)
+// and takes a contiguous range of column tiles, 12-13 for the logits. Each
+// tile is cut into four K quarters; the quarter units are dealt to the 8
+// wavefronts round-robin, so the CUs and the wavefronts stream equal byte
+// counts, and a unit's US weight loads (16 bytes per lane each) are issued
+// together. The four quarter partials of a tile are summed in LDS in a
+// fixed order (bitwise reproducible), then the epilogue adds bias and
+// residual and applies the activation.
+constexpr int kWideWaves = 8;
+constexpr int kWideMaxTiles = 16;  // column tiles per workgroup (N <= 65536 on 256 CUs)
+
+template <int US, bool LN>
+__global__ __launch_bounds__(kWideWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void k_linear_wide(LinArgs a, int tiles_total) {
+  extern __shared__ float wsm[];  // x rows [16][K + 4], then partials [tiles][4][64][4]
+  __shared__ float wstat[16][2];
+  const int K = a.K, P = K + 4;   // K = 64 * US
+  float* xs = wsm;
+  float* part = wsm + 16 * P;
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, lr = l & 15, lk = l >> 4;
+  const int M = a.M;
+  // this workgroup's column tiles [t0, t1)
+  const int G = gridDim.x;
+  const int t0 = (int)((long long)blockIdx.x * tiles_total / G);
+  const int t1 = (int)((long long)(blockIdx.x + 1) * tiles_total / G);
+  const int nt = t1 - t0;
+  // this wavefront's quarter units: u_k = wave + 8 k, k < nk (u = 4 j + q:
+  // quarter q of tile j)
+  const int nk = (4 * nt - wave + kWideWaves - 1) / kWideWaves;
+  auto issue = [&](int k, float4 (&w)[US]) {
+    // past the last unit the wavefront re-reads its last one (an L2 hit):
+    // loads behind a condition would make the compiler wait for both sets
+    const int u = wave + kWideWaves * min(k, max(nk - 1, 0));
+    const int j = u >> 2, q = u & 3;
+    const int n = min((t0 + j) * 16 + lr, a.N - 1);
+    const float* wp = a.wt + (size_t)n * K + q * (K / 4) + 4 * lk;
+#pragma unroll
+    for (int st = 0; st < US; ++st) w[st] = *reinterpret_cast<const float4*>(wp + 16 * st);
+    // keep the loads here: the scheduler would otherwise move them down next
+    // to their use, one unit's latency per unit
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // x rows (16 x K, rows past M read row 0 and are zeroed): US / 2 float4
+  // per thread, loaded first; then the first unit's weights, so both round
+  // trips overlap (loads complete in issue order, so x can be waited for
+  // while the weights are still in flight); then x goes to LDS
+  constexpr int XV = US / 2;  // 16 * 64 * US / 4 / (8 * 64)
+  float4 xr[XV], gr[LN ? XV : 1], br[LN ? XV : 1];
+#pragma unroll
+  for (int v = 0; v < XV; ++v) {
+    const int i = (tid + v * kWideWaves * 64) * 4;
+    const int r = i / K, k = i - r * K;
+    xr[v] = *reinterpret_cast<const float4*>(a.x + (size_t)(r < M ? r : 0) * K + k);
+  }
+  if constexpr (LN) {
+    // the norm's scale and shift at the same positions, so that nothing
+    // after this waits on a global load while the weights are in flight
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      const int k = ((tid + v * kWideWaves * 64) * 4) % K;
+      gr[v] = *reinterpret_cast<const float4*>(a.ln_g + k);
+      br[v] = *reinterpret_cast<const float4*>(a.ln_b + k);
+    }
+  }
+  float4 wa[US], wb[US];
+  issue(0, wa);
+#pragma unroll
+  for (int v = 0; v < XV; ++v) {
+    const int i = (tid + v * kWideWaves * 64) * 4;
+    const int r = i / K, k = i - r * K;
+    if (r >= M) xr[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    *reinterpret_cast<float4*>(xs + r * P + k) = xr[v];
+  }
+  __syncthreads();
+  if constexpr (LN) {
+    // row statistics (sums shifted by the row's first element), two rows per
+    // wavefront, then the rows normalized in place
+    for (int r = 2 * wave; r < 2 * wave + 2; ++r) {
+      const float c = xs[r * P];
+      float su = 0.f, sq = 0.f;
+      for (int k = l; k < K; k += 64) {
+        const float d = xs[r * P + k] - c;
+        su += d;
+        sq += d * d;
+      }
+      su = wave_sum(su);
+      sq = wave_sum(sq);
+      if (l == 0) {
+        const float ms = su / K;
+        wstat[r][0] = c + ms;
+        wstat[r][1] = 1.f / sqrtf(fmaxf(sq / K - ms * ms, 0.f) + a.ln_eps);
+      }
+    }
+    __syncthreads();
+    // each thread normalizes the elements it staged (rows past M stay zero)
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      const int i = (tid + v * kWideWaves * 64) * 4;
+      const int r = i / K, k = i - r * K;
+      if (r >= M) continue;
+      const float mu = wstat[r][0], rs = wstat[r][1];
+      float4 x = xr[v];
+      x.x = (x.x - mu) * rs * gr[v].x + br[v].x;
+      x.y = (x.y - mu) * rs * gr[v].y + br[v].y;
+      x.z = (x.z - mu) * rs * gr[v].z + br[v].z;
+      x.w = (x.w - mu) * rs * gr[v].w + br[v].w;
+      *reinterpret_cast<float4*>(xs + r * P + k) = x;
+    }
+    __syncthreads();
+  }
+
+  // quarter unit u_k from the weights in w
+  auto compute = [&](int k, const float4 (&w)[US]) {
+    const int u = wave + kWideWaves * k;
+    const int q = u & 3;
+    const float* xp = xs + lr * P + q * (K / 4) + 4 * lk;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < US; ++st) {
+      const float4 xv = *reinterpret_cast<const float4*>(xp + 16 * st);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, w[st].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, w[st].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, w[st].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, w[st].w, acc, 0, 0, 0);
+    }
+    *reinterpret_cast<f32x4*>(part + ((size_t)u * 64 + l) * 4) = acc;
+  };
+  // two units in flight per wavefront: unit k + 1 loads while unit k is
+  // consumed. The body has no branch between a load and its use (with one the
+  // compiler sinks the loads next to their use and the overlap is lost); an
+  // odd last unit is done after the loop.
+  int k = 0;
+  for (; k + 1 < nk; k += 2) {
+    issue(k + 1, wb);
+    compute(k, wa);
+    issue(k + 2, wa);
+    compute(k + 1, wb);
+  }
+  if (k < nk) compute(k, wa);
+  __syncthreads();
+  // epilogue: tile j by wavefront j % 8; slot i of lane l is row 4 lk + i, column lr
+  for (int j = wave; j < nt; j += kWideWaves) {
+    const int n = (t0 + j) * 16 + lr;
+    if (n >= a.N) continue;
+    f32x4 v = *reinterpret_cast<const f32x4*>(part + ((size_t)(4 * j) * 64 + l) * 4);
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+      v += *reinterpret_cast<const f32x4*>(part + ((size_t)(4 * j + q) * 64 + l) * 4);
+    const float bv = a.bias ? a.bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * lk + i;
+      if (m >= M) continue;
+      float y = v[i] + bv;
+      if (a.act == 1) y = gelu_tanh(y);
+      if (a.res) y += a.res[(size_t)m * a.N + n];
+      a.y[(size_t)m * a.N + n] = y;
+    }
+  }
+}
+
+// Skinny projections (M <= 16 rows, one row tile) with K = 16 * STEPS * NW:
+// one 16-column tile per workgroup, wavefront w taking the K range
+// [16 STEPS w, 16 STEPS (w + 1)). A decode step's projections are a few MB
+// each (16 x 768 -> 2304 is 7.1 MB), so one HBM round trip of every
+// workgroup's loads, the products and one cross-wavefront sum set the time;
+// per-phase clocks on MI355X showed that what costs is what a CU returns to
+// its registers (weights and x rows, 16 bytes a lane each, as many bytes of
+// x as of weights) and every wait between phases. So:
+//  - every load (weights, x, and the epilogue's bias, residual and
+//    LayerNorm terms) is issued before the first use, weights and x
+//    interleaved by step, so the products of step s start when step s has
+//    arrived;
+//  - with LN the weights come folded (skv_linear_fold_ln): w' = gamma * w,
+//    c1[n] = sum_k w'[n, k], c2[n] = beta . w[n, :] + bias[n], and
+//      LN(x) . w^T + bias = rstd (sum_k (x - c) w' - (mean - c) c1) + c2
+//    for any shift c (c = x[m, 0] here, so that neither the sums of the row
+//    statistics nor the products cancel against a large mean). The products
+//    run on raw x as soon as it lands, the row sums of (x - c) and (x - c)^2
+//    come from the same registers, and both meet in the epilogue after the
+//    one barrier; gamma and beta are never loaded (16 x 768 -> 2304 with
+//    LN went from 8.0 to ... us).
+// Rows past M read row M - 1 (their results are dropped), so no load is
+// conditional. The NW wavefront partials are summed in order in LDS.
+//
+// Split K (grid.y = S > 1, no LN): workgroup (j, z) takes the K range
+// [z K / S, (z + 1) K / S) of tile j, for narrow layers with too few tiles
+// to occupy the CUs (16 x 3072 -> 768: 48 tiles). The last of a tile's S
+// workgroups to finish sums the S partial tiles, in z order, and runs the
+// epilogue; no second launch. A device-scope fence in every workgroup would
+// write back its XCD's L2 (~30 us a call, measured on MI355X), so the
+// partials instead go out as device-scope atomic stores, which write
+// through to memory: each thread waits until its store is acknowledged
+// before the workgroup's barrier, one thread then counts the arrival with a
+// device-scope atomic add, and the last arriver reads the partials with
+// device-scope atomic loads, which are served from memory. The arrival
+// counters (one per tile, in the caller's workspace) start at zero and the
+// last arriver puts its tile's back to zero.
+template <int STEPS, bool LN>
+__global__ __launch_bounds__(1024) void k_linear_skinny(LinArgs a, const float* __restrict__ c1,
+                                                        unsigned* __restrict__ cnt) {
+  extern __shared__ float sred[];  // [NW][64][4] partial tiles, then [NW][16][2] row sums
+  const int NW = blockDim.x >> 6;
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, lr = l & 15, lk = l >> 4;
+  const int M = a.M, K = a.K, N = a.N;
+  const int n0 = blockIdx.x * 16;
+  // epilogue operands: thread t < 256 finishes y[m = t / 16, n0 + t % 16]
+  const int em = tid >> 4, en = n0 + (tid & 15);
+  const int emc = min(em, M - 1), enc = min(en, N - 1);
+  size_t oidx = (size_t)emc * N + enc;
+  if (a.split > 0) {
+    const int seg = enc / a.split;
+    oidx = ((size_t)seg * M + emc) * a.split + (enc - seg * a.split);
+  }
+  const float e_bias = a.bias ? a.bias[enc] : 0.f;
+  const float e_res = a.res ? a.res[oidx] : 0.f;
+  const float e_c1 = LN ? c1[enc] : 0.f;
+  // this lane's x row (the A operand's row is lane % 16) and its shift
+  const int rx = min(lr, M - 1);
+  const float cs = LN ? a.x[(size_t)rx * K] : 0.f;
+  const int kb = blockIdx.y * a.kz + wave * (STEPS * 16) + 4 * lk;
+  const float* wp = a.wt + (size_t)min(n0 + lr, N - 1) * K + kb;
+  const float* xp = a.x + (size_t)rx * K + kb;
+  float4 w[STEPS], xv[STEPS];
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    w[st] = *reinterpret_cast<const float4*>(wp + 16 * st);
+    xv[st] = *reinterpret_cast<const float4*>(xp + 16 * st);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  float su = 0.f, sq = 0.f;
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    float4 v = xv[st];
+    if constexpr (LN) {
+      v.x -= cs;
+      v.y -= cs;
+      v.z -= cs;
+      v.w -= cs;
+      su += (v.x + v.y) + (v.z + v.w);
+      sq += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(v.x, w[st].x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(v.y, w[st].y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(v.z, w[st].z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(v.w, w[st].w, acc, 0, 0, 0);
+  }
+  // slot i of lane l: row 4 (l / 16) + i, column l % 16
+  *reinterpret_cast<f32x4*>(sred + ((size_t)wave * 64 + l) * 4) = acc;
+  float* rsum = sred + (size_t)NW * 256;
+  if constexpr (LN) {
+    // lanes lr, lr + 16, lr + 32, lr + 48 hold row lr
+    su += __shfl_xor(su, 16);
+    sq += __shfl_xor(sq, 16);
+    su += __shfl_xor(su, 32);
+    sq += __shfl_xor(sq, 32);
+    if (lk == 0) {
+      rsum[(wave * 16 + lr) * 2] = su;
+      rsum[(wave * 16 + lr) * 2 + 1] = sq;
+    }
+  }
+  __syncthreads();
+  const bool et = tid < 256;
+  const int pl = 16 * (em >> 2) + (en - n0), pi = em & 3;
+  float v = 0.f;
+  if (et)
+    for (int wv = 0; wv < NW; ++wv) v += sred[((size_t)wv * 64 + pl) * 4 + pi];
+  const int S = gridDim.y;
+  if (!LN && S > 1) {
+    __shared__ unsigned s_last;
+    float* pt = a.part + (size_t)blockIdx.x * S * 256;
+    if (et) __hip_atomic_store(pt + blockIdx.y * 256 + tid, v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the write-through store is acknowledged
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(cnt + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!et) return;
+    float pz[8];
+    v = 0.f;
+    for (int z0 = 0; z0 < S; z0 += 8) {  // up to 8 loads in flight, summed in z order
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        pz[i] = __hip_atomic_load(pt + min(z0 + i, S - 1) * 256 + tid, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (z0 + i < S) v += pz[i];
+    }
+  }
+  if (!et || em >= M || en >= N) return;
+  if constexpr (LN) {
+    float s1 = 0.f, s2 = 0.f;
+    for (int wv = 0; wv < NW; ++wv) {
+      s1 += rsum[(wv * 16 + em) * 2];
+      s2 += rsum[(wv * 16 + em) * 2 + 1];
+    }
+    const float ms = s1 / K;  // mean - c
+    const float rstd = 1.f / sqrtf(fmaxf(s2 / K - ms * ms, 0.f) + a.ln_eps);
+    v = rstd * (v - ms * e_c1);
+  }
+  v += e_bias;
+  if (a.act == 1) v = gelu_tanh(v);
+  a.y[oidx] = v + e_res;
+}
+
+// Steps per wavefront of k_linear_skinny for this K (NW = K / (16 STEPS)
+// wavefronts, 4..16), 0 when none fits.
+int skinny_steps(int K) {
+  for (int st : {3, 4, 6, 8, 12}) {
+    if (K % (16 * st)) continue;
+    const int nw = K / (16 * st);
+    if (nw >= 4 && nw <= 16) return st;
+  }
+  return 0;
+}
+
+// K splits of k_linear_skinny for a projection without LayerNorm: narrow
+// layers (fewer than 128 tiles) split until about 192 workgroups, keeping
+// every split's K range a k_linear_skinny shape.
+int skinny_splits(int M, int N, int K) {
+  const int tiles = (N + 15) / 16;
+  if (M > 16 || tiles >= 128) return 1;
+  int best = 1;
+  for (int S : {2, 3, 4, 6, 8}) {
+    if (K % S || skinny_steps(K / S) == 0 || (long)tiles * S > 256) continue;
+    best = S;
+  }
+  return best;
+}
+
+// Workspace of the M <= 64 paths: the skinny kernel's arrival counters
+// always sit in its first kLinCntBytes (one per tile; a split layer has
+// fewer than 128 tiles), and every partial buffer after them, so that calls
+// of different shapes sharing one workspace never write over each other's
+// counters (which each call leaves at zero).
+constexpr size_t kLinCntBytes = 1024;
+
+// Bytes of workspace a skinny split needs: the counters, then the partial tiles.
+size_t skinny_ws_bytes(int N, int S) {
+  const size_t tiles = (N + 15) / 16;
+  return S > 1 ? kLinCntBytes + tiles * S * 256 * sizeof(float) : 0;
+}
+
+// a.kz: K range of one split (K when S == 1); a.part: partials; cnt: counters
+int launch_skinny(const LinArgs& a, const float* c1, bool ln, int S, unsigned* cnt,
+                  hipStream_t s) {
+  const int st = skinny_steps(a.kz);
+  const int nw = a.kz / (16 * st);
+  const size_t lds = (size_t)nw * (256 + 32) * sizeof(float);
+  const dim3 grid((a.N + 15) / 16, S);
+#define SKV_SK(S_)                                                                      \
+  if (st == S_) {                                                                       \
+    if (ln)                                                                             \
+      hipLaunchKernelGGL((k_linear_skinny<S_, true>), grid, dim3(nw * 64), lds, s, a, c1,  \
+                         cnt);                                                           \
+    else                                                                                \
+      hipLaunchKernelGGL((k_linear_skinny<S_, false>), grid, dim3(nw * 64), lds, s, a, c1, \
+                         cnt);                                                           \
+  }
+  SKV_SK(3) SKV_SK(4) SKV_SK(6) SKV_SK(8) SKV_SK(12)
+#undef SKV_SK
+  return check_launch("skv_linear");
+}
+
+// LayerNorm folding for k_linear_skinny: one workgroup per weight row n,
+// sums in double in a fixed order.
+__global__ __launch_bounds__(256) void k_fold_ln(float* __restrict__ wf, float* __restrict__ c1,
+                                                 float* __restrict__ c2,
+                                                 const float* __restrict__ w,
+                                                 const float* __restrict__ g,
+                                                 const float* __restrict__ b,
+                                                 const float* __restrict__ bias, int K) {
+  __shared__ double s1[256], s2[256];
+  const int n = blockIdx.x, t = threadIdx.x;
+  double a1 = 0.0, a2 = 0.0;
+  for (int k = t; k < K; k += 256) {
+    const float wv = w[(size_t)n * K + k];
+    const float f = g[k] * wv;
+    wf[(size_t)n * K + k] = f;
+    a1 += (double)f;
+    a2 += (double)b[k] * (double)wv;
+  }
+  s1[t] = a1;
+  s2[t] = a2;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (t < o) {
+      s1[t] += s1[t + o];
+      s2[t] += s2[t + o];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    c1[n] = (float)s1[0];
+    c2[n] = (float)(s2[0] + (bias ? (double)bias[n] : 0.0));
+  }
+}
+
 // Split-K finish: y = act(bias + sum of the S partials, in order) + res, one
 // thread per output element.
 __global__ __launch_bounds__(256) void k_linear_reduce(LinArgs a, int S) {
@@ -543,9 +953,13 @@ extern "C" int skv_layernorm(float* y, const float* x, const float* gamma, const
 extern "C" size_t skv_linear_workspace_bytes(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   // the GEMM path (more than one 64-row tile): LayerNorm row statistics
-  if (M > kLinRowsPerBlock) return (size_t)M * 2 * sizeof(float);
+  if (M > kLinRowsPerBlock) return kLinCntBytes + (size_t)M * 2 * sizeof(float);
+  // the skinny kernel's split and the LN path's k_linear split (either may
+  // run for these sizes), after the counters
+  const size_t sk = M <= 16 && skinny_steps(K) > 0 ? skinny_ws_bytes(N, skinny_splits(M, N, K)) : 0;
   const int S = linear_splits(M, N, K);
-  return S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+  const size_t kl = S > 1 ? kLinCntBytes + (size_t)S * M * N * sizeof(float) : 0;
+  return sk > kl ? sk : kl;
 }
 
 extern "C" int skv_linear(float* y, const float* x, const float* w_t, const float* bias,
@@ -563,17 +977,52 @@ extern "C" int skv_linear(float* y, const float* x, const float* w_t, const floa
   // Many rows (a prompt's prefill): the tiled GEMM, bound by the products
   // rather than by the weight stream.
   if (M > kLinRowsPerBlock) {
-    const bool room = ws != nullptr && ws_bytes >= (size_t)M * 2 * sizeof(float);
+    const bool room = ws != nullptr && ws_bytes >= kLinCntBytes + (size_t)M * 2 * sizeof(float);
+    float* stats = room ? reinterpret_cast<float*>(static_cast<char*>(ws) + kLinCntBytes) : nullptr;
     return gemm_linear(y, x, w_t, bias, residual, ln_gamma, ln_beta, ln_eps, M, N, K, activation,
-                       split_cols, room ? static_cast<float*>(ws) : nullptr, (hipStream_t)stream);
+                       split_cols, stats, (hipStream_t)stream);
+  }
+  // One row tile over many columns (the tied logits): k_linear_wide.
+  {
+    const int col_tiles = (N + 15) / 16;
+    const int per_wg = (col_tiles + kNumCUs - 1) / kNumCUs;
+    const int us = K / 64;
+    if (M <= 16 && split_cols == 0 && col_tiles >= 1024 && K % 64 == 0 &&
+        per_wg <= kWideMaxTiles && (us == 8 || us == 12 || us == 16)) {
+      LinArgs a{y, x, w_t, bias, residual, ln_gamma, ln_beta, ln_eps, M, N, K, activation, 0, K,
+                nullptr};
+      const size_t lds = ((size_t)16 * (K + 4) + (size_t)per_wg * 4 * 64 * 4) * sizeof(float);
+      const bool ln = ln_gamma != nullptr;
+      hipStream_t s = (hipStream_t)stream;
+#define SKV_WIDE(U, L)                                                                            if (us == U && ln == L)                                                                           hipLaunchKernelGGL((k_linear_wide<U, L>), dim3(kNumCUs), dim3(kWideWaves * 64), lds, s, a,                        col_tiles);
+      SKV_WIDE(8, false) SKV_WIDE(8, true) SKV_WIDE(12, false) SKV_WIDE(12, true)
+      SKV_WIDE(16, false) SKV_WIDE(16, true)
+#undef SKV_WIDE
+      return check_launch("skv_linear");
+    }
+  }
+  // One row tile without LayerNorm, K a multiple of 48..192 (the decode
+  // step's attention output and MLP down projections): k_linear_skinny.
+  if (M <= 16 && ln_gamma == nullptr && skinny_steps(K) > 0) {
+    int S = skinny_splits(M, N, K);
+    if (S > 1 && (ws == nullptr || ws_bytes < skinny_ws_bytes(N, S))) S = 1;
+    if (S > 1 || skinny_splits(M, N, K) == 1) {
+      char* wsb = static_cast<char*>(ws);
+      LinArgs a{y, x, w_t, bias, residual, nullptr, nullptr, 0.f, M, N, K, activation,
+                split_cols, K / S, S > 1 ? reinterpret_cast<float*>(wsb + kLinCntBytes) : nullptr};
+      return launch_skinny(a, nullptr, false, S, S > 1 ? reinterpret_cast<unsigned*>(wsb) : nullptr,
+                           (hipStream_t)stream);
+    }
   }
   const int ksteps = (K + 15) / 16;
   // split K when the caller gave room for the partials
   int S = linear_splits(M, N, K);
-  if (S > 1 && (ws == nullptr || ws_bytes < (size_t)S * M * N * sizeof(float))) S = 1;
+  if (S > 1 && (ws == nullptr || ws_bytes < kLinCntBytes + (size_t)S * M * N * sizeof(float)))
+    S = 1;
   const int kz_steps = (ksteps + S - 1) / S;
   LinArgs a{y, x, w_t, bias, residual, ln_gamma, ln_beta, ln_eps, M, N, K, activation,
-            split_cols, S > 1 ? kz_steps * 16 : K, S > 1 ? static_cast<float*>(ws) : nullptr};
+            split_cols, S > 1 ? kz_steps * 16 : K,
+            S > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kLinCntBytes) : nullptr};
   const int col_tiles = (N + 15) / 16;
   const int tiles = M >= kLinRowsPerBlock ? 4 : (M + 15) / 16;
   // Wavefronts per workgroup and 16-k steps per wavefront and pass, measured
@@ -630,6 +1079,37 @@ extern "C" int skv_linear(float* y, const float* x, const float* w_t, const floa
   hipLaunchKernelGGL(k_linear_reduce, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s, a,
                      S);
   return check_launch("skv_linear");
+}
+
+extern "C" int skv_linear_fold_ln(float* w_fold, float* c1, float* c2, const float* w_t,
+                                  const float* ln_gamma, const float* ln_beta, const float* bias,
+                                  int N, int K, skv_stream_t stream) {
+  SKV_REQUIRE(w_fold && c1 && c2 && w_t && ln_gamma && ln_beta, SKV_E_INVALID,
+              "skv_linear_fold_ln: null pointer argument");
+  SKV_REQUIRE(N > 0 && K > 0, SKV_E_INVALID, "skv_linear_fold_ln: dims must be > 0");
+  SKV_REQUIRE(w_fold != w_t, SKV_E_INVALID, "skv_linear_fold_ln: w_fold may not alias w_t");
+  hipLaunchKernelGGL(k_fold_ln, dim3(N), dim3(256), 0, (hipStream_t)stream, w_fold, c1, c2, w_t,
+                     ln_gamma, ln_beta, bias, K);
+  return check_launch("skv_linear_fold_ln");
+}
+
+extern "C" int skv_linear_folded(float* y, const float* x, const float* w_fold, const float* c1,
+                                 const float* c2, const float* residual, float ln_eps, int M,
+                                 int N, int K, int activation, int split_cols,
+                                 skv_stream_t stream) {
+  SKV_REQUIRE(y && x && w_fold && c1 && c2, SKV_E_INVALID,
+              "skv_linear_folded: null pointer argument");
+  SKV_REQUIRE(M > 0 && N > 0 && K > 0, SKV_E_INVALID, "skv_linear_folded: dims must be > 0");
+  SKV_REQUIRE(activation == 0 || activation == 1, SKV_E_INVALID,
+              "skv_linear_folded: bad activation");
+  SKV_REQUIRE(split_cols >= 0 && (split_cols == 0 || N % split_cols == 0), SKV_E_INVALID,
+              "skv_linear_folded: N=%d is not a multiple of split_cols=%d", N, split_cols);
+  SKV_REQUIRE(M <= 16, SKV_E_UNSUPPORTED, "skv_linear_folded: M=%d > 16 rows", M);
+  SKV_REQUIRE(skinny_steps(K) > 0, SKV_E_UNSUPPORTED,
+              "skv_linear_folded: K=%d is not 16 * s * w for s in {3,4,6,8,12}, 4 <= w <= 16", K);
+  LinArgs a{y, x, w_fold, c2, residual, nullptr, nullptr, ln_eps, M, N, K, activation,
+            split_cols, K, nullptr};
+  return launch_skinny(a, c1, true, 1, nullptr, (hipStream_t)stream);
 }
 
 extern "C" size_t skv_argmax_workspace_bytes(int M, int N) {

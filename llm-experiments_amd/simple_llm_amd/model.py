@@ -126,7 +126,7 @@ class _Buffers:
         # linears (stream ordered)
         lin = max(L.skv_linear_workspace_bytes(B, n, k)
                   for n, k in ((3 * d, d), (d, d), (mlp, d), (d, mlp), (vocab, d)))
-        self.lin_ws = torch.empty(max(lin, 4), dtype=torch.uint8, device=dev)
+        self.lin_ws = torch.zeros(max(lin, 4), dtype=torch.uint8, device=dev)
 
 
 class _PrefillBuffers:
@@ -151,7 +151,7 @@ class _PrefillBuffers:
         L = _lib.lib()
         lin = max(L.skv_linear_workspace_bytes(M, n, k)
                   for n, k in ((3 * d, d), (d, d), (mlp, d), (d, mlp)))
-        self.lin_ws = torch.empty(max(lin, 4), dtype=torch.uint8, device=dev)
+        self.lin_ws = torch.zeros(max(lin, 4), dtype=torch.uint8, device=dev)
 
 
 class TransformerModel:
@@ -253,6 +253,38 @@ class TransformerModel:
             self._bufs[key] = (chunk, n, ws)
         return self._bufs[key]
 
+    def _folded(self):
+        """Per layer, the LayerNorm-folded q/k/v and MLP-up weights of
+        skv_linear_folded (made once, on the current stream), or None when
+        the decode kernels do not take d (K = 16 * s * w, s in {3, 4, 6, 8,
+        12}, 4 <= w <= 16)."""
+        key = "folded"
+        if key not in self._bufs:
+            d = self.tm_params.embedding_dim
+            if not any(d % (16 * st) == 0 and 4 <= d // (16 * st) <= 16
+                       for st in (3, 4, 6, 8, 12)):
+                self._bufs[key] = None
+                return None
+            L = _lib.lib()
+            s = _lib.stream_handle(self.ctx.device)
+            out = []
+            for lw in self.layers:
+                f = {}
+                for name, w, g, be, b in (("qkv", lw["wqkv_t"], lw["g1"], lw["be1"], None),
+                                          ("w1", lw["w1_t"], lw["g2"], lw["be2"], lw["b1"])):
+                    n, k = w.shape
+                    wf = torch.empty_like(w)
+                    c1 = torch.empty(n, device=w.device)
+                    c2 = torch.empty(n, device=w.device)
+                    _lib.check(L.skv_linear_fold_ln(wf.data_ptr(), c1.data_ptr(), c2.data_ptr(),
+                                                    w.data_ptr(), g.data_ptr(), be.data_ptr(),
+                                                    b.data_ptr() if b is not None else None, n,
+                                                    k, s), "skv_linear_fold_ln")
+                    f[name] = (wf, c1, c2)
+                out.append(f)
+            self._bufs[key] = out
+        return self._bufs[key]
+
     def _launch_step(self, cache: KVCache, bf: _Buffers) -> None:
         L = _lib.lib()
         tm = self.tm_params
@@ -268,14 +300,21 @@ class TransformerModel:
         q_ptr, k_ptr, v_ptr = qkv, qkv + B * d * 4, qkv + 2 * B * d * 4
         lw_ws, lw_n = bf.lin_ws.data_ptr(), bf.lin_ws.numel()
         lens0 = cache.layers[0].lens.data_ptr()
+        # up to 16 rows: LayerNorm folded into the weights (skv_linear_folded)
+        folded = self._folded() if B <= 16 else None
         chk(L.skv_embed(x, bf.ids.data_ptr(), lens0, self.emb.data_ptr(), self.pe.data_ptr(), B, d,
                         tm.vocab_size, self.pe.shape[0], s), "skv_embed")
-        for lw, layer in zip(self.layers, cache.layers):
+        for li, (lw, layer) in enumerate(zip(self.layers, cache.layers)):
             kc, vc = layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr()
             # q, k, v = LN1(x) . [Wq Wk Wv] (LayerNorm folded into the projection)
-            chk(L.skv_linear(qkv, x, lw["wqkv_t"].data_ptr(), None, None, lw["g1"].data_ptr(),
-                             lw["be1"].data_ptr(), 1e-5, B, 3 * d, d, 0, d, lw_ws, lw_n, s),
-                "skv_linear")
+            if folded is not None:
+                wf, c1, c2 = folded[li]["qkv"]
+                chk(L.skv_linear_folded(qkv, x, wf.data_ptr(), c1.data_ptr(), c2.data_ptr(), None,
+                                        1e-5, B, 3 * d, d, 0, d, s), "skv_linear_folded")
+            else:
+                chk(L.skv_linear(qkv, x, lw["wqkv_t"].data_ptr(), None, None,
+                                 lw["g1"].data_ptr(), lw["be1"].data_ptr(), 1e-5, B, 3 * d, d,
+                                 0, d, lw_ws, lw_n, s), "skv_linear")
             # append k, v at each sequence's fill and attend [0, fill] (one call)
             chk(L.skv_append_decode_attn(attn, q_ptr, kc, vc, k_ptr, v_ptr, layer.lens.data_ptr(),
                                          B, H, H, D, T, scale, chunk, n_chunks, ws.data_ptr(),
@@ -285,9 +324,14 @@ class TransformerModel:
             chk(L.skv_linear(x, attn, lw["wo_t"].data_ptr(), None, x, None, None, 0.0, B, d, d, 0,
                              0, lw_ws, lw_n, s), "skv_linear")
             # ff = gelu(LN2(x) . W1 + b1); x += ff . W2 + b2
-            chk(L.skv_linear(ff, x, lw["w1_t"].data_ptr(), lw["b1"].data_ptr(), None,
-                             lw["g2"].data_ptr(), lw["be2"].data_ptr(), 1e-5, B, self.mlp_dim, d,
-                             1, 0, lw_ws, lw_n, s), "skv_linear")
+            if folded is not None:
+                wf, c1, c2 = folded[li]["w1"]
+                chk(L.skv_linear_folded(ff, x, wf.data_ptr(), c1.data_ptr(), c2.data_ptr(), None,
+                                        1e-5, B, self.mlp_dim, d, 1, 0, s), "skv_linear_folded")
+            else:
+                chk(L.skv_linear(ff, x, lw["w1_t"].data_ptr(), lw["b1"].data_ptr(), None,
+                                 lw["g2"].data_ptr(), lw["be2"].data_ptr(), 1e-5, B,
+                                 self.mlp_dim, d, 1, 0, lw_ws, lw_n, s), "skv_linear")
             chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, None, None, 0.0,
                              B, d, self.mlp_dim, 0, 0, lw_ws, lw_n, s), "skv_linear")
         chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, None, None,
@@ -379,7 +423,7 @@ class TransformerModel:
             layer.host_lens = np.minimum(start + n_host, T)
         if all_logits:
             out = torch.empty((B, C, tm.vocab_size), device=self.ctx.device)
-            lws = torch.empty(max(L.skv_linear_workspace_bytes(M, tm.vocab_size, d), 4),
+            lws = torch.zeros(max(L.skv_linear_workspace_bytes(M, tm.vocab_size, d), 4),
                               dtype=torch.uint8, device=self.ctx.device)
             chk(L.skv_linear(out.data_ptr(), x, self.emb.data_ptr(), None, None, None, None, 0.0,
                              M, tm.vocab_size, d, 0, 0, lws.data_ptr(), lws.numel(), s),

@@ -47,6 +47,11 @@ LINEAR_SHAPES = [(1, 256, 256), (5, 100, 260), (16, 768, 768), (17, 3072, 768), 
                  (3, 50304, 768), (2, 80, 4100), (16, 768, 3072), (1, 256, 1024), (7, 200, 700),
                  (16, 64, 520), (4, 96, 768),
                  (4, 2304, 256),  # M = 4: the last compact-epilogue row count
+                 # M <= 16 without LN: k_linear_skinny, K split over 4 workgroups
+                 # summed by the last one to finish (a partial last tile, M = 1 and 3)
+                 (3, 1000, 768), (1, 768, 3072), (16, 3072, 768), (12, 48, 1536),
+                 # one row tile over >= 1024 column tiles: k_linear_wide (the logits)
+                 (16, 50304, 768), (16, 20000, 512), (9, 16400, 1024),
                  # more than 64 rows: the tiled GEMM (the prefill's projections)
                  (65, 96, 64), (100, 1024, 64), (130, 2304, 768), (257, 768, 3072),
                  (1000, 3072, 768), (4352, 768, 768), (129, 50, 36), (300, 130, 20)]
@@ -89,9 +94,12 @@ def test_linear_matches_numpy(gpu_ctx, M, N, K, epi):
     L = _lib.lib()
     res0 = y.clone()
     # without a workspace: one kernel; with one: narrow shapes split K over
-    # more workgroups and finish in a reduce kernel
+    # more workgroups, summed by the last workgroup of a tile (M <= 16, no
+    # LN; arrival counters in the zero-filled workspace, which every call
+    # leaves at zero: the second call below must write the same bits) or by
+    # a reduce kernel
     wsb = L.skv_linear_workspace_bytes(M, N, K)
-    ws = torch.full((max(wsb, 4) // 4,), float("nan"), device="cuda")  # stale partials
+    ws = torch.zeros((max(wsb, 4) // 4,), device="cuda")
     for use_ws in ([False, True] if wsb else [False]):
         for rep in range(2):  # a second call gives the same bits
             y.copy_(res0)
@@ -111,6 +119,88 @@ def test_linear_matches_numpy(gpu_ctx, M, N, K, epi):
             got = got.reshape(3, M, split).transpose(1, 0, 2).reshape(M, N)
         print(f"use_ws={use_ws} rel_err={rel_rows(got, want):.3e}")
         assert rel_rows(got, want) < FP32_TOL
+
+
+def test_linear_split_shapes_share_workspace(gpu_ctx):
+    """Split projections of different shapes, interleaved on one workspace
+    (as a model's layers and logits share it): each keeps its arrival
+    counters where no other shape's partial tiles land, so every call is
+    complete (a 384-wide projection's partials once overwrote the 300-wide
+    logits' counters, whose tiles were then never written)."""
+    banner("linear split shapes share a workspace")
+    _lib = lib()
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    r = np.random.default_rng(5)
+    shapes = [(1, 384, 384), (1, 300, 384), (16, 768, 3072), (3, 1000, 768), (1, 384, 384)]
+    wsb = max(L.skv_linear_workspace_bytes(M, N, K) for M, N, K in shapes)
+    ws = torch.zeros(wsb // 4 + 1, device="cuda")
+    for rep in range(2):
+        for M, N, K in shapes:
+            x = r.standard_normal((M, K)).astype(np.float32)
+            w = (r.standard_normal((N, K)) * 0.05).astype(np.float32)
+            y = torch.full((M, N), float("nan"), device="cuda")
+            xd, wd = dev(x), dev(w)  # held until the kernel has run
+            _lib.check(L.skv_linear(y.data_ptr(), xd.data_ptr(), wd.data_ptr(), None, None,
+                                    None, None, 0.0, M, N, K, 0, 0, ws.data_ptr(), wsb, s),
+                       "skv_linear")
+            err = rel_rows(y.cpu().numpy(), x.astype(np.float64) @ w.T.astype(np.float64))
+            print(f"rep {rep} M={M} N={N} K={K} rel_err={err:.3e}")
+            assert err < FP32_TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 768), (16, 2304, 768), (16, 3072, 768),
+                                   (7, 1000, 1024), (16, 96, 3072), (3, 2304, 256)])
+def test_linear_folded_matches_numpy(gpu_ctx, M, N, K):
+    """skv_linear_fold_ln + skv_linear_folded: LN(x) . w + bias (GELU, residual,
+    q/k/v segments) from the folded weights, against float64 numpy; rows with a
+    large mean (the shift by x[m, 0] keeps the sums from cancelling)."""
+    banner(f"linear folded M={M} N={N} K={K}")
+    _lib = lib()
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    r = np.random.default_rng(M + N + K)
+    x = (r.standard_normal((M, K)) * 2 + 30 * r.standard_normal((M, 1))).astype(np.float32)
+    w = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(K)).astype(np.float32)
+    beta = (0.1 * r.standard_normal(K)).astype(np.float32)
+    b = r.standard_normal(N).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    wtd, gd, bd, biasd = dev(np.ascontiguousarray(w.T)), dev(g), dev(beta), dev(b)
+    wf = torch.empty((N, K), device="cuda")
+    c1 = torch.empty(N, device="cuda")
+    c2 = torch.empty(N, device="cuda")
+    _lib.check(L.skv_linear_fold_ln(wf.data_ptr(), c1.data_ptr(), c2.data_ptr(), wtd.data_ptr(),
+                                    gd.data_ptr(), bd.data_ptr(), biasd.data_ptr(), N, K, s), "fold")
+    np.testing.assert_allclose(wf.cpu().numpy(), g[None, :] * w.T, rtol=1e-7)
+    xd = dev(x)
+    lnx = mo.layer_norm(x, g, beta)
+    for act, with_res, split in ((0, False, 0), (1, False, 0), (0, True, 0), (0, False, N // 3)):
+        if split and N % 3:
+            continue
+        want = lnx @ w.astype(np.float64) + b
+        if act:
+            want = mo.gelu_tanh(want)
+        y = torch.empty((M, N), device="cuda")
+        rd = None
+        if with_res:
+            y.copy_(torch.from_numpy(res))
+            rd = y
+            want = want + res
+        _lib.check(L.skv_linear_folded(y.data_ptr(), xd.data_ptr(), wf.data_ptr(), c1.data_ptr(),
+                                       c2.data_ptr(), rd.data_ptr() if rd is not None else None,
+                                       1e-5, M, N, K, act, split, s), "skv_linear_folded")
+        got = y.cpu().numpy()
+        if split:
+            got = got.reshape(3, M, split).transpose(1, 0, 2).reshape(M, N)
+        err = rel_rows(got, want)
+        print(f"act={act} res={with_res} split={split} rel_err={err:.3e}")
+        assert err < FP32_TOL
+    # shapes it does not take
+    y = torch.empty((17, N), device="cuda")
+    x17 = torch.zeros((17, K), device="cuda")
+    assert L.skv_linear_folded(y.data_ptr(), x17.data_ptr(), wf.data_ptr(), c1.data_ptr(),
+                               c2.data_ptr(), None, 1e-5, 17, N, K, 0, 0, s) != 0
 
 
 def test_layernorm_and_embed(gpu_ctx):
