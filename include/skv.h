@@ -303,6 +303,27 @@ int skv_linear_folded(float* y, const float* x, const float* w_fold, const float
                       const float* c2, const float* residual, float ln_eps, int M, int N, int K,
                       int activation, int split_cols, skv_stream_t stream);
 
+/* Bytes of skv_linear_pack's copy of a [N, K] weight matrix (0 if K is not
+ * a multiple of 16): N rounded up to 16 rows. */
+size_t skv_linear_packed_bytes(int N, int K);
+
+/* Copies w_t [N, K] into the matrix-core lane order skv_linear_packed reads:
+ * 16-column tiles, then 16-k steps, then 64 lanes of 4 floats (lane l holds
+ * w_t[16 t + l % 16, 16 s + 4 (l / 16) .. + 3]), rows past N zero. Run once
+ * per weight set (no counterpart in the reference, whose weights are used in
+ * place). */
+int skv_linear_pack(float* w_packed, const float* w_t, int N, int K, skv_stream_t stream);
+
+/* y = act(x . w^T + bias) + residual from skv_linear_pack's copy of w, for
+ * one row tile over many columns (the tied logits projection): M <= 16,
+ * K in {512, 768, 1024}, 16384 <= N <= 65536; otherwise SKV_E_UNSUPPORTED.
+ * Every 16-k step of a tile is 1 KB of consecutive bytes, streamed by 16
+ * wavefronts per CU; sums run in a fixed order (its own, so the bits may
+ * differ from skv_linear's within fp32 rounding). */
+int skv_linear_packed(float* y, const float* x, const float* w_packed, const float* bias,
+                      const float* residual, int M, int N, int K, int activation,
+                      skv_stream_t stream);
+
 /* Workspace skv_linear can use for these sizes: the split-K partials (and
  * arrival counters) of a narrow projection of at most 64 rows (0: it never
  * splits them), or, for more than 64 rows, M * 2 floats of LayerNorm row

@@ -375,15 +375,23 @@ __global__ __launch_bounds__(STEPS > 4 ? 512 : kLinMaxWaves * 64) void k_linear(
 // together. The four quarter partials of a tile are summed in LDS in a
 // fixed order (bitwise reproducible), then the epilogue adds bias and
 // residual and applies the activation.
+//
+// PACKED: the weights come in the MFMA lane order of skv_linear_pack
+// (tile-major, then 16-k steps, then lane, 16 bytes a lane), so the 64 lanes
+// of one step load 1 KB of consecutive bytes and a quarter unit is one
+// contiguous block; in the [N, K] layout a step reads 64 bytes from each of
+// 16 rows, which streamed ~8 % slower on MI355X (24.4 against 22.4 us for
+// the logits' 154.5 MB, loads only).
 constexpr int kWideWaves = 8;
 constexpr int kWideMaxTiles = 16;  // column tiles per workgroup (N <= 65536 on 256 CUs)
 
-template <int US, bool LN>
-__global__ __launch_bounds__(kWideWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+template <int US, bool LN, bool PACKED = false, int NW = kWideWaves>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void k_linear_wide(LinArgs a, int tiles_total) {
-  extern __shared__ float wsm[];  // x rows [16][K + 4], then partials [tiles][4][64][4]
+  constexpr int PARTS = NW / 2;  // K parts of a tile (units), 16 US columns of K each
+  extern __shared__ float wsm[];  // x rows [16][K + 4], then partials [tiles][PARTS][64][4]
   __shared__ float wstat[16][2];
-  const int K = a.K, P = K + 4;   // K = 64 * US
+  const int K = a.K, P = K + 4;   // K = 16 * US * PARTS
   float* xs = wsm;
   float* part = wsm + 16 * P;
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, lr = l & 15, lk = l >> 4;
@@ -393,18 +401,30 @@ void k_linear_wide(LinArgs a, int tiles_total) {
   const int t0 = (int)((long long)blockIdx.x * tiles_total / G);
   const int t1 = (int)((long long)(blockIdx.x + 1) * tiles_total / G);
   const int nt = t1 - t0;
-  // this wavefront's quarter units: u_k = wave + 8 k, k < nk (u = 4 j + q:
-  // quarter q of tile j)
-  const int nk = (4 * nt - wave + kWideWaves - 1) / kWideWaves;
+  // this wavefront's units: u_k = wave + NW k, k < nk (u = PARTS j + q: part
+  // q of tile j)
+  const int nk = (PARTS * nt - wave + NW - 1) / NW;
   auto issue = [&](int k, float4 (&w)[US]) {
     // past the last unit the wavefront re-reads its last one (an L2 hit):
     // loads behind a condition would make the compiler wait for both sets
-    const int u = wave + kWideWaves * min(k, max(nk - 1, 0));
-    const int j = u >> 2, q = u & 3;
-    const int n = min((t0 + j) * 16 + lr, a.N - 1);
-    const float* wp = a.wt + (size_t)n * K + q * (K / 4) + 4 * lk;
+    const int u = wave + NW * min(k, max(nk - 1, 0));
+    const int j = u / PARTS, q = u % PARTS;
+    if constexpr (PACKED) {
+      // tile t0 + j, steps [q US, (q + 1) US): 256 floats a step, streamed
+      // (non-temporal: 32.3 -> 30.8 us for the cold logits on MI355X)
+      const float* wp = a.wt + (((size_t)(t0 + j) * (K / 16) + q * US) * 64 + l) * 4;
 #pragma unroll
-    for (int st = 0; st < US; ++st) w[st] = *reinterpret_cast<const float4*>(wp + 16 * st);
+      for (int st = 0; st < US; ++st) {
+        const u32x4_t t = stream_load16(wp + 256 * st);
+        w[st] = make_float4(__uint_as_float(t[0]), __uint_as_float(t[1]), __uint_as_float(t[2]),
+                            __uint_as_float(t[3]));
+      }
+    } else {
+      const int n = min((t0 + j) * 16 + lr, a.N - 1);
+      const float* wp = a.wt + (size_t)n * K + q * (K / PARTS) + 4 * lk;
+#pragma unroll
+      for (int st = 0; st < US; ++st) w[st] = *reinterpret_cast<const float4*>(wp + 16 * st);
+    }
     // keep the loads here: the scheduler would otherwise move them down next
     // to their use, one unit's latency per unit
     __builtin_amdgcn_sched_barrier(0);
@@ -413,11 +433,11 @@ void k_linear_wide(LinArgs a, int tiles_total) {
   // per thread, loaded first; then the first unit's weights, so both round
   // trips overlap (loads complete in issue order, so x can be waited for
   // while the weights are still in flight); then x goes to LDS
-  constexpr int XV = US / 2;  // 16 * 64 * US / 4 / (8 * 64)
+  constexpr int XV = US / 2;  // 16 K / 4 / (NW * 64) float4 a thread
   float4 xr[XV], gr[LN ? XV : 1], br[LN ? XV : 1];
 #pragma unroll
   for (int v = 0; v < XV; ++v) {
-    const int i = (tid + v * kWideWaves * 64) * 4;
+    const int i = (tid + v * NW * 64) * 4;
     const int r = i / K, k = i - r * K;
     xr[v] = *reinterpret_cast<const float4*>(a.x + (size_t)(r < M ? r : 0) * K + k);
   }
@@ -426,7 +446,7 @@ void k_linear_wide(LinArgs a, int tiles_total) {
     // after this waits on a global load while the weights are in flight
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
-      const int k = ((tid + v * kWideWaves * 64) * 4) % K;
+      const int k = ((tid + v * NW * 64) * 4) % K;
       gr[v] = *reinterpret_cast<const float4*>(a.ln_g + k);
       br[v] = *reinterpret_cast<const float4*>(a.ln_b + k);
     }
@@ -435,16 +455,16 @@ void k_linear_wide(LinArgs a, int tiles_total) {
   issue(0, wa);
 #pragma unroll
   for (int v = 0; v < XV; ++v) {
-    const int i = (tid + v * kWideWaves * 64) * 4;
+    const int i = (tid + v * NW * 64) * 4;
     const int r = i / K, k = i - r * K;
     if (r >= M) xr[v] = make_float4(0.f, 0.f, 0.f, 0.f);
     *reinterpret_cast<float4*>(xs + r * P + k) = xr[v];
   }
   __syncthreads();
   if constexpr (LN) {
-    // row statistics (sums shifted by the row's first element), two rows per
-    // wavefront, then the rows normalized in place
-    for (int r = 2 * wave; r < 2 * wave + 2; ++r) {
+    // row statistics (sums shifted by the row's first element), 16 / NW rows
+    // per wavefront, then the rows normalized in place
+    for (int r = wave * (16 / NW); r < (wave + 1) * (16 / NW); ++r) {
       const float c = xs[r * P];
       float su = 0.f, sq = 0.f;
       for (int k = l; k < K; k += 64) {
@@ -464,7 +484,7 @@ void k_linear_wide(LinArgs a, int tiles_total) {
     // each thread normalizes the elements it staged (rows past M stay zero)
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
-      const int i = (tid + v * kWideWaves * 64) * 4;
+      const int i = (tid + v * NW * 64) * 4;
       const int r = i / K, k = i - r * K;
       if (r >= M) continue;
       const float mu = wstat[r][0], rs = wstat[r][1];
@@ -478,11 +498,11 @@ void k_linear_wide(LinArgs a, int tiles_total) {
     __syncthreads();
   }
 
-  // quarter unit u_k from the weights in w
+  // unit u_k from the weights in w
   auto compute = [&](int k, const float4 (&w)[US]) {
-    const int u = wave + kWideWaves * k;
-    const int q = u & 3;
-    const float* xp = xs + lr * P + q * (K / 4) + 4 * lk;
+    const int u = wave + NW * k;
+    const int q = u % PARTS;
+    const float* xp = xs + lr * P + q * (K / PARTS) + 4 * lk;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < US; ++st) {
@@ -507,14 +527,14 @@ void k_linear_wide(LinArgs a, int tiles_total) {
   }
   if (k < nk) compute(k, wa);
   __syncthreads();
-  // epilogue: tile j by wavefront j % 8; slot i of lane l is row 4 lk + i, column lr
-  for (int j = wave; j < nt; j += kWideWaves) {
+  // epilogue: tile j by wavefront j % NW; slot i of lane l is row 4 lk + i, column lr
+  for (int j = wave; j < nt; j += NW) {
     const int n = (t0 + j) * 16 + lr;
     if (n >= a.N) continue;
-    f32x4 v = *reinterpret_cast<const f32x4*>(part + ((size_t)(4 * j) * 64 + l) * 4);
+    f32x4 v = *reinterpret_cast<const f32x4*>(part + ((size_t)(PARTS * j) * 64 + l) * 4);
 #pragma unroll
-    for (int q = 1; q < 4; ++q)
-      v += *reinterpret_cast<const f32x4*>(part + ((size_t)(4 * j + q) * 64 + l) * 4);
+    for (int q = 1; q < PARTS; ++q)
+      v += *reinterpret_cast<const f32x4*>(part + ((size_t)(PARTS * j + q) * 64 + l) * 4);
     const float bv = a.bias ? a.bias[n] : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -548,7 +568,7 @@ void k_linear_wide(LinArgs a, int tiles_total) {
 //    run on raw x as soon as it lands, the row sums of (x - c) and (x - c)^2
 //    come from the same registers, and both meet in the epilogue after the
 //    one barrier; gamma and beta are never loaded (16 x 768 -> 2304 with
-//    LN went from 8.0 to ... us).
+//    LN: 8.0 -> 6.1 us a call, weights streamed from HBM, on MI355X).
 // Rows past M read row M - 1 (their results are dropped), so no load is
 // conditional. The NW wavefront partials are summed in order in LDS.
 //
@@ -735,6 +755,25 @@ int launch_skinny(const LinArgs& a, const float* c1, bool ln, int S, unsigned* c
   SKV_SK(3) SKV_SK(4) SKV_SK(6) SKV_SK(8) SKV_SK(12)
 #undef SKV_SK
   return check_launch("skv_linear");
+}
+
+// skv_linear_pack: float4 p of the packed copy is lane l = p % 64 of 16-k
+// step s = (p / 64) % (K / 16) of tile t = p / (64 K / 16): w[16 t + l % 16,
+// 16 s + 4 (l / 16) .. + 3], zero past row N.
+__global__ __launch_bounds__(256) void k_pack_mfma(float* __restrict__ wp,
+                                                   const float* __restrict__ w, int N, int K,
+                                                   size_t total4) {
+  const size_t p = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= total4) return;
+  const int l = (int)(p & 63);
+  const size_t ts = p >> 6;
+  const int steps = K / 16;
+  const int s = (int)(ts % steps);
+  const size_t t = ts / steps;
+  const size_t n = t * 16 + (l & 15);
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (n < (size_t)N) v = *reinterpret_cast<const float4*>(w + n * K + 16 * s + 4 * (l >> 4));
+  *reinterpret_cast<float4*>(wp + p * 4) = v;
 }
 
 // LayerNorm folding for k_linear_skinny: one workgroup per weight row n,
@@ -1110,6 +1149,68 @@ extern "C" int skv_linear_folded(float* y, const float* x, const float* w_fold, 
   LinArgs a{y, x, w_fold, c2, residual, nullptr, nullptr, ln_eps, M, N, K, activation,
             split_cols, K, nullptr};
   return launch_skinny(a, c1, true, 1, nullptr, (hipStream_t)stream);
+}
+
+extern "C" size_t skv_linear_packed_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 16) return 0;
+  return (size_t)((N + 15) / 16) * 16 * K * sizeof(float);
+}
+
+extern "C" int skv_linear_pack(float* w_packed, const float* w_t, int N, int K,
+                               skv_stream_t stream) {
+  SKV_REQUIRE(w_packed && w_t, SKV_E_INVALID, "skv_linear_pack: null pointer argument");
+  SKV_REQUIRE(N > 0 && K > 0 && K % 16 == 0, SKV_E_INVALID,
+              "skv_linear_pack: N=%d, K=%d (K must be a positive multiple of 16)", N, K);
+  const size_t total4 = skv_linear_packed_bytes(N, K) / 16;
+  hipLaunchKernelGGL(k_pack_mfma, dim3((unsigned)((total4 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, w_packed, w_t, N, K, total4);
+  return check_launch("skv_linear_pack");
+}
+
+extern "C" int skv_linear_packed(float* y, const float* x, const float* w_packed,
+                                 const float* bias, const float* residual, int M, int N, int K,
+                                 int activation, skv_stream_t stream) {
+  SKV_REQUIRE(y && x && w_packed, SKV_E_INVALID, "skv_linear_packed: null pointer argument");
+  SKV_REQUIRE(M > 0 && N > 0 && K > 0, SKV_E_INVALID, "skv_linear_packed: dims must be > 0");
+  SKV_REQUIRE(activation == 0 || activation == 1, SKV_E_INVALID,
+              "skv_linear_packed: bad activation");
+  const int col_tiles = (N + 15) / 16;
+  const int per_wg = (col_tiles + kNumCUs - 1) / kNumCUs;
+  const int us = K / 64;
+  SKV_REQUIRE(M <= 16 && K % 64 == 0 && (us == 8 || us == 12 || us == 16) &&
+                  col_tiles >= 1024 && per_wg <= kWideMaxTiles,
+              SKV_E_UNSUPPORTED,
+              "skv_linear_packed: M=%d N=%d K=%d (needs M <= 16, K in {512, 768, 1024}, "
+              "16384 <= N <= 65536)", M, N, K);
+  LinArgs a{y, x, w_packed, bias, residual, nullptr, nullptr, 0.f, M, N, K, activation, 0, K,
+            nullptr};
+  hipStream_t s = (hipStream_t)stream;
+  // 16 wavefronts of K / 128 float4 a unit (eighths of a tile) where their
+  // partials fit LDS beside x: a cold 154.5 MB stream measured 25.5 us at 16
+  // wavefronts x 6 loads against 27.2 us at 8 x 12 on MI355X; else 8
+  // wavefronts of quarters.
+  const size_t x_lds = (size_t)16 * (K + 4) * sizeof(float);
+  const size_t lds16 = x_lds + (size_t)per_wg * 8 * 64 * 4 * sizeof(float);
+  const size_t lds8 = x_lds + (size_t)per_wg * 4 * 64 * 4 * sizeof(float);
+  if (lds16 <= 160 * 1024) {
+#define SKV_PK16(U)                                                                             \
+  hipLaunchKernelGGL((k_linear_wide<U, false, true, 16>), dim3(kNumCUs), dim3(16 * 64), lds16, s, \
+                     a, col_tiles)
+    if (K == 512) SKV_PK16(4);
+    else if (K == 768) SKV_PK16(6);
+    else SKV_PK16(8);
+#undef SKV_PK16
+  } else if (us == 8) {
+    hipLaunchKernelGGL((k_linear_wide<8, false, true>), dim3(kNumCUs), dim3(kWideWaves * 64), lds8,
+                       s, a, col_tiles);
+  } else if (us == 12) {
+    hipLaunchKernelGGL((k_linear_wide<12, false, true>), dim3(kNumCUs), dim3(kWideWaves * 64),
+                       lds8, s, a, col_tiles);
+  } else {
+    hipLaunchKernelGGL((k_linear_wide<16, false, true>), dim3(kNumCUs), dim3(kWideWaves * 64),
+                       lds8, s, a, col_tiles);
+  }
+  return check_launch("skv_linear_packed");
 }
 
 extern "C" size_t skv_argmax_workspace_bytes(int M, int N) {

@@ -285,6 +285,24 @@ class TransformerModel:
             self._bufs[key] = out
         return self._bufs[key]
 
+    def _packed_logits(self):
+        """The tied output projection in skv_linear_pack's lane order (made
+        once), or None when skv_linear_packed does not take the sizes
+        (K in {512, 768, 1024}, 16384 <= vocab <= 65536)."""
+        key = "packed_logits"
+        if key not in self._bufs:
+            V, d = self.emb.shape
+            ok = d in (512, 768, 1024) and 16384 <= V <= 65536
+            wp = None
+            if ok:
+                L = _lib.lib()
+                wp = torch.empty(L.skv_linear_packed_bytes(V, d) // 4, device=self.emb.device)
+                _lib.check(L.skv_linear_pack(wp.data_ptr(), self.emb.data_ptr(), V, d,
+                                             _lib.stream_handle(self.ctx.device)),
+                           "skv_linear_pack")
+            self._bufs[key] = wp
+        return self._bufs[key]
+
     def _launch_step(self, cache: KVCache, bf: _Buffers) -> None:
         L = _lib.lib()
         tm = self.tm_params
@@ -334,8 +352,13 @@ class TransformerModel:
                                  self.mlp_dim, d, 1, 0, lw_ws, lw_n, s), "skv_linear")
             chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, None, None, 0.0,
                              B, d, self.mlp_dim, 0, 0, lw_ws, lw_n, s), "skv_linear")
-        chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, None, None,
-                         0.0, B, tm.vocab_size, d, 0, 0, lw_ws, lw_n, s), "skv_linear")
+        packed = self._packed_logits() if B <= 16 else None
+        if packed is not None:
+            chk(L.skv_linear_packed(bf.logits.data_ptr(), x, packed.data_ptr(), None, None, B,
+                                    tm.vocab_size, d, 0, s), "skv_linear_packed")
+        else:
+            chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, None,
+                             None, 0.0, B, tm.vocab_size, d, 0, 0, lw_ws, lw_n, s), "skv_linear")
 
     # -- many steps ----------------------------------------------------------
 

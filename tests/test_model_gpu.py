@@ -149,6 +149,53 @@ def test_linear_split_shapes_share_workspace(gpu_ctx):
             assert err < FP32_TOL
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 50304, 768), (1, 20000, 512), (9, 16400, 1024),
+                                   (16, 65536, 768)])
+def test_linear_packed_matches_unpacked(gpu_ctx, M, N, K):
+    """skv_linear_pack + skv_linear_packed: the lane-ordered copy gives what
+    skv_linear gives on the [N, K] weights (within fp32 rounding: the K
+    parts are summed in another fixed order) and float64 numpy; bias, GELU
+    and residual included; a second call gives the same bits."""
+    banner(f"linear packed M={M} N={N} K={K}")
+    _lib = lib()
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    r = np.random.default_rng(M + N + K)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    w = (r.standard_normal((N, K)) * 0.05).astype(np.float32)
+    b = r.standard_normal(N).astype(np.float32)
+    res = r.standard_normal((M, N)).astype(np.float32)
+    xd, wd, bd, rd = dev(x), dev(w), dev(b), dev(res)
+    nb = L.skv_linear_packed_bytes(N, K)
+    assert nb == ((N + 15) // 16) * 16 * K * 4
+    wp = torch.full((nb // 4,), float("nan"), device="cuda")
+    _lib.check(L.skv_linear_pack(wp.data_ptr(), wd.data_ptr(), N, K, s), "pack")
+    for act, use_bias, use_res in ((0, False, False), (1, True, False), (0, True, True)):
+        y1 = torch.empty((M, N), device="cuda")
+        y2 = torch.empty((M, N), device="cuda")
+        args = (bd.data_ptr() if use_bias else None, rd.data_ptr() if use_res else None)
+        _lib.check(L.skv_linear(y1.data_ptr(), xd.data_ptr(), wd.data_ptr(), args[0], args[1],
+                                None, None, 0.0, M, N, K, act, 0, None, 0, s), "skv_linear")
+        _lib.check(L.skv_linear_packed(y2.data_ptr(), xd.data_ptr(), wp.data_ptr(), args[0],
+                                       args[1], M, N, K, act, s), "skv_linear_packed")
+        y3 = torch.empty_like(y2)
+        _lib.check(L.skv_linear_packed(y3.data_ptr(), xd.data_ptr(), wp.data_ptr(), args[0],
+                                       args[1], M, N, K, act, s), "skv_linear_packed")
+        assert torch.equal(y2, y3)
+        assert rel_rows(y2.cpu().numpy(), y1.cpu().numpy()) < 1e-6
+        want = x.astype(np.float64) @ w.T.astype(np.float64) + (b if use_bias else 0)
+        if act:
+            want = mo.gelu_tanh(want)
+        if use_res:
+            want = want + res
+        assert rel_rows(y2.cpu().numpy(), want) < FP32_TOL
+    # sizes the kernel does not take
+    assert L.skv_linear_packed(y2.data_ptr(), xd.data_ptr(), wp.data_ptr(), None, None, 17, N, K,
+                               0, s) != 0
+    assert L.skv_linear_packed(y2.data_ptr(), xd.data_ptr(), wp.data_ptr(), None, None, M, 1000,
+                               K, 0, s) != 0
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 256, 768), (16, 2304, 768), (16, 3072, 768),
                                    (7, 1000, 1024), (16, 96, 3072), (3, 2304, 256)])
 def test_linear_folded_matches_numpy(gpu_ctx, M, N, K):
