@@ -141,12 +141,19 @@ void launch_partial(const DecodeArgs& a, hipStream_t s) {
   // 4 x 16 B for bf16 D=128 without GQA, which the plan runs at one
   // workgroup per CU on long streams: C4 158.8 -> 155.5 us per call on
   // MI355X (8 tokens in flight: 82.9% of 8 TB/s, 4: 84.6%).
+  // Without GQA at D = 64 (C2, C3: short pieces of 32-token chunks) groups of
+  // 4 tokens with the prefetching loop, for both cache types: against 8-token
+  // groups (prefetching fp32, single-set bf16), C3 598.5 against 605.1 us per
+  // step with the fp32 cache and 543.3 against 545.1 with bf16, C2 19.6
+  // against 20.1 us per call (two rounds on one MI355X); 2-token groups and
+  // 16-token groups were slower.
+  constexpr bool kMha64 = D == 64 && G == 1;
   constexpr bool kMhaBf16 = sizeof(TC) == 2 && D == 128 && G == 1;
-  constexpr int TPG = ((sizeof(TC) == 4 && D == 128) || kMhaBf16) ? 4 : 8;
+  constexpr int TPG = ((sizeof(TC) == 4 && D == 128) || kMhaBf16 || kMha64) ? 4 : 8;
   // Load prefetch across token groups (a second register set) for fp32
   // caches without GQA: C2/C3 measured 2-3 % faster per call on MI355X; the
   // bf16 C4 case measured 1 % slower (occupancy 4 -> 2), so it keeps one set.
-  constexpr bool PF = G == 1 && sizeof(TC) == 4;
+  constexpr bool PF = (G == 1 && sizeof(TC) == 4) || kMha64;
   launch_partial_t<TC, D, G, TPG, PAGED, PF, 1, false>(a, s);
 }
 

@@ -46,16 +46,18 @@ def _gpu():
 # decode attention
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("D", HEAD_DIMS)
-@pytest.mark.parametrize("Hq,Hkv,dtype,paged", [
+_DECODE_LAYOUTS = [
     (6, 6, torch.float32, False),
     (8, 2, torch.bfloat16, True),    # G = 4 over a paged cache
-    (8, 1, torch.bfloat16, False),   # G = 8 (head dims up to 128)
+    (8, 1, torch.bfloat16, False),   # G = 8 (head dims up to 128: register budget)
     (3, 3, torch.float32, True),
-])
+]
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,dtype,paged", [
+    (D, *lay) for lay in _DECODE_LAYOUTS for D in HEAD_DIMS
+    if not (lay[0] // lay[1] == 8 and D > 128)])
 def test_decode_any_head_dim(gpu_ctx, D, Hq, Hkv, dtype, paged):
-    if Hq // Hkv == 8 and D > 128:
-        pytest.skip("G = 8 takes head dims up to 128 (register budget); this size has no kernel")
     banner(f"decode D={D} Hq={Hq} Hkv={Hkv} {dtype} paged={paged}")
     gpu = _gpu()
     rng = np.random.default_rng(D * 10 + Hq)
@@ -70,6 +72,20 @@ def test_decode_any_head_dim(gpu_ctx, D, Hq, Hkv, dtype, paged):
     assert err < FP32_TOL
     np.testing.assert_array_equal(got[1], np.broadcast_to(
         np.repeat(v[1, 0], Hq // Hkv, axis=0), got[1].shape))  # one token: its value row
+
+
+@pytest.mark.parametrize("D", [d for d in HEAD_DIMS if d > 128])
+def test_decode_g8_rejects_head_dims_past_128(gpu_ctx, D):
+    """G = 8 has kernels for head dims up to 128 only: larger ones raise
+    ValueError (SKV_E_UNSUPPORTED) instead of launching."""
+    gpu = _gpu()
+    rng = np.random.default_rng(D)
+    B, T = 2, 64
+    lens = np.array([T, 5])
+    cache, _, _, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, 8, 1, D, torch.bfloat16, lens, False)
+    q = rng.standard_normal((B, 8, D)).astype(np.float32)
+    with pytest.raises(ValueError):
+        _decode(gpu, gpu_ctx, cache, q)
 
 
 def test_decode_g8_above_128_is_rejected(gpu_ctx):
