@@ -319,10 +319,13 @@ int skv_linear_pack(float* w_packed, const float* w_t, int N, int K, skv_stream_
  * K in {512, 768, 1024}, 16384 <= N <= 65536; otherwise SKV_E_UNSUPPORTED.
  * Every 16-k step of a tile is 1 KB of consecutive bytes, streamed by 16
  * wavefronts per CU; sums run in a fixed order (its own, so the bits may
- * differ from skv_linear's within fp32 rounding). */
+ * differ from skv_linear's within fp32 rounding). argmax_cand (may be NULL;
+ * skv_linear_packed_cand_bytes(M) bytes): each of the 256 workgroups also
+ * writes, per row, the first maximum of y over its columns (value, column),
+ * the first step of the argmax that skv_next_embed finishes. */
 int skv_linear_packed(float* y, const float* x, const float* w_packed, const float* bias,
                       const float* residual, int M, int N, int K, int activation,
-                      skv_stream_t stream);
+                      float* argmax_cand, skv_stream_t stream);
 
 /* Workspace skv_linear can use for these sizes: the split-K partials (and
  * arrival counters) of a narrow projection of at most 64 rows (0: it never
@@ -378,6 +381,25 @@ int skv_sample(int32_t* out, float* probs_out, const float* logits, const int32_
 int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                     const int32_t* prompt, const int32_t* prompt_len, const int32_t* pos, int B,
                     int max_prompt, int seq_cap, skv_stream_t stream);
+
+/* Bytes of skv_linear_packed's argmax candidates for M rows: [M][256]
+ * float values, then [M][256] int32 columns. */
+size_t skv_linear_packed_cand_bytes(int M);
+
+/* skv_next_tokens and skv_embed in one launch, ending the argmax: with
+ * n_cand > 0 the previous token of row b is the first maximum over its
+ * n_cand candidates (cand: [B][n_cand] float values, then [B][n_cand] int32
+ * columns, as skv_linear_packed writes them; a row of NaN only gives token
+ * 0), else argmax_prev[b]. Then ids[b] and seq as skv_next_tokens, and, when
+ * embedding is not NULL, x[b, :] = embedding[ids[b], :] + pos_table[pos[b], :]
+ * as skv_embed (ids and positions clamped into the tables). No counterpart
+ * in the reference, whose generate loop picks and embeds on the host side
+ * (generate.py:29-69, jax_backend.py:144, 466-469). */
+int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
+                   const float* cand, int n_cand, const int32_t* prompt,
+                   const int32_t* prompt_len, const int32_t* pos, int B, int max_prompt,
+                   int seq_cap, const float* embedding, const float* pos_table, int d, int vocab,
+                   int ctx, skv_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Training-side attention in fp32: causal FlashAttention forward and backward.

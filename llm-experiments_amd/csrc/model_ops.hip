@@ -106,6 +106,15 @@ __device__ __forceinline__ float gelu_tanh(float v) {
   return 0.5f * v * (1.f + tanhf(k0 * (v + 0.044715f * v * v * v)));
 }
 
+// argmax step: (v, i) replaces the best (bv, bi) if v is larger, or equal
+// with a smaller index (the first maximum wins; NaN never does)
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
 struct LinArgs {
   float* y;
   const float* x;
@@ -120,6 +129,7 @@ struct LinArgs {
   int split;    // > 0: column n goes to segment n / split of a [N/split][M][split] output
   int kz;       // K range of one workgroup along grid z (a multiple of 16; K when unsplit)
   float* part;  // split K: raw partial sums [grid z][M][N]; the reduce pass finishes them
+  float* cand;  // k_linear_wide: per-row argmax candidates [M][grid] values, then indices
 };
 
 // Lane layout of v_mfma_f32_16x16x4_f32: operand A lane l holds
@@ -527,7 +537,13 @@ void k_linear_wide(LinArgs a, int tiles_total) {
   }
   if (k < nk) compute(k, wa);
   __syncthreads();
-  // epilogue: tile j by wavefront j % NW; slot i of lane l is row 4 lk + i, column lr
+  // epilogue: tile j by wavefront j % NW; slot i of lane l is row 4 lk + i, column lr.
+  // With a.cand (PACKED only) each row's first maximum over this workgroup's
+  // columns is tracked as well: per lane, then over the 16 columns of a lane
+  // group, then over the wavefronts in LDS, in an order-independent way
+  // (larger value, or equal value and smaller column).
+  float cbv[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  int cbi[4] = {a.N, a.N, a.N, a.N};
   for (int j = wave; j < nt; j += NW) {
     const int n = (t0 + j) * 16 + lr;
     if (n >= a.N) continue;
@@ -544,6 +560,34 @@ void k_linear_wide(LinArgs a, int tiles_total) {
       if (a.act == 1) y = gelu_tanh(y);
       if (a.res) y += a.res[(size_t)m * a.N + n];
       a.y[(size_t)m * a.N + n] = y;
+      if constexpr (PACKED) better(cbv[i], cbi[i], y, n);
+    }
+  }
+  if constexpr (PACKED) {
+    if (a.cand == nullptr) return;  // uniform
+    __shared__ float s_cv[NW][16];
+    __shared__ int s_ci[NW][16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) {  // the 16 columns of a lane group
+        const float ov = __shfl_xor(cbv[i], o);
+        const int oi = __shfl_xor(cbi[i], o);
+        better(cbv[i], cbi[i], ov, oi);
+      }
+      if (lr == 0) {
+        s_cv[wave][4 * lk + i] = cbv[i];
+        s_ci[wave][4 * lk + i] = cbi[i];
+      }
+    }
+    __syncthreads();
+    if (tid < M) {
+      float bv = -INFINITY;
+      int bi = a.N;
+      for (int w = 0; w < NW; ++w) better(bv, bi, s_cv[w][tid], s_ci[w][tid]);
+      const int G = gridDim.x;
+      a.cand[(size_t)tid * G + blockIdx.x] = bv;
+      reinterpret_cast<int*>(a.cand + (size_t)M * G)[(size_t)tid * G + blockIdx.x] = bi;
     }
   }
 }
@@ -848,13 +892,6 @@ int linear_splits(int M, int N, int K) {
 // ---------------------------------------------------------------------------
 // argmax over each row (first index on ties), one workgroup per row
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
-  if (v > bv || (v == bv && i < bi)) {
-    bv = v;
-    bi = i;
-  }
-}
-
 constexpr int kArgCols = 2048;  // columns per argmax workgroup (8 per thread)
 
 __device__ __forceinline__ void block_better(float& bv, int& bi) {
@@ -941,6 +978,54 @@ __global__ void k_next_tokens(int32_t* __restrict__ ids, int32_t* __restrict__ s
   else t = argmax_prev[b];
   ids[b] = t;
   if (p >= 0 && p < seq_cap) seq[(size_t)b * seq_cap + p] = t;
+}
+
+// k_next_tokens and k_embed in one launch, with the argmax's last step: row
+// b picks the first maximum over its n_cand (value, column) candidates (one
+// wavefront), or reads argmax_prev[b] when n_cand is 0, applies the
+// next-token rule above, records the token, and writes x[b] = embedding[t] +
+// pos_table[pos] (no x when the embedding is null).
+__global__ __launch_bounds__(256) void k_next_embed(
+    float* __restrict__ x, int32_t* __restrict__ ids, int32_t* __restrict__ seq,
+    const int32_t* __restrict__ argmax_prev, const float* __restrict__ cand, int n_cand,
+    const int32_t* __restrict__ prompt, const int32_t* __restrict__ prompt_len,
+    const int32_t* __restrict__ pos, int B, int max_prompt, int seq_cap,
+    const float* __restrict__ emb, const float* __restrict__ pe, int d, int vocab, int ctx) {
+  __shared__ int s_t;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int p = pos[b];
+  if (tid < 64) {
+    int t;
+    if (p < prompt_len[b]) {
+      t = prompt[(size_t)b * max_prompt + min(max(p, 0), max_prompt - 1)];
+    } else if (n_cand > 0) {
+      const float* cv = cand + (size_t)b * n_cand;
+      const int* ci = reinterpret_cast<const int*>(cand + (size_t)B * n_cand) + (size_t)b * n_cand;
+      float bv = -INFINITY;
+      int bi = vocab;
+      for (int k = tid; k < n_cand; k += 64) better(bv, bi, cv[k], ci[k]);
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        better(bv, bi, ov, oi);
+      }
+      t = bi < vocab ? bi : 0;  // a row of NaN only: token 0
+    } else {
+      t = argmax_prev[b];
+    }
+    if (tid == 0) {
+      ids[b] = t;
+      if (p >= 0 && p < seq_cap) seq[(size_t)b * seq_cap + p] = t;
+      s_t = t;
+    }
+  }
+  if (emb == nullptr) return;  // uniform
+  __syncthreads();
+  const int id = min(max(s_t, 0), vocab - 1);
+  const int pp = min(max(p, 0), ctx - 1);
+  for (int j = tid; j < d; j += blockDim.x)
+    x[(size_t)b * d + j] = emb[(size_t)id * d + j] + pe[(size_t)pp * d + j];
 }
 
 // y[m, :] = x[rows[m], :]; rows are clamped into [0, n_rows).
@@ -1169,7 +1254,7 @@ extern "C" int skv_linear_pack(float* w_packed, const float* w_t, int N, int K,
 
 extern "C" int skv_linear_packed(float* y, const float* x, const float* w_packed,
                                  const float* bias, const float* residual, int M, int N, int K,
-                                 int activation, skv_stream_t stream) {
+                                 int activation, float* argmax_cand, skv_stream_t stream) {
   SKV_REQUIRE(y && x && w_packed, SKV_E_INVALID, "skv_linear_packed: null pointer argument");
   SKV_REQUIRE(M > 0 && N > 0 && K > 0, SKV_E_INVALID, "skv_linear_packed: dims must be > 0");
   SKV_REQUIRE(activation == 0 || activation == 1, SKV_E_INVALID,
@@ -1183,7 +1268,7 @@ extern "C" int skv_linear_packed(float* y, const float* x, const float* w_packed
               "skv_linear_packed: M=%d N=%d K=%d (needs M <= 16, K in {512, 768, 1024}, "
               "16384 <= N <= 65536)", M, N, K);
   LinArgs a{y, x, w_packed, bias, residual, nullptr, nullptr, 0.f, M, N, K, activation, 0, K,
-            nullptr};
+            nullptr, argmax_cand};
   hipStream_t s = (hipStream_t)stream;
   // 16 wavefronts of K / 128 float4 a unit (eighths of a tile) where their
   // partials fit LDS beside x: a cold 154.5 MB stream measured 25.5 us at 16
@@ -1233,6 +1318,30 @@ extern "C" int skv_argmax(int32_t* out, const float* x, int M, int N, void* ws, 
   hipLaunchKernelGGL(k_argmax, dim3(ns, M), dim3(256), 0, s, out, x, N, cv, ci);
   if (ns > 1) hipLaunchKernelGGL(k_argmax_pick, dim3(M), dim3(64), 0, s, out, cv, ci, ns, N);
   return check_launch("skv_argmax");
+}
+
+extern "C" size_t skv_linear_packed_cand_bytes(int M) {
+  return M > 0 ? (size_t)M * kNumCUs * 8 : 0;
+}
+
+extern "C" int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
+                              const float* cand, int n_cand, const int32_t* prompt,
+                              const int32_t* prompt_len, const int32_t* pos, int B,
+                              int max_prompt, int seq_cap, const float* embedding,
+                              const float* pos_table, int d, int vocab, int ctx,
+                              skv_stream_t stream) {
+  SKV_REQUIRE(ids && seq && prompt && prompt_len && pos, SKV_E_INVALID,
+              "skv_next_embed: null pointer argument");
+  SKV_REQUIRE(B > 0 && max_prompt > 0 && seq_cap > 0 && vocab > 0 && n_cand >= 0, SKV_E_INVALID,
+              "skv_next_embed: bad sizes");
+  SKV_REQUIRE(n_cand > 0 ? cand != nullptr : argmax_prev != nullptr, SKV_E_INVALID,
+              "skv_next_embed: candidates or the previous argmax needed");
+  SKV_REQUIRE(embedding == nullptr || (x && pos_table && d > 0 && ctx > 0), SKV_E_INVALID,
+              "skv_next_embed: embedding needs x, pos_table, d and ctx");
+  hipLaunchKernelGGL(k_next_embed, dim3(B), dim3(256), 0, (hipStream_t)stream, x, ids, seq,
+                     argmax_prev, cand, n_cand, prompt, prompt_len, pos, B, max_prompt, seq_cap,
+                     embedding, pos_table, d, vocab, ctx);
+  return check_launch("skv_next_embed");
 }
 
 extern "C" int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,

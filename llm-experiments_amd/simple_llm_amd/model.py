@@ -127,6 +127,10 @@ class _Buffers:
         lin = max(L.skv_linear_workspace_bytes(B, n, k)
                   for n, k in ((3 * d, d), (d, d), (mlp, d), (d, mlp), (vocab, d)))
         self.lin_ws = torch.zeros(max(lin, 4), dtype=torch.uint8, device=dev)
+        # per-row argmax candidates of the packed logits projection (the
+        # step's argmax, finished by skv_next_embed)
+        self.cand = torch.zeros(max(L.skv_linear_packed_cand_bytes(B) // 4, 1), device=dev)
+        self.n_cand = L.skv_linear_packed_cand_bytes(B) // (8 * B)
 
 
 class _PrefillBuffers:
@@ -303,7 +307,11 @@ class TransformerModel:
             self._bufs[key] = wp
         return self._bufs[key]
 
-    def _launch_step(self, cache: KVCache, bf: _Buffers) -> None:
+    def _launch_step(self, cache: KVCache, bf: _Buffers, fused: bool = False) -> None:
+        """One decode step's launches. fused: x already holds the step's input
+        rows (skv_next_embed ran), and the packed logits projection also
+        writes the argmax candidates into bf.cand (skv_next_embed finishes
+        them at the next step); needs _packed_logits() and B <= 16."""
         L = _lib.lib()
         tm = self.tm_params
         B, d, H, D, T = cache.batch_size, tm.embedding_dim, tm.n_heads, self.head_dim, \
@@ -320,8 +328,9 @@ class TransformerModel:
         lens0 = cache.layers[0].lens.data_ptr()
         # up to 16 rows: LayerNorm folded into the weights (skv_linear_folded)
         folded = self._folded() if B <= 16 else None
-        chk(L.skv_embed(x, bf.ids.data_ptr(), lens0, self.emb.data_ptr(), self.pe.data_ptr(), B, d,
-                        tm.vocab_size, self.pe.shape[0], s), "skv_embed")
+        if not fused:
+            chk(L.skv_embed(x, bf.ids.data_ptr(), lens0, self.emb.data_ptr(), self.pe.data_ptr(),
+                            B, d, tm.vocab_size, self.pe.shape[0], s), "skv_embed")
         for li, (lw, layer) in enumerate(zip(self.layers, cache.layers)):
             kc, vc = layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr()
             # q, k, v = LN1(x) . [Wq Wk Wv] (LayerNorm folded into the projection)
@@ -353,9 +362,12 @@ class TransformerModel:
             chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, None, None, 0.0,
                              B, d, self.mlp_dim, 0, 0, lw_ws, lw_n, s), "skv_linear")
         packed = self._packed_logits() if B <= 16 else None
+        if fused and packed is None:
+            raise ValueError("the fused step needs the packed logits projection")
         if packed is not None:
             chk(L.skv_linear_packed(bf.logits.data_ptr(), x, packed.data_ptr(), None, None, B,
-                                    tm.vocab_size, d, 0, s), "skv_linear_packed")
+                                    tm.vocab_size, d, 0, bf.cand.data_ptr() if fused else None,
+                                    s), "skv_linear_packed")
         else:
             chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, None,
                              None, 0.0, B, tm.vocab_size, d, 0, 0, lw_ws, lw_n, s), "skv_linear")
@@ -508,7 +520,7 @@ class Generator:
                  total_len: Sequence[int] | int, use_graph: bool = False,
                  temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
                  min_p: float = 0.0, repetition_penalty: float = 1.0,
-                 repetition_window: int = 64, seed: int = 42):
+                 repetition_window: int = 64, seed: int = 42, fused_tail: bool = True):
         tm = model.tm_params
         self.model = model
         B = len(prompts)
@@ -553,6 +565,12 @@ class Generator:
         self.seed = int(seed) & ((1 << 64) - 1)
         # greedy without a penalty takes the multi-workgroup argmax
         self.greedy = temperature == 0.0 and repetition_penalty == 1.0
+        # greedy up to 16 rows with the packed logits: the logits projection
+        # leaves per-workgroup argmax candidates and skv_next_embed finishes
+        # the argmax, picks the next input token and embeds it (one launch
+        # for skv_argmax's two, skv_next_tokens and skv_embed)
+        self.fused = bool(fused_tail) and self.greedy and B <= 16 and \
+            model._packed_logits() is not None
         self.reset()
 
     def reset(self) -> None:
@@ -562,6 +580,26 @@ class Generator:
         self.seq.zero_()
         self.seq[:, :self.prompt.shape[1]].copy_(self.prompt)
         self.bufs.argmax.zero_()
+        # the fused tail reads the previous step's candidates, or the
+        # prefill's argmax before the first step
+        self._cand_ready = False
+
+    def _next_embed(self, embed: bool) -> None:
+        """skv_next_embed: the previous token from the candidates (after a
+        fused step) or from argmax (after the prefill), recorded in seq,
+        embedded into x when embed."""
+        L = _lib.lib()
+        m, c, bf = self.model, self.cache, self.bufs
+        s = _lib.stream_handle(m.ctx.device)
+        tm = m.tm_params
+        _lib.check(L.skv_next_embed(bf.x.data_ptr() if embed else None, bf.ids.data_ptr(),
+                                    self.seq.data_ptr(), bf.argmax.data_ptr(),
+                                    bf.cand.data_ptr(), bf.n_cand if self._cand_ready else 0,
+                                    self.prompt.data_ptr(), self.prompt_len.data_ptr(),
+                                    c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
+                                    self.seq.shape[1], m.emb.data_ptr() if embed else None,
+                                    m.pe.data_ptr() if embed else None, tm.embedding_dim,
+                                    tm.vocab_size, m.pe.shape[0], s), "skv_next_embed")
 
     def _pick(self) -> None:
         """Next token of every sequence from the logits buffer into argmax."""
@@ -587,6 +625,11 @@ class Generator:
         L = _lib.lib()
         m, c, bf = self.model, self.cache, self.bufs
         s = _lib.stream_handle(m.ctx.device)
+        if self.fused:
+            self._next_embed(embed=True)
+            m._launch_step(c, bf, fused=True)
+            self._cand_ready = True
+            return
         _lib.check(L.skv_next_tokens(bf.ids.data_ptr(), self.seq.data_ptr(), bf.argmax.data_ptr(),
                                      self.prompt.data_ptr(), self.prompt_len.data_ptr(),
                                      c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
@@ -623,12 +666,15 @@ class Generator:
         # record the last new token at its position
         L = _lib.lib()
         s = _lib.stream_handle(self.model.ctx.device)
-        _lib.check(L.skv_next_tokens(self.bufs.ids.data_ptr(), self.seq.data_ptr(),
-                                     self.bufs.argmax.data_ptr(), self.prompt.data_ptr(),
-                                     self.prompt_len.data_ptr(),
-                                     self.cache.layers[0].lens.data_ptr(), self.B,
-                                     self.prompt.shape[1], self.seq.shape[1], s),
-                   "skv_next_tokens")
+        if self.fused:
+            self._next_embed(embed=False)
+        else:
+            _lib.check(L.skv_next_tokens(self.bufs.ids.data_ptr(), self.seq.data_ptr(),
+                                         self.bufs.argmax.data_ptr(), self.prompt.data_ptr(),
+                                         self.prompt_len.data_ptr(),
+                                         self.cache.layers[0].lens.data_ptr(), self.B,
+                                         self.prompt.shape[1], self.seq.shape[1], s),
+                       "skv_next_tokens")
         for layer in self.cache.layers:
             layer.host_lens = layer.lens.cpu().numpy().astype(np.int64)
         seq = self.seq.cpu().numpy()

@@ -177,10 +177,10 @@ def test_linear_packed_matches_unpacked(gpu_ctx, M, N, K):
         _lib.check(L.skv_linear(y1.data_ptr(), xd.data_ptr(), wd.data_ptr(), args[0], args[1],
                                 None, None, 0.0, M, N, K, act, 0, None, 0, s), "skv_linear")
         _lib.check(L.skv_linear_packed(y2.data_ptr(), xd.data_ptr(), wp.data_ptr(), args[0],
-                                       args[1], M, N, K, act, s), "skv_linear_packed")
+                                       args[1], M, N, K, act, None, s), "skv_linear_packed")
         y3 = torch.empty_like(y2)
         _lib.check(L.skv_linear_packed(y3.data_ptr(), xd.data_ptr(), wp.data_ptr(), args[0],
-                                       args[1], M, N, K, act, s), "skv_linear_packed")
+                                       args[1], M, N, K, act, None, s), "skv_linear_packed")
         assert torch.equal(y2, y3)
         assert rel_rows(y2.cpu().numpy(), y1.cpu().numpy()) < 1e-6
         want = x.astype(np.float64) @ w.T.astype(np.float64) + (b if use_bias else 0)
@@ -191,9 +191,86 @@ def test_linear_packed_matches_unpacked(gpu_ctx, M, N, K):
         assert rel_rows(y2.cpu().numpy(), want) < FP32_TOL
     # sizes the kernel does not take
     assert L.skv_linear_packed(y2.data_ptr(), xd.data_ptr(), wp.data_ptr(), None, None, 17, N, K,
-                               0, s) != 0
+                               0, None, s) != 0
     assert L.skv_linear_packed(y2.data_ptr(), xd.data_ptr(), wp.data_ptr(), None, None, M, 1000,
-                               K, 0, s) != 0
+                               K, 0, None, s) != 0
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 50304, 768), (3, 16400, 512)])
+def test_packed_argmax_candidates_and_next_embed(gpu_ctx, M, N, K):
+    """The packed logits' per-workgroup argmax candidates, finished by
+    skv_next_embed, give numpy's first argmax of every row (rows with exact
+    ties placed in different workgroups' column ranges, a row of one NaN
+    column, a row with its maximum in the last column), the token goes to
+    ids and seq, and x gets the embedding + position row; rows inside their
+    prompt take the prompt token; with n_cand = 0 the previous argmax
+    buffer is used; without an embedding only ids and seq are written."""
+    banner(f"packed argmax candidates M={M} N={N} K={K}")
+    _lib = lib()
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    r = np.random.default_rng(N + M)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    w = (r.standard_normal((N, K)) * 0.05).astype(np.float32)
+    # columns 5 and N - 3: the same weights and a +100 bias, so every row has
+    # an exact tie at its top (workgroups 0 and 255 hold them: the first
+    # wins); row 1: a larger value in the last column; row 2: a NaN column
+    w[N - 3] = w[5]
+    bias = np.zeros(N, np.float32)
+    bias[5] = bias[N - 3] = 100.0
+    res = np.zeros((M, N), np.float32)
+    if M > 1:
+        res[1, N - 1] = 1000.0
+    if M > 2:
+        res[2, 7] = np.nan
+    xd, wd, biasd, resd = dev(x), dev(w), dev(bias), dev(res)
+    wp = torch.empty(L.skv_linear_packed_bytes(N, K) // 4, device="cuda")
+    _lib.check(L.skv_linear_pack(wp.data_ptr(), wd.data_ptr(), N, K, s), "pack")
+    y = torch.empty((M, N), device="cuda")
+    cand = torch.full((L.skv_linear_packed_cand_bytes(M) // 4,), float("nan"), device="cuda")
+    n_cand = L.skv_linear_packed_cand_bytes(M) // (8 * M)
+    assert n_cand == 256
+    _lib.check(L.skv_linear_packed(y.data_ptr(), xd.data_ptr(), wp.data_ptr(), biasd.data_ptr(),
+                                   resd.data_ptr(), M, N, K, 0, cand.data_ptr(), s),
+               "skv_linear_packed")
+    yh = y.cpu().numpy()
+    assert yh[0, 5] == yh[0, N - 3]
+    want = np.array([int(np.nanargmax(row)) for row in yh])  # NaN never wins
+    assert want[0] == 5
+    if M > 1:
+        assert want[1] == N - 1
+    D, V, T = 64, N, 40
+    emb = r.standard_normal((V, D)).astype(np.float32)
+    pe = r.standard_normal((T, D)).astype(np.float32)
+    pos = np.array([(b % 3) + 1 for b in range(M)], np.int32)
+    plen = np.zeros(M, np.int32)
+    plen[M - 1] = pos[M - 1] + 1  # the last row is still inside its prompt
+    prompt = np.full((M, 4), 11, np.int32)
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    seq = torch.zeros((M, T), dtype=torch.int32, device="cuda")
+    xo = torch.zeros((M, D), device="cuda")
+    argmax_prev = dev(np.arange(M, dtype=np.int32) + 1000)
+    embd, ped, promptd, plend, posd = dev(emb), dev(pe), dev(prompt), dev(plen), dev(pos)
+    _lib.check(L.skv_next_embed(xo.data_ptr(), ids.data_ptr(), seq.data_ptr(),
+                                argmax_prev.data_ptr(), cand.data_ptr(), n_cand,
+                                promptd.data_ptr(), plend.data_ptr(), posd.data_ptr(), M, 4, T,
+                                embd.data_ptr(), ped.data_ptr(), D, V, T, s), "skv_next_embed")
+    tok = want.copy()
+    tok[M - 1] = 11  # pos < prompt_len: the prompt token
+    np.testing.assert_array_equal(ids.cpu().numpy(), tok)
+    sq = seq.cpu().numpy()
+    for b in range(M):
+        assert sq[b, pos[b]] == tok[b]
+    np.testing.assert_allclose(xo.cpu().numpy(), emb[tok] + pe[pos], rtol=0, atol=0)
+    # n_cand = 0: the previous argmax buffer; no embedding: x untouched
+    xo.zero_()
+    _lib.check(L.skv_next_embed(None, ids.data_ptr(), seq.data_ptr(), argmax_prev.data_ptr(),
+                                None, 0, promptd.data_ptr(), plend.data_ptr(), posd.data_ptr(), M,
+                                4, T, None, None, D, V, T, s), "skv_next_embed")
+    tok2 = np.arange(M) + 1000
+    tok2[M - 1] = 11
+    np.testing.assert_array_equal(ids.cpu().numpy(), tok2)
+    assert float(xo.abs().sum().item()) == 0.0
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 256, 768), (16, 2304, 768), (16, 3072, 768),
@@ -545,6 +622,28 @@ def test_prefill_then_decode_logits_match_oracle(gpu_ctx, shape, kv, tol):
     assert err < tol
     if kv == torch.float32:  # prefill alone, every row (the reference's forward)
         assert rel_rows(m.forward(toks), want) < tol
+
+
+def test_fused_step_tail_generates_the_same_tokens(gpu_ctx):
+    """Greedy generation with the fused step tail (argmax candidates from the
+    packed logits, skv_next_embed) gives the tokens of the unfused one
+    (skv_argmax, skv_next_tokens, skv_embed), graph-replayed and eager, and
+    a second run of the same generator repeats them."""
+    banner("fused step tail vs unfused")
+    from simple_llm_amd import model as M
+    m, params = make_model(gpu_ctx, 16400, 512, 8, 2, 128, seed=3, std=0.05)
+    r = np.random.default_rng(9)
+    prompts = [r.integers(0, 16400, n).tolist() for n in (5, 17, 30)]
+    g = M.Generator(m, prompts, 70, use_graph=True)
+    assert g.fused
+    a = g.run()
+    a2 = g.run()
+    b = M.Generator(m, prompts, 70, use_graph=True, fused_tail=False)
+    assert not b.fused
+    bb = b.run()
+    c = M.Generator(m, prompts, 70, use_graph=False).run()
+    assert a == bb == c == a2
+    assert all(len(o) == 70 and o[:len(p)] == p for o, p in zip(a, prompts))
 
 
 def test_prefill_graph_generate_equals_eager_and_decode_only(gpu_ctx):
