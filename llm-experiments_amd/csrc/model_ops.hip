@@ -743,9 +743,12 @@ __global__ __launch_bounds__(1024) void k_linear_skinny(LinArgs a, const float* 
 }
 
 // Steps per wavefront of k_linear_skinny for this K (NW = K / (16 STEPS)
-// wavefronts, 4..16), 0 when none fits.
+// wavefronts, 4..16), 0 when none fits. At K = 768 (and each 768-wide split
+// of K = 3072) 8 wavefronts of 6 steps measured best on MI355X, weights cold:
+// q/k/v 6.17 us against 6.32 (16 x 3) and 6.60 (4 x 12), MLP up 6.40 against
+// 6.54 and 6.83, MLP down 7.20 against 7.36; C3 595.5 against 599.1 us per step.
 int skinny_steps(int K) {
-  for (int st : {3, 4, 6, 8, 12}) {
+  for (int st : {6, 4, 3, 8, 12}) {
     if (K % (16 * st)) continue;
     const int nw = K / (16 * st);
     if (nw >= 4 && nw <= 16) return st;
