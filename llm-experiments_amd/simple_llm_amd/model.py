@@ -307,11 +307,12 @@ class TransformerModel:
             self._bufs[key] = wp
         return self._bufs[key]
 
-    def _launch_step(self, cache: KVCache, bf: _Buffers, fused: bool = False) -> None:
-        """One decode step's launches. fused: x already holds the step's input
-        rows (skv_next_embed ran), and the packed logits projection also
-        writes the argmax candidates into bf.cand (skv_next_embed finishes
-        them at the next step); needs _packed_logits() and B <= 16."""
+    def _launch_step(self, cache: KVCache, bf: _Buffers, embedded: bool = False,
+                     cand: bool = False) -> None:
+        """One decode step's launches. embedded: x already holds the step's
+        input rows (skv_next_embed ran). cand: the packed logits projection
+        also writes the argmax candidates into bf.cand (skv_next_embed
+        finishes them at the next step); needs _packed_logits() and B <= 16."""
         L = _lib.lib()
         tm = self.tm_params
         B, d, H, D, T = cache.batch_size, tm.embedding_dim, tm.n_heads, self.head_dim, \
@@ -328,7 +329,7 @@ class TransformerModel:
         lens0 = cache.layers[0].lens.data_ptr()
         # up to 16 rows: LayerNorm folded into the weights (skv_linear_folded)
         folded = self._folded() if B <= 16 else None
-        if not fused:
+        if not embedded:
             chk(L.skv_embed(x, bf.ids.data_ptr(), lens0, self.emb.data_ptr(), self.pe.data_ptr(),
                             B, d, tm.vocab_size, self.pe.shape[0], s), "skv_embed")
         for li, (lw, layer) in enumerate(zip(self.layers, cache.layers)):
@@ -362,11 +363,11 @@ class TransformerModel:
             chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, None, None, 0.0,
                              B, d, self.mlp_dim, 0, 0, lw_ws, lw_n, s), "skv_linear")
         packed = self._packed_logits() if B <= 16 else None
-        if fused and packed is None:
-            raise ValueError("the fused step needs the packed logits projection")
+        if cand and packed is None:
+            raise ValueError("argmax candidates need the packed logits projection")
         if packed is not None:
             chk(L.skv_linear_packed(bf.logits.data_ptr(), x, packed.data_ptr(), None, None, B,
-                                    tm.vocab_size, d, 0, bf.cand.data_ptr() if fused else None,
+                                    tm.vocab_size, d, 0, bf.cand.data_ptr() if cand else None,
                                     s), "skv_linear_packed")
         else:
             chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, None,
@@ -565,11 +566,13 @@ class Generator:
         self.seed = int(seed) & ((1 << 64) - 1)
         # greedy without a penalty takes the multi-workgroup argmax
         self.greedy = temperature == 0.0 and repetition_penalty == 1.0
-        # greedy up to 16 rows with the packed logits: the logits projection
-        # leaves per-workgroup argmax candidates and skv_next_embed finishes
-        # the argmax, picks the next input token and embeds it (one launch
-        # for skv_argmax's two, skv_next_tokens and skv_embed)
-        self.fused = bool(fused_tail) and self.greedy and B <= 16 and \
+        # Every step starts with skv_next_embed (skv_next_tokens and
+        # skv_embed in one launch), reading the previous token from argmax.
+        # Greedy up to 16 rows with the packed logits also folds the argmax
+        # in: the logits projection leaves per-workgroup candidates and
+        # skv_next_embed finishes them (no skv_argmax launches).
+        self.fused = bool(fused_tail)
+        self.cand_mode = self.fused and self.greedy and B <= 16 and \
             model._packed_logits() is not None
         self.reset()
 
@@ -580,7 +583,7 @@ class Generator:
         self.seq.zero_()
         self.seq[:, :self.prompt.shape[1]].copy_(self.prompt)
         self.bufs.argmax.zero_()
-        # the fused tail reads the previous step's candidates, or the
+        # with candidates, skv_next_embed reads the previous step's, or the
         # prefill's argmax before the first step
         self._cand_ready = False
 
@@ -594,7 +597,8 @@ class Generator:
         tm = m.tm_params
         _lib.check(L.skv_next_embed(bf.x.data_ptr() if embed else None, bf.ids.data_ptr(),
                                     self.seq.data_ptr(), bf.argmax.data_ptr(),
-                                    bf.cand.data_ptr(), bf.n_cand if self._cand_ready else 0,
+                                    bf.cand.data_ptr(),
+                                    bf.n_cand if self.cand_mode and self._cand_ready else 0,
                                     self.prompt.data_ptr(), self.prompt_len.data_ptr(),
                                     c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
                                     self.seq.shape[1], m.emb.data_ptr() if embed else None,
@@ -627,8 +631,11 @@ class Generator:
         s = _lib.stream_handle(m.ctx.device)
         if self.fused:
             self._next_embed(embed=True)
-            m._launch_step(c, bf, fused=True)
-            self._cand_ready = True
+            m._launch_step(c, bf, embedded=True, cand=self.cand_mode)
+            if self.cand_mode:
+                self._cand_ready = True
+            else:
+                self._pick()
             return
         _lib.check(L.skv_next_tokens(bf.ids.data_ptr(), self.seq.data_ptr(), bf.argmax.data_ptr(),
                                      self.prompt.data_ptr(), self.prompt_len.data_ptr(),

@@ -635,15 +635,35 @@ def test_fused_step_tail_generates_the_same_tokens(gpu_ctx):
     r = np.random.default_rng(9)
     prompts = [r.integers(0, 16400, n).tolist() for n in (5, 17, 30)]
     g = M.Generator(m, prompts, 70, use_graph=True)
-    assert g.fused
+    assert g.fused and g.cand_mode
     a = g.run()
     a2 = g.run()
     b = M.Generator(m, prompts, 70, use_graph=True, fused_tail=False)
-    assert not b.fused
+    assert not b.fused and not b.cand_mode
     bb = b.run()
     c = M.Generator(m, prompts, 70, use_graph=False).run()
     assert a == bb == c == a2
     assert all(len(o) == 70 and o[:len(p)] == p for o, p in zip(a, prompts))
+
+
+@pytest.mark.parametrize("temperature", [0.0, 0.8])
+def test_next_embed_step_generates_the_same_tokens(gpu_ctx, temperature):
+    """Without argmax candidates (vocab below the packed projection's range,
+    and sampling), the step still starts with skv_next_embed, reading the
+    argmax or sample buffer: the tokens equal those of skv_next_tokens +
+    skv_embed, graph-replayed and eager."""
+    banner(f"next_embed step, temperature {temperature}")
+    from simple_llm_amd import model as M
+    m, params = make_model(gpu_ctx, 300, 128, 4, 2, 96, seed=6, std=0.1)
+    r = np.random.default_rng(12)
+    prompts = [r.integers(0, 300, n).tolist() for n in (4, 19, 33)]
+    kw = dict(temperature=temperature, top_k=20, seed=7)
+    g = M.Generator(m, prompts, 80, use_graph=True, **kw)
+    assert g.fused and not g.cand_mode
+    a = g.run()
+    b = M.Generator(m, prompts, 80, use_graph=True, fused_tail=False, **kw).run()
+    c = M.Generator(m, prompts, 80, use_graph=False, **kw).run()
+    assert a == b == c
 
 
 def test_prefill_graph_generate_equals_eager_and_decode_only(gpu_ctx):
