@@ -383,7 +383,7 @@ int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                     int max_prompt, int seq_cap, skv_stream_t stream);
 
 /* Bytes of skv_linear_packed's argmax candidates for M rows: [M][256]
- * float values, then [M][256] int32 columns. */
+ * float values, then [M][256] int32 columns (one per workgroup). */
 size_t skv_linear_packed_cand_bytes(int M);
 
 /* skv_next_tokens and skv_embed in one launch, ending the argmax: with

@@ -19,6 +19,8 @@
 // LayerNorm in front of a projection can be folded into its x reads.
 // Weights are stored transposed, Wt[N][K], so every lane reads 16
 // contiguous bytes of a weight row per step.
+#include <type_traits>
+
 #include "skv_common.h"
 
 namespace skv {
@@ -104,6 +106,16 @@ constexpr int kLinMaxWaves = 16;      // wavefronts per workgroup, splitting K
 __device__ __forceinline__ float gelu_tanh(float v) {
   const float k0 = 0.7978845608028654f;  // sqrt(2 / pi)
   return 0.5f * v * (1.f + tanhf(k0 * (v + 0.044715f * v * v * v)));
+}
+
+// Barrier over the workgroup's LDS only: each wavefront waits for its own LDS
+// operations, not for its global loads and stores (__syncthreads() waits for
+// those too: before the logits' argmax step it waited for the logits' own
+// stores, ~3 us a call).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // argmax step: (v, i) replaces the best (bv, bi) if v is larger, or equal
@@ -401,6 +413,11 @@ void k_linear_wide(LinArgs a, int tiles_total) {
   constexpr int PARTS = NW / 2;  // K parts of a tile (units), 16 US columns of K each
   extern __shared__ float wsm[];  // x rows [16][K + 4], then partials [tiles][PARTS][64][4]
   __shared__ float wstat[16][2];
+  // argmax candidates (PACKED with a.cand): per-wavefront bests, arrivals
+  __shared__ float s_cv[PACKED ? NW : 1][16];
+  __shared__ int s_ci[PACKED ? NW : 1][16];
+  __shared__ unsigned s_done;
+  if (PACKED && threadIdx.x == 0) s_done = 0;  // used after the barrier below
   const int K = a.K, P = K + 4;   // K = 16 * US * PARTS
   float* xs = wsm;
   float* part = wsm + 16 * P;
@@ -536,7 +553,7 @@ void k_linear_wide(LinArgs a, int tiles_total) {
     compute(k + 1, wb);
   }
   if (k < nk) compute(k, wa);
-  __syncthreads();
+  lds_barrier();  // the partials; a clamped re-read may still be in flight
   // epilogue: tile j by wavefront j % NW; slot i of lane l is row 4 lk + i, column lr.
   // With a.cand (PACKED only) each row's first maximum over this workgroup's
   // columns is tracked as well: per lane, then over the 16 columns of a lane
@@ -565,29 +582,48 @@ void k_linear_wide(LinArgs a, int tiles_total) {
   }
   if constexpr (PACKED) {
     if (a.cand == nullptr) return;  // uniform
-    __shared__ float s_cv[NW][16];
-    __shared__ int s_ci[NW][16];
+    // Per row, the best of the 16 columns of a lane group by DPP row shifts
+    // (lane 15 of the group ends with all 16); each wavefront's bests go to
+    // LDS, it counts itself done on an LDS counter, and the last wavefront to
+    // arrive reduces the NW of them and writes the workgroup's candidates: no
+    // barrier. (Cross-lane shuffles and a barrier before a reduction by 16
+    // threads cost the projection ~3 us a call; every wavefront writing its
+    // own candidates, 16 times as many, slowed the picking.)
+    auto shr_step = [&](auto n) {  // lane j of a row takes lane j - n's (row_shr:n)
+      constexpr int ctl = 0x110 + decltype(n)::value;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) {  // the 16 columns of a lane group
-        const float ov = __shfl_xor(cbv[i], o);
-        const int oi = __shfl_xor(cbi[i], o);
+      for (int i = 0; i < 4; ++i) {
+        const float ov = __int_as_float(__builtin_amdgcn_update_dpp(
+            __float_as_int(cbv[i]), __float_as_int(cbv[i]), ctl, 0xF, 0xF, false));
+        const int oi = __builtin_amdgcn_update_dpp(cbi[i], cbi[i], ctl, 0xF, 0xF, false);
         better(cbv[i], cbi[i], ov, oi);
       }
-      if (lr == 0) {
+    };
+    shr_step(std::integral_constant<int, 1>{});
+    shr_step(std::integral_constant<int, 2>{});
+    shr_step(std::integral_constant<int, 4>{});
+    shr_step(std::integral_constant<int, 8>{});
+    if (lr == 15) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
         s_cv[wave][4 * lk + i] = cbv[i];
         s_ci[wave][4 * lk + i] = cbi[i];
       }
     }
-    __syncthreads();
-    if (tid < M) {
+    int last = 0;
+    if (l == 0)
+      last = __hip_atomic_fetch_add(&s_done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+             (unsigned)(NW - 1);
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if (l < M) {
       float bv = -INFINITY;
       int bi = a.N;
-      for (int w = 0; w < NW; ++w) better(bv, bi, s_cv[w][tid], s_ci[w][tid]);
+#pragma unroll
+      for (int w = 0; w < NW; ++w) better(bv, bi, s_cv[w][l], s_ci[w][l]);
       const int G = gridDim.x;
-      a.cand[(size_t)tid * G + blockIdx.x] = bv;
-      reinterpret_cast<int*>(a.cand + (size_t)M * G)[(size_t)tid * G + blockIdx.x] = bi;
+      a.cand[(size_t)l * G + blockIdx.x] = bv;
+      reinterpret_cast<int*>(a.cand + (size_t)M * G)[(size_t)l * G + blockIdx.x] = bi;
     }
   }
 }
@@ -984,8 +1020,8 @@ __global__ void k_next_tokens(int32_t* __restrict__ ids, int32_t* __restrict__ s
 }
 
 // k_next_tokens and k_embed in one launch, with the argmax's last step: row
-// b picks the first maximum over its n_cand (value, column) candidates (one
-// wavefront), or reads argmax_prev[b] when n_cand is 0, applies the
+// b picks the first maximum over its n_cand (value, column) candidates (256
+// threads), or reads argmax_prev[b] when n_cand is 0, applies the
 // next-token rule above, records the token, and writes x[b] = embedding[t] +
 // pos_table[pos] (no x when the embedding is null).
 __global__ __launch_bounds__(256) void k_next_embed(
@@ -995,33 +1031,45 @@ __global__ __launch_bounds__(256) void k_next_embed(
     const int32_t* __restrict__ pos, int B, int max_prompt, int seq_cap,
     const float* __restrict__ emb, const float* __restrict__ pe, int d, int vocab, int ctx) {
   __shared__ int s_t;
+  __shared__ float s_bv[4];
+  __shared__ int s_bi[4];
   const int b = blockIdx.x, tid = threadIdx.x;
   const int p = pos[b];
-  if (tid < 64) {
+  const bool in_prompt = p < prompt_len[b];  // uniform
+  if (!in_prompt && n_cand > 0) {
+    // the first maximum over the row's candidates, all 256 threads
+    const float* cv = cand + (size_t)b * n_cand;
+    const int* ci = reinterpret_cast<const int*>(cand + (size_t)B * n_cand) + (size_t)b * n_cand;
+    float bv = -INFINITY;
+    int bi = vocab;
+    for (int k = tid; k < n_cand; k += 256) better(bv, bi, cv[k], ci[k]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      better(bv, bi, ov, oi);
+    }
+    if ((tid & 63) == 0) {
+      s_bv[tid >> 6] = bv;
+      s_bi[tid >> 6] = bi;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
     int t;
-    if (p < prompt_len[b]) {
+    if (in_prompt) {
       t = prompt[(size_t)b * max_prompt + min(max(p, 0), max_prompt - 1)];
     } else if (n_cand > 0) {
-      const float* cv = cand + (size_t)b * n_cand;
-      const int* ci = reinterpret_cast<const int*>(cand + (size_t)B * n_cand) + (size_t)b * n_cand;
-      float bv = -INFINITY;
-      int bi = vocab;
-      for (int k = tid; k < n_cand; k += 64) better(bv, bi, cv[k], ci[k]);
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        better(bv, bi, ov, oi);
-      }
+      float bv = s_bv[0];
+      int bi = s_bi[0];
+      for (int w = 1; w < 4; ++w) better(bv, bi, s_bv[w], s_bi[w]);
       t = bi < vocab ? bi : 0;  // a row of NaN only: token 0
     } else {
       t = argmax_prev[b];
     }
-    if (tid == 0) {
-      ids[b] = t;
-      if (p >= 0 && p < seq_cap) seq[(size_t)b * seq_cap + p] = t;
-      s_t = t;
-    }
+    ids[b] = t;
+    if (p >= 0 && p < seq_cap) seq[(size_t)b * seq_cap + p] = t;
+    s_t = t;
   }
   if (emb == nullptr) return;  // uniform
   __syncthreads();

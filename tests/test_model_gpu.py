@@ -229,7 +229,7 @@ def test_packed_argmax_candidates_and_next_embed(gpu_ctx, M, N, K):
     y = torch.empty((M, N), device="cuda")
     cand = torch.full((L.skv_linear_packed_cand_bytes(M) // 4,), float("nan"), device="cuda")
     n_cand = L.skv_linear_packed_cand_bytes(M) // (8 * M)
-    assert n_cand == 256
+    assert n_cand == 256  # one per workgroup
     _lib.check(L.skv_linear_packed(y.data_ptr(), xd.data_ptr(), wp.data_ptr(), biasd.data_ptr(),
                                    resd.data_ptr(), M, N, K, 0, cand.data_ptr(), s),
                "skv_linear_packed")
