@@ -28,6 +28,8 @@ Extensions beyond the reference's four functions:
 from __future__ import annotations
 
 import ctypes
+import math
+import threading
 from typing import List, Optional
 
 import numpy as np
@@ -250,19 +252,51 @@ def _workspace(ctx: GPUContext, nbytes: int) -> torch.Tensor:
     return ws
 
 
+_WS_BYTES: dict = {}
+_PLAN_OUT = threading.local()
+
+
+def _decode_ws_bytes(B: int, h_q: int, d: int, n_chunks: int) -> int:
+    # skv_decode_workspace_bytes, memoised: a decode loop asks for the same few
+    # sizes every call and the ctypes round trip costs more than the lookup
+    key = (B, h_q, d, n_chunks)
+    need = _WS_BYTES.get(key)
+    if need is None:
+        if len(_WS_BYTES) > 4096:
+            _WS_BYTES.clear()
+        need = _WS_BYTES[key] = int(_lib.lib().skv_decode_workspace_bytes(B, h_q, d, n_chunks))
+    return need
+
+
+def _fills_after_append(fills: np.ndarray, cap: int) -> tuple[np.ndarray, int, int]:
+    """(fills after one append, their maximum, their sum); full sequences stay put.
+
+    Small batches go through Python ints: three numpy calls on an 8-entry
+    array cost about 4 us of host time per decode call, the list about 1 us."""
+    if fills.size <= 64:
+        after = [f + 1 if f < cap else cap for f in fills.tolist()]
+        top = max(after) if after else 0
+        return np.array(after, dtype=np.int64), top, sum(after)
+    after = np.minimum(fills + 1, cap)
+    return after, int(after.max()), int(after.sum())
+
+
 def decode_plan(ctx: GPUContext, batch_size: int, n_heads: int, n_kv_heads: int, max_len: int,
                 total_len: int = 0, *, head_dim: int, dtype: torch.dtype) -> tuple[int, int]:
     """(chunk_tokens, n_chunks_max) of the split-K decode for these sizes.
 
     total_len: filled tokens over the batch (0: batch_size * max_len);
     head_dim and the cache dtype select the kernel the plan is tuned for."""
-    L = _lib.lib()
-    c, n = ctypes.c_int(), ctypes.c_int()
-    rc = L.skv_decode_plan(batch_size, n_heads, n_kv_heads, int(head_dim), _lib.dtype_code(dtype),
-                           max(int(max_len), 1), int(total_len),
-                           int(ctx.config.decode_chunk_tokens), ctypes.byref(c), ctypes.byref(n))
-    _lib.check(rc, "skv_decode_plan")
-    return c.value, n.value
+    out = getattr(_PLAN_OUT, "refs", None)
+    if out is None:  # per thread: the call releases the GIL while it fills them
+        c, n = ctypes.c_int(), ctypes.c_int()
+        out = _PLAN_OUT.refs = (c, n, ctypes.byref(c), ctypes.byref(n))
+    rc = _lib.lib().skv_decode_plan(batch_size, n_heads, n_kv_heads, int(head_dim),
+                                    _lib.dtype_code(dtype), max(int(max_len), 1), int(total_len),
+                                    int(ctx.config.decode_chunk_tokens), out[2], out[3])
+    if rc:
+        _lib.check(rc, "skv_decode_plan")
+    return out[0].value, out[1].value
 
 
 def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.Tensor,
@@ -291,9 +325,9 @@ def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.T
     chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
                                   total, head_dim=cache.head_dim, dtype=cache.dtype)
     L = _lib.lib()
-    need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
+    need = _decode_ws_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
     ws = _workspace(ctx, need)
-    sc = float(scale) if scale is not None else 1.0 / float(np.sqrt(cache.head_dim))
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(cache.head_dim)
     stream = _lib.stream_handle(dev)
     cdt, qdt, odt = (_lib.dtype_code(cache.dtype), _lib.dtype_code(q.dtype),
                      _lib.dtype_code(out.dtype))
@@ -345,19 +379,18 @@ def kv_cache_append_attend(ctx: GPUContext, cache: KVCache, layer_idx: int, new_
                          f"{cache.batch_size * e_q} elements")
     batch_count(ctx)
     cap = cache.block_table.shape[1] * cache.block_size if cache.paged else cache.max_seq_len
-    after = np.minimum(layer.host_lens + 1, cap)  # full sequences stay put
+    after, top, total = _fills_after_append(layer.host_lens, cap)
     if max_len is None:
-        max_len = int(after.max())
-        total = int(after.sum())
-    else:
-        _check_max_len(max_len, after)
-        total = int(np.minimum(after, max_len).sum())
+        max_len = top
+    elif max_len < top:
+        _check_max_len(max_len, after)  # raises
+    # every fill is <= max_len here, so the total needs no clamp
     chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
                                   total, head_dim=cache.head_dim, dtype=cache.dtype)
     L = _lib.lib()
-    need = L.skv_decode_workspace_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
+    need = _decode_ws_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
     ws = _workspace(ctx, need)
-    sc = float(scale) if scale is not None else 1.0 / float(np.sqrt(cache.head_dim))
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(cache.head_dim)
     stream = _lib.stream_handle(dev)
     cdt, idt = _lib.dtype_code(cache.dtype), _lib.dtype_code(new_k.dtype)
     qdt, odt = _lib.dtype_code(q.dtype), _lib.dtype_code(out.dtype)
