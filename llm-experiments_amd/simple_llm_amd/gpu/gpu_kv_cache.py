@@ -299,6 +299,49 @@ def decode_plan(ctx: GPUContext, batch_size: int, n_heads: int, n_kv_heads: int,
     return out[0].value, out[1].value
 
 
+# Plans by (sizes, max_len, chunk hint): the plan of a total fill in [lo, hi] is (chunk, n).
+_PLAN_SPANS: dict = {}
+
+
+def _decode_plan_span(ctx: GPUContext, batch_size: int, n_heads: int, n_kv_heads: int,
+                      max_len: int, total_len: int, head_dim: int,
+                      dtype: torch.dtype) -> tuple[int, int]:
+    """decode_plan for a decode loop: the plan changes rarely as the fills grow, and
+    skv_decode_plan's chunk never decreases as total_len grows (n_chunks_max follows the
+    chunk; tests/test_abi.py checks both). So a miss also finds, by doubling and bisection,
+    the largest total with the same plan, and the calls up to it skip the ctypes query (~2
+    us of host time each)."""
+    hint = int(ctx.config.decode_chunk_tokens)
+    key = (batch_size, n_heads, n_kv_heads, head_dim, dtype, max_len, hint)
+    span = _PLAN_SPANS.get(key)
+    if span is not None and span[0] <= total_len <= span[1]:
+        return span[2], span[3]
+    plan = decode_plan(ctx, batch_size, n_heads, n_kv_heads, max_len, total_len,
+                       head_dim=head_dim, dtype=dtype)
+
+    def same(t: int) -> bool:
+        return decode_plan(ctx, batch_size, n_heads, n_kv_heads, max_len, t,
+                           head_dim=head_dim, dtype=dtype) == plan
+
+    # largest total with this plan, up to every sequence at max_len
+    top = max(batch_size * max(int(max_len), 1), total_len)
+    lo, step = total_len, 1
+    while lo + step <= top and same(lo + step):
+        lo += step
+        step *= 2
+    hi = min(lo + step, top + 1)  # plan(lo) == plan, plan(hi) != plan or hi past top
+    while hi - lo > 1:
+        mid = (lo + hi) // 2
+        if same(mid):
+            lo = mid
+        else:
+            hi = mid
+    if len(_PLAN_SPANS) > 1024:
+        _PLAN_SPANS.clear()
+    _PLAN_SPANS[key] = (total_len, lo, plan[0], plan[1])
+    return plan
+
+
 def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.Tensor,
                      out: torch.Tensor, scale: Optional[float] = None,
                      max_len: Optional[int] = None) -> None:
@@ -322,8 +365,8 @@ def decode_attention(ctx: GPUContext, cache: KVCache, layer_idx: int, q: torch.T
         max_len = int(layer.host_lens.max())
     _check_max_len(max_len, layer.host_lens)
     total = int(np.minimum(layer.host_lens, max_len).sum())
-    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
-                                  total, head_dim=cache.head_dim, dtype=cache.dtype)
+    chunk, nchunks = _decode_plan_span(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads,
+                                       max_len, total, cache.head_dim, cache.dtype)
     L = _lib.lib()
     need = _decode_ws_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
     ws = _workspace(ctx, need)
@@ -385,8 +428,8 @@ def kv_cache_append_attend(ctx: GPUContext, cache: KVCache, layer_idx: int, new_
     elif max_len < top:
         _check_max_len(max_len, after)  # raises
     # every fill is <= max_len here, so the total needs no clamp
-    chunk, nchunks = decode_plan(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads, max_len,
-                                  total, head_dim=cache.head_dim, dtype=cache.dtype)
+    chunk, nchunks = _decode_plan_span(ctx, cache.batch_size, cache.n_heads, cache.n_kv_heads,
+                                       max_len, total, cache.head_dim, cache.dtype)
     L = _lib.lib()
     need = _decode_ws_bytes(cache.batch_size, cache.n_heads, cache.head_dim, nchunks)
     ws = _workspace(ctx, need)

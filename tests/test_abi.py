@@ -233,3 +233,53 @@ def test_check_maps_status_to_exceptions():
         _lib.check(_lib.SKV_E_INVALID, "x")
     with pytest.raises(_lib.SkvError):
         _lib.check(_lib.SKV_E_HIP, "x")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,dt,L,hint", [
+    (8, 8, 8, 64, _lib.F32, 2048, 0),        # C2
+    (16, 12, 12, 64, _lib.F32, 1024, 0),     # C3
+    (4, 16, 16, 128, _lib.BF16, 32768, 0),   # C4
+    (64, 32, 8, 128, _lib.BF16, 8320, 0),    # C5 (matrix-core GQA plan)
+    (3, 6, 2, 48, _lib.F32, 5000, 0),
+    (8, 8, 8, 64, _lib.F32, 2048, 100),      # a caller's chunk hint
+])
+def test_decode_plan_is_monotone_in_total(B, Hq, Hkv, D, dt, L, hint):
+    """The host's plan memo relies on it: the chunk never decreases as the
+    batch's total fill grows, and the slot count follows the chunk. (A total
+    of 0 stands for B * max_len.)"""
+    assert _plan(B, Hkv, L, hint=hint, total=0, Hq=Hq, D=D, dt=dt) == \
+        _plan(B, Hkv, L, hint=hint, total=B * L, Hq=Hq, D=D, dt=dt)
+    prev = None
+    for total in sorted(set(list(range(1, B * L + 1, max(1, B * L // 4000))) + [B * L])):
+        rc, chunk, n = _plan(B, Hkv, L, hint=hint, total=total, Hq=Hq, D=D, dt=dt)
+        assert rc == 0
+        if prev is not None:
+            assert chunk >= prev[0], (total, prev, chunk)
+            if chunk == prev[0]:
+                assert n == prev[1]
+        prev = (chunk, n)
+
+
+def test_memoised_plan_matches_the_query():
+    import random
+
+    import numpy as np
+    import torch
+
+    from simple_llm_amd.gpu import gpu_kv_cache as kvc
+    from simple_llm_amd.gpu.gpu_types import GPUConfig, GPUContext, PipelineCache
+
+    ctx = GPUContext(device=torch.device("cpu"), config=GPUConfig(), batch_state=None,
+                     pipeline_cache=PipelineCache())
+    rng = random.Random(0)
+    for B, Hq, Hkv, D, dtype, L in [(8, 8, 8, 64, torch.float32, 2048),
+                                    (64, 32, 8, 128, torch.bfloat16, 8320),
+                                    (4, 16, 16, 128, torch.bfloat16, 32768)]:
+        kvc._PLAN_SPANS.clear()
+        # a decode loop (totals grow by B), then resets and random totals
+        totals = [B + i * B for i in range(300)] + [rng.randrange(0, B * L + 1) for _ in range(300)]
+        totals += list(np.linspace(0, B * L, 200).astype(int))
+        for t in totals:
+            want = kvc.decode_plan(ctx, B, Hq, Hkv, L, int(t), head_dim=D, dtype=dtype)
+            got = kvc._decode_plan_span(ctx, B, Hq, Hkv, L, int(t), D, dtype)
+            assert got == want, (B, Hq, Hkv, D, L, t, got, want)
