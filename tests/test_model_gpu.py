@@ -150,7 +150,7 @@ def test_linear_split_shapes_share_workspace(gpu_ctx):
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 50304, 768), (1, 20000, 512), (9, 16400, 1024),
-                                   (16, 65536, 768)])
+                                   (16, 65536, 768), (16, 50257, 768)])
 def test_linear_packed_matches_unpacked(gpu_ctx, M, N, K):
     """skv_linear_pack + skv_linear_packed: the lane-ordered copy gives what
     skv_linear gives on the [N, K] weights (within fp32 rounding: the K
@@ -196,7 +196,7 @@ def test_linear_packed_matches_unpacked(gpu_ctx, M, N, K):
                                K, 0, None, s) != 0
 
 
-@pytest.mark.parametrize("M,N,K", [(16, 50304, 768), (3, 16400, 512)])
+@pytest.mark.parametrize("M,N,K", [(16, 50304, 768), (3, 16400, 512), (5, 50257, 768)])
 def test_packed_argmax_candidates_and_next_embed(gpu_ctx, M, N, K):
     """The packed logits' per-workgroup argmax candidates, finished by
     skv_next_embed, give numpy's first argmax of every row (rows with exact
@@ -624,16 +624,18 @@ def test_prefill_then_decode_logits_match_oracle(gpu_ctx, shape, kv, tol):
         assert rel_rows(m.forward(toks), want) < tol
 
 
-def test_fused_step_tail_generates_the_same_tokens(gpu_ctx):
+@pytest.mark.parametrize("vocab", [16400, 16411])
+def test_fused_step_tail_generates_the_same_tokens(gpu_ctx, vocab):
     """Greedy generation with the fused step tail (argmax candidates from the
     packed logits, skv_next_embed) gives the tokens of the unfused one
     (skv_argmax, skv_next_tokens, skv_embed), graph-replayed and eager, and
-    a second run of the same generator repeats them."""
-    banner("fused step tail vs unfused")
+    a second run of the same generator repeats them; also for a vocabulary
+    that is not a multiple of the 16-column tile (padded columns never win)."""
+    banner(f"fused step tail vs unfused, vocab {vocab}")
     from simple_llm_amd import model as M
-    m, params = make_model(gpu_ctx, 16400, 512, 8, 2, 128, seed=3, std=0.05)
+    m, params = make_model(gpu_ctx, vocab, 512, 8, 2, 128, seed=3, std=0.05)
     r = np.random.default_rng(9)
-    prompts = [r.integers(0, 16400, n).tolist() for n in (5, 17, 30)]
+    prompts = [r.integers(0, vocab, n).tolist() for n in (5, 17, 30)]
     g = M.Generator(m, prompts, 70, use_graph=True)
     assert g.fused and g.cand_mode
     a = g.run()
