@@ -283,3 +283,46 @@ def test_memoised_plan_matches_the_query():
             want = kvc.decode_plan(ctx, B, Hq, Hkv, L, int(t), head_dim=D, dtype=dtype)
             got = kvc._decode_plan_span(ctx, B, Hq, Hkv, L, int(t), D, dtype)
             assert got == want, (B, Hq, Hkv, D, L, t, got, want)
+
+
+def test_step_entry_points_reject_bad_arguments():
+    """The decode step's fused entry points (LayerNorm-folded and packed
+    projections, argmax candidates + next token + embedding) fail validation
+    before any device work."""
+    L = _lib.lib()
+    fake = 4096  # never dereferenced
+    # packed logits: M <= 16, K in {512, 768, 1024}, 16384 <= N <= 65536
+    for M, N, K in [(17, 50304, 768), (16, 1000, 768), (16, 50304, 640), (16, 70000, 768)]:
+        assert L.skv_linear_packed(fake, fake, fake, None, None, M, N, K, 0, None, None) == \
+            _lib.SKV_E_UNSUPPORTED, (M, N, K)
+    assert L.skv_linear_packed(fake, fake, fake, None, None, 16, 50304, 768, 2, None, None) == \
+        _lib.SKV_E_INVALID  # activation
+    assert L.skv_linear_packed(None, fake, fake, None, None, 16, 50304, 768, 0, None, None) == \
+        _lib.SKV_E_INVALID
+    assert L.skv_linear_packed_cand_bytes(16) == 16 * 256 * 8
+    # folded projections: up to 16 rows, K a shape of the one-tile kernel
+    assert L.skv_linear_folded(fake, fake, fake, fake, fake, None, 1e-5, 17, 768, 768, 0, 0,
+                               None) == _lib.SKV_E_UNSUPPORTED
+    assert L.skv_linear_folded(fake, fake, fake, fake, fake, None, 1e-5, 16, 768, 100, 0, 0,
+                               None) == _lib.SKV_E_UNSUPPORTED
+    assert L.skv_linear_folded(fake, fake, fake, None, fake, None, 1e-5, 16, 768, 768, 0, 0,
+                               None) == _lib.SKV_E_INVALID  # c1 missing
+    assert L.skv_linear_folded(fake, fake, fake, fake, fake, None, 1e-5, 16, 768, 768, 0, 5,
+                               None) == _lib.SKV_E_INVALID  # split_cols
+    # next token + embedding
+
+    def ne(**kw):
+        a = dict(x=fake, argmax_prev=fake, cand=None, n_cand=0, B=4, emb=fake, d=64, vocab=100,
+                 ctx=32)
+        a.update(kw)
+        return L.skv_next_embed(a["x"], fake, fake, a["argmax_prev"], a["cand"], a["n_cand"],
+                                fake, fake, fake, a["B"], 8, 64, a["emb"], fake, a["d"],
+                                a["vocab"], a["ctx"], None)
+
+    assert ne(B=0) == _lib.SKV_E_INVALID
+    assert ne(n_cand=-1) == _lib.SKV_E_INVALID
+    assert ne(n_cand=256) == _lib.SKV_E_INVALID  # candidates missing
+    assert b"candidates or the previous argmax" in L.skv_last_error()
+    assert ne(argmax_prev=None) == _lib.SKV_E_INVALID
+    assert ne(x=None) == _lib.SKV_E_INVALID  # an embedding needs x
+    assert ne(d=0) == _lib.SKV_E_INVALID
