@@ -121,10 +121,11 @@ __device__ __forceinline__ void lds_barrier() {
 // argmax step: (v, i) replaces the best (bv, bi) if v is larger, or equal
 // with a smaller index (the first maximum wins; NaN never does)
 __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
-  if (v > bv || (v == bv && i < bi)) {
-    bv = v;
-    bi = i;
-  }
+  // selects, not a branch: a branch split every use into basic blocks, so
+  // the loads feeding a chain of these could not be issued together
+  const bool take = v > bv || (v == bv && i < bi);
+  bv = take ? v : bv;
+  bi = take ? i : bi;
 }
 
 struct LinArgs {
@@ -173,7 +174,9 @@ struct LinArgs {
 // 256 registers.
 template <int TILES, int STEPS, bool LN, bool SPREAD>
 __global__ __launch_bounds__(STEPS > 4 ? 512 : kLinMaxWaves * 64) void k_linear(LinArgs a) {
-  extern __shared__ float red[];  // partial tiles of the W wavefronts (layout below)
+  // 16-byte aligned: the dynamic block starts after the static variables, at
+  // their size rounded up to this alignment, and is read as float4
+  extern __shared__ __attribute__((aligned(16))) float red[];  // partial tiles of the W wavefronts
   __shared__ float stat[kLinRowsPerBlock][2];
   // Row statistics from the registers when a pass covers all of K, for one
   // row tile and passes of 4+ steps: with fewer, the x rows are short (the
@@ -407,17 +410,22 @@ __global__ __launch_bounds__(STEPS > 4 ? 512 : kLinMaxWaves * 64) void k_linear(
 constexpr int kWideWaves = 8;
 constexpr int kWideMaxTiles = 16;  // column tiles per workgroup (N <= 65536 on 256 CUs)
 
-template <int US, bool LN, bool PACKED = false, int NW = kWideWaves>
+template <int US, bool LN, bool PACKED = false, int NW = kWideWaves, bool CAND = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void k_linear_wide(LinArgs a, int tiles_total) {
+  static_assert(!CAND || PACKED, "argmax candidates come with the packed weights only");
   constexpr int PARTS = NW / 2;  // K parts of a tile (units), 16 US columns of K each
-  extern __shared__ float wsm[];  // x rows [16][K + 4], then partials [tiles][PARTS][64][4]
+  // 16-byte aligned: the dynamic block starts after the static variables, at
+  // their size rounded up to this alignment, and is read as float4 (after the
+  // 2052 bytes of the candidates' variables it started misaligned by 4, and
+  // the packed logits took 33-36 instead of 29 us)
+  extern __shared__ __attribute__((aligned(16))) float wsm[];  // x rows [16][K + 4], then partials
   __shared__ float wstat[16][2];
-  // argmax candidates (PACKED with a.cand): per-wavefront bests, arrivals
-  __shared__ float s_cv[PACKED ? NW : 1][16];
-  __shared__ int s_ci[PACKED ? NW : 1][16];
+  // argmax candidates (CAND): per-wavefront bests, arrivals
+  __shared__ float s_cv[CAND ? NW : 1][16];
+  __shared__ int s_ci[CAND ? NW : 1][16];
   __shared__ unsigned s_done;
-  if (PACKED && threadIdx.x == 0) s_done = 0;  // used after the barrier below
+  if (CAND && threadIdx.x == 0) s_done = 0;  // used after the barrier below
   const int K = a.K, P = K + 4;   // K = 16 * US * PARTS
   float* xs = wsm;
   float* part = wsm + 16 * P;
@@ -555,7 +563,7 @@ void k_linear_wide(LinArgs a, int tiles_total) {
   if (k < nk) compute(k, wa);
   lds_barrier();  // the partials; a clamped re-read may still be in flight
   // epilogue: tile j by wavefront j % NW; slot i of lane l is row 4 lk + i, column lr.
-  // With a.cand (PACKED only) each row's first maximum over this workgroup's
+  // With CAND (a.cand given, packed weights) each row's first maximum over this workgroup's
   // columns is tracked as well: per lane, then over the 16 columns of a lane
   // group, then over the wavefronts in LDS, in an order-independent way
   // (larger value, or equal value and smaller column).
@@ -577,11 +585,10 @@ void k_linear_wide(LinArgs a, int tiles_total) {
       if (a.act == 1) y = gelu_tanh(y);
       if (a.res) y += a.res[(size_t)m * a.N + n];
       a.y[(size_t)m * a.N + n] = y;
-      if constexpr (PACKED) better(cbv[i], cbi[i], y, n);
+      if constexpr (CAND) better(cbv[i], cbi[i], y, n);
     }
   }
-  if constexpr (PACKED) {
-    if (a.cand == nullptr) return;  // uniform
+  if constexpr (CAND) {
     // Per row, the best of the 16 columns of a lane group by DPP row shifts
     // (lane 15 of the group ends with all 16); each wavefront's bests go to
     // LDS, it counts itself done on an LDS counter, and the last wavefront to
@@ -617,10 +624,17 @@ void k_linear_wide(LinArgs a, int tiles_total) {
     if (!__builtin_amdgcn_readfirstlane(last)) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     if (l < M) {
+      float vv[NW];
+      int ii[NW];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {  // every read issued before the first compare
+        vv[w] = s_cv[w][l];
+        ii[w] = s_ci[w][l];
+      }
       float bv = -INFINITY;
       int bi = a.N;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) better(bv, bi, s_cv[w][l], s_ci[w][l]);
+      for (int w = 0; w < NW; ++w) better(bv, bi, vv[w], ii[w]);
       const int G = gridDim.x;
       a.cand[(size_t)l * G + blockIdx.x] = bv;
       reinterpret_cast<int*>(a.cand + (size_t)M * G)[(size_t)l * G + blockIdx.x] = bi;
@@ -668,7 +682,8 @@ void k_linear_wide(LinArgs a, int tiles_total) {
 template <int STEPS, bool LN>
 __global__ __launch_bounds__(1024) void k_linear_skinny(LinArgs a, const float* __restrict__ c1,
                                                         unsigned* __restrict__ cnt) {
-  extern __shared__ float sred[];  // [NW][64][4] partial tiles, then [NW][16][2] row sums
+  // 16-byte aligned (read as float4; see k_linear_wide)
+  extern __shared__ __attribute__((aligned(16))) float sred[];  // [NW][64][4] partial tiles, then [NW][16][2] row sums
   const int NW = blockDim.x >> 6;
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, lr = l & 15, lk = l >> 4;
   const int M = a.M, K = a.K, N = a.N;
@@ -1328,24 +1343,31 @@ extern "C" int skv_linear_packed(float* y, const float* x, const float* w_packed
   const size_t x_lds = (size_t)16 * (K + 4) * sizeof(float);
   const size_t lds16 = x_lds + (size_t)per_wg * 8 * 64 * 4 * sizeof(float);
   const size_t lds8 = x_lds + (size_t)per_wg * 4 * 64 * 4 * sizeof(float);
-  if (lds16 <= 160 * 1024) {
-#define SKV_PK16(U)                                                                             \
-  hipLaunchKernelGGL((k_linear_wide<U, false, true, 16>), dim3(kNumCUs), dim3(16 * 64), lds16, s, \
-                     a, col_tiles)
-    if (K == 512) SKV_PK16(4);
-    else if (K == 768) SKV_PK16(6);
-    else SKV_PK16(8);
-#undef SKV_PK16
+  // the candidates' static LDS (16 wavefronts x 16 rows of value and column,
+  // the arrival counter, padding to 16 bytes) comes on top of lds16
+  const size_t cand_lds = argmax_cand ? 16 * 16 * 8 + 16 : 0;
+  // The candidates are a kernel of their own (CAND): compiled into the plain
+  // one, the unexecuted reduction left it ~5 us slower per call.
+  const bool cand = argmax_cand != nullptr;
+#define SKV_PKL(U, NWV, LDS)                                                                  \
+  if (cand)                                                                                   \
+    hipLaunchKernelGGL((k_linear_wide<U, false, true, NWV, true>), dim3(kNumCUs),             \
+                       dim3(NWV * 64), LDS, s, a, col_tiles);                                 \
+  else                                                                                        \
+    hipLaunchKernelGGL((k_linear_wide<U, false, true, NWV, false>), dim3(kNumCUs),            \
+                       dim3(NWV * 64), LDS, s, a, col_tiles);
+  if (lds16 + cand_lds <= 160 * 1024) {
+    if (K == 512) { SKV_PKL(4, 16, lds16) }
+    else if (K == 768) { SKV_PKL(6, 16, lds16) }
+    else { SKV_PKL(8, 16, lds16) }
   } else if (us == 8) {
-    hipLaunchKernelGGL((k_linear_wide<8, false, true>), dim3(kNumCUs), dim3(kWideWaves * 64), lds8,
-                       s, a, col_tiles);
+    SKV_PKL(8, kWideWaves, lds8)
   } else if (us == 12) {
-    hipLaunchKernelGGL((k_linear_wide<12, false, true>), dim3(kNumCUs), dim3(kWideWaves * 64),
-                       lds8, s, a, col_tiles);
+    SKV_PKL(12, kWideWaves, lds8)
   } else {
-    hipLaunchKernelGGL((k_linear_wide<16, false, true>), dim3(kNumCUs), dim3(kWideWaves * 64),
-                       lds8, s, a, col_tiles);
+    SKV_PKL(16, kWideWaves, lds8)
   }
+#undef SKV_PKL
   return check_launch("skv_linear_packed");
 }
 
