@@ -1049,15 +1049,24 @@ __global__ __launch_bounds__(256) void k_next_embed(
   __shared__ float s_bv[4];
   __shared__ int s_bi[4];
   const int b = blockIdx.x, tid = threadIdx.x;
+  // The fill, the prompt length and the first 256 candidates are loaded
+  // together, for every row (one inside its prompt ignores the candidates):
+  // the candidates then arrive with the fill instead of one round trip after
+  // it.
   const int p = pos[b];
-  const bool in_prompt = p < prompt_len[b];  // uniform
-  if (!in_prompt && n_cand > 0) {
+  const int plen = prompt_len[b];
+  float bv = -INFINITY;
+  int bi = vocab;
+  const float* cv = cand + (size_t)b * n_cand;
+  const int* ci = reinterpret_cast<const int*>(cand + (size_t)B * n_cand) + (size_t)b * n_cand;
+  if (tid < n_cand) {
+    bv = cv[tid];
+    bi = ci[tid];
+  }
+  for (int k = tid + 256; k < n_cand; k += 256) better(bv, bi, cv[k], ci[k]);
+  const bool in_prompt = p < plen;  // uniform
+  if (n_cand > 0) {
     // the first maximum over the row's candidates, all 256 threads
-    const float* cv = cand + (size_t)b * n_cand;
-    const int* ci = reinterpret_cast<const int*>(cand + (size_t)B * n_cand) + (size_t)b * n_cand;
-    float bv = -INFINITY;
-    int bi = vocab;
-    for (int k = tid; k < n_cand; k += 256) better(bv, bi, cv[k], ci[k]);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
       const float ov = __shfl_xor(bv, o);
