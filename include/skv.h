@@ -386,11 +386,32 @@ int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
  * float values, then [M][256] int32 columns (one per workgroup). */
 size_t skv_linear_packed_cand_bytes(int M);
 
+/* y = x . w_t^T + bias (bias may be NULL) for M <= 16 rows, as skv_linear
+ * computes it, with each row's argmax candidates in argmax_cand
+ * (skv_linear_cand_bytes(M, N, K) bytes): for every 16-column tile j of N,
+ * [M][ceil(N / 16)] float values (the first maximum of row m over columns
+ * [16 j, 16 j + 16); larger value, or equal value and smaller column; NaN
+ * never wins), then [M][ceil(N / 16)] int32 columns, for skv_next_embed with
+ * n_cand = ceil(N / 16). K must be 16 s w with s in {3, 4, 6, 8, 12} and
+ * 4 <= w <= 16 (48..3072), else SKV_E_UNSUPPORTED. ws (may be NULL) of
+ * skv_linear_workspace_bytes(M, N, K) bytes lets a narrow projection split
+ * K, as for skv_linear (zero-filled before its first use, stream ordered).
+ * The tied logits
+ * projection (jax_backend.py:147) for vocabularies skv_linear_packed does
+ * not take, and the first step of the greedy pick (jnp.argmax,
+ * jax_backend.py:469) that skv_next_embed finishes. */
+int skv_linear_cand(float* y, const float* x, const float* w_t, const float* bias, int M, int N,
+                    int K, float* argmax_cand, void* ws, size_t ws_bytes, skv_stream_t stream);
+
+/* Bytes of skv_linear_cand's candidates: M * ceil(N / 16) * 8, or 0 when
+ * skv_linear_cand does not take M and K. */
+size_t skv_linear_cand_bytes(int M, int N, int K);
+
 /* skv_next_tokens and skv_embed in one launch, ending the argmax: with
  * n_cand > 0 the previous token of row b is the first maximum over its
  * n_cand candidates (cand: [B][n_cand] float values, then [B][n_cand] int32
- * columns, as skv_linear_packed writes them; a row of NaN only gives token
- * 0), else argmax_prev[b]. Then ids[b] and seq as skv_next_tokens, and, when
+ * columns, as skv_linear_packed and skv_linear_cand write them; a row of
+ * NaN only gives token 0), else argmax_prev[b]. Then ids[b] and seq as skv_next_tokens, and, when
  * embedding is not NULL, x[b, :] = embedding[ids[b], :] + pos_table[pos[b], :]
  * as skv_embed (ids and positions clamped into the tables). No counterpart
  * in the reference, whose generate loop picks and embeds on the host side

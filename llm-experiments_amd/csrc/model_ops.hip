@@ -666,6 +666,11 @@ void k_linear_wide(LinArgs a, int tiles_total) {
 // Rows past M read row M - 1 (their results are dropped), so no load is
 // conditional. The NW wavefront partials are summed in order in LDS.
 //
+// CAND (no LN; a.cand given): the workgroup also writes each row's first
+// maximum over its 16 columns (larger value, or equal value and smaller
+// column; NaN never wins) to a.cand[m][blockIdx.x], values then columns, by
+// DPP row shifts over the 16 epilogue lanes of the row: no LDS, no barrier.
+//
 // Split K (grid.y = S > 1, no LN): workgroup (j, z) takes the K range
 // [z K / S, (z + 1) K / S) of tile j, for narrow layers with too few tiles
 // to occupy the CUs (16 x 3072 -> 768: 48 tiles). The last of a tile's S
@@ -679,9 +684,10 @@ void k_linear_wide(LinArgs a, int tiles_total) {
 // device-scope atomic loads, which are served from memory. The arrival
 // counters (one per tile, in the caller's workspace) start at zero and the
 // last arriver puts its tile's back to zero.
-template <int STEPS, bool LN>
+template <int STEPS, bool LN, bool CAND = false>
 __global__ __launch_bounds__(1024) void k_linear_skinny(LinArgs a, const float* __restrict__ c1,
                                                         unsigned* __restrict__ cnt) {
+  static_assert(!CAND || !LN, "candidates only without LayerNorm");
   // 16-byte aligned (read as float4; see k_linear_wide)
   extern __shared__ __attribute__((aligned(16))) float sred[];  // [NW][64][4] partial tiles, then [NW][16][2] row sums
   const int NW = blockDim.x >> 6;
@@ -777,20 +783,46 @@ __global__ __launch_bounds__(1024) void k_linear_skinny(LinArgs a, const float* 
         if (z0 + i < S) v += pz[i];
     }
   }
-  if (!et || em >= M || en >= N) return;
-  if constexpr (LN) {
-    float s1 = 0.f, s2 = 0.f;
-    for (int wv = 0; wv < NW; ++wv) {
-      s1 += rsum[(wv * 16 + em) * 2];
-      s2 += rsum[(wv * 16 + em) * 2 + 1];
+  const bool live = et && em < M && en < N;
+  if (!CAND && !live) return;
+  if (live) {
+    if constexpr (LN) {
+      float s1 = 0.f, s2 = 0.f;
+      for (int wv = 0; wv < NW; ++wv) {
+        s1 += rsum[(wv * 16 + em) * 2];
+        s2 += rsum[(wv * 16 + em) * 2 + 1];
+      }
+      const float ms = s1 / K;  // mean - c
+      const float rstd = 1.f / sqrtf(fmaxf(s2 / K - ms * ms, 0.f) + a.ln_eps);
+      v = rstd * (v - ms * e_c1);
     }
-    const float ms = s1 / K;  // mean - c
-    const float rstd = 1.f / sqrtf(fmaxf(s2 / K - ms * ms, 0.f) + a.ln_eps);
-    v = rstd * (v - ms * e_c1);
+    v += e_bias;
+    if (a.act == 1) v = gelu_tanh(v);
+    v += e_res;
+    a.y[oidx] = v;
   }
-  v += e_bias;
-  if (a.act == 1) v = gelu_tanh(v);
-  a.y[oidx] = v + e_res;
+  if constexpr (CAND) {
+    if (!et || 4 * wave >= M) return;  // whole wavefronts: rows 4 wave .. 4 wave + 3
+    float bv = -INFINITY;
+    int bi = N;
+    if (live) better(bv, bi, v, en);
+    auto shr_step = [&](auto n) {  // lane j of a row takes lane j - n's (row_shr:n)
+      constexpr int ctl = 0x110 + decltype(n)::value;
+      const float ov = __int_as_float(
+          __builtin_amdgcn_update_dpp(__float_as_int(bv), __float_as_int(bv), ctl, 0xF, 0xF, false));
+      const int oi = __builtin_amdgcn_update_dpp(bi, bi, ctl, 0xF, 0xF, false);
+      better(bv, bi, ov, oi);
+    };
+    shr_step(std::integral_constant<int, 1>{});
+    shr_step(std::integral_constant<int, 2>{});
+    shr_step(std::integral_constant<int, 4>{});
+    shr_step(std::integral_constant<int, 8>{});
+    if ((tid & 15) == 15 && em < M) {  // lane 15 of the row holds all 16
+      const int G = gridDim.x;
+      a.cand[(size_t)em * G + blockIdx.x] = bv;
+      reinterpret_cast<int*>(a.cand + (size_t)M * G)[(size_t)em * G + blockIdx.x] = bi;
+    }
+  }
 }
 
 // Steps per wavefront of k_linear_skinny for this K (NW = K / (16 STEPS)
@@ -834,21 +866,26 @@ size_t skinny_ws_bytes(int N, int S) {
   return S > 1 ? kLinCntBytes + tiles * S * 256 * sizeof(float) : 0;
 }
 
-// a.kz: K range of one split (K when S == 1); a.part: partials; cnt: counters
+// a.kz: K range of one split (K when S == 1); a.part: partials; cnt: counters;
+// a.cand (no LN): argmax candidates
 int launch_skinny(const LinArgs& a, const float* c1, bool ln, int S, unsigned* cnt,
                   hipStream_t s) {
   const int st = skinny_steps(a.kz);
   const int nw = a.kz / (16 * st);
   const size_t lds = (size_t)nw * (256 + 32) * sizeof(float);
   const dim3 grid((a.N + 15) / 16, S);
-#define SKV_SK(S_)                                                                      \
-  if (st == S_) {                                                                       \
-    if (ln)                                                                             \
-      hipLaunchKernelGGL((k_linear_skinny<S_, true>), grid, dim3(nw * 64), lds, s, a, c1,  \
-                         cnt);                                                           \
-    else                                                                                \
-      hipLaunchKernelGGL((k_linear_skinny<S_, false>), grid, dim3(nw * 64), lds, s, a, c1, \
-                         cnt);                                                           \
+  const bool cand = a.cand != nullptr;
+#define SKV_SK(S_)                                                                          \
+  if (st == S_) {                                                                           \
+    if (ln)                                                                                 \
+      hipLaunchKernelGGL((k_linear_skinny<S_, true>), grid, dim3(nw * 64), lds, s, a, c1,      \
+                         cnt);                                                               \
+    else if (cand)                                                                          \
+      hipLaunchKernelGGL((k_linear_skinny<S_, false, true>), grid, dim3(nw * 64), lds, s, a, \
+                         c1, cnt);                                                           \
+    else                                                                                    \
+      hipLaunchKernelGGL((k_linear_skinny<S_, false>), grid, dim3(nw * 64), lds, s, a, c1,     \
+                         cnt);                                                               \
   }
   SKV_SK(3) SKV_SK(4) SKV_SK(6) SKV_SK(8) SKV_SK(12)
 #undef SKV_SK
@@ -1404,6 +1441,32 @@ extern "C" int skv_argmax(int32_t* out, const float* x, int M, int N, void* ws, 
 
 extern "C" size_t skv_linear_packed_cand_bytes(int M) {
   return M > 0 ? (size_t)M * kNumCUs * 8 : 0;
+}
+
+// The logits of a vocabulary too narrow for skv_linear_packed (C1: 256 from
+// 256): skv_linear's one-tile-per-workgroup kernel (split K as skv_linear
+// splits it when the workspace allows), with the candidates in its epilogue,
+// so the step needs no argmax launch.
+extern "C" int skv_linear_cand(float* y, const float* x, const float* w_t, const float* bias,
+                               int M, int N, int K, float* argmax_cand, void* ws,
+                               size_t ws_bytes, skv_stream_t stream) {
+  SKV_REQUIRE(y && x && w_t && argmax_cand, SKV_E_INVALID, "skv_linear_cand: null pointer argument");
+  SKV_REQUIRE(M > 0 && N > 0 && K > 0, SKV_E_INVALID, "skv_linear_cand: dims must be > 0");
+  SKV_REQUIRE(M <= 16 && skinny_steps(K) > 0, SKV_E_UNSUPPORTED,
+              "skv_linear_cand: M=%d K=%d (needs M <= 16 and K = 16 s w, s in {3, 4, 6, 8, 12}, "
+              "4 <= w <= 16)", M, K);
+  int S = skinny_splits(M, N, K);
+  if (S > 1 && (ws == nullptr || ws_bytes < skinny_ws_bytes(N, S))) S = 1;
+  char* wsb = static_cast<char*>(ws);
+  LinArgs a{y, x, w_t, bias, nullptr, nullptr, nullptr, 0.f, M, N, K, 0, 0, K / S,
+            S > 1 ? reinterpret_cast<float*>(wsb + kLinCntBytes) : nullptr, argmax_cand};
+  return launch_skinny(a, nullptr, false, S, S > 1 ? reinterpret_cast<unsigned*>(wsb) : nullptr,
+                       (hipStream_t)stream);
+}
+
+extern "C" size_t skv_linear_cand_bytes(int M, int N, int K) {
+  if (M <= 0 || M > 16 || N <= 0 || K <= 0 || skinny_steps(K) == 0) return 0;
+  return (size_t)M * ((N + 15) / 16) * 8;
 }
 
 extern "C" int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_t* argmax_prev,

@@ -127,10 +127,11 @@ class _Buffers:
         lin = max(L.skv_linear_workspace_bytes(B, n, k)
                   for n, k in ((3 * d, d), (d, d), (mlp, d), (d, mlp), (vocab, d)))
         self.lin_ws = torch.zeros(max(lin, 4), dtype=torch.uint8, device=dev)
-        # per-row argmax candidates of the packed logits projection (the
-        # step's argmax, finished by skv_next_embed)
-        self.cand = torch.zeros(max(L.skv_linear_packed_cand_bytes(B) // 4, 1), device=dev)
-        self.n_cand = L.skv_linear_packed_cand_bytes(B) // (8 * B)
+        # per-row argmax candidates of the logits projection (the step's
+        # argmax, finished by skv_next_embed): skv_linear_packed's or
+        # skv_linear_cand's, whichever the model's sizes take
+        cb = max(L.skv_linear_packed_cand_bytes(B), L.skv_linear_cand_bytes(B, vocab, d))
+        self.cand = torch.zeros(max(cb // 4, 1), device=dev)
 
 
 class _PrefillBuffers:
@@ -307,12 +308,24 @@ class TransformerModel:
             self._bufs[key] = wp
         return self._bufs[key]
 
+    def _n_cand(self, B: int) -> int:
+        """Argmax candidates per row the logits projection of a B-row step
+        can write (0: none): one per workgroup of skv_linear_packed, else one
+        per 16-column tile of skv_linear_cand."""
+        if B > 16:
+            return 0
+        L = _lib.lib()
+        if self._packed_logits() is not None:
+            return L.skv_linear_packed_cand_bytes(B) // (8 * B)
+        V, d = self.emb.shape
+        return L.skv_linear_cand_bytes(B, V, d) // (8 * B)
+
     def _launch_step(self, cache: KVCache, bf: _Buffers, embedded: bool = False,
                      cand: bool = False) -> None:
         """One decode step's launches. embedded: x already holds the step's
-        input rows (skv_next_embed ran). cand: the packed logits projection
-        also writes the argmax candidates into bf.cand (skv_next_embed
-        finishes them at the next step); needs _packed_logits() and B <= 16."""
+        input rows (skv_next_embed ran). cand: the logits projection also
+        writes the argmax candidates into bf.cand (skv_next_embed finishes
+        them at the next step); needs _n_cand(B) > 0."""
         L = _lib.lib()
         tm = self.tm_params
         B, d, H, D, T = cache.batch_size, tm.embedding_dim, tm.n_heads, self.head_dim, \
@@ -363,12 +376,17 @@ class TransformerModel:
             chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, None, None, 0.0,
                              B, d, self.mlp_dim, 0, 0, lw_ws, lw_n, s), "skv_linear")
         packed = self._packed_logits() if B <= 16 else None
-        if cand and packed is None:
-            raise ValueError("argmax candidates need the packed logits projection")
+        if cand and self._n_cand(B) == 0:
+            raise ValueError("argmax candidates need B <= 16 and a logits projection that "
+                             "writes them (skv_linear_packed or skv_linear_cand sizes)")
         if packed is not None:
             chk(L.skv_linear_packed(bf.logits.data_ptr(), x, packed.data_ptr(), None, None, B,
                                     tm.vocab_size, d, 0, bf.cand.data_ptr() if cand else None,
                                     s), "skv_linear_packed")
+        elif cand:
+            chk(L.skv_linear_cand(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, B,
+                                  tm.vocab_size, d, bf.cand.data_ptr(), lw_ws, lw_n, s),
+                "skv_linear_cand")
         else:
             chk(L.skv_linear(bf.logits.data_ptr(), x, self.emb.data_ptr(), None, None, None,
                              None, 0.0, B, tm.vocab_size, d, 0, 0, lw_ws, lw_n, s), "skv_linear")
@@ -568,12 +586,13 @@ class Generator:
         self.greedy = temperature == 0.0 and repetition_penalty == 1.0
         # Every step starts with skv_next_embed (skv_next_tokens and
         # skv_embed in one launch), reading the previous token from argmax.
-        # Greedy up to 16 rows with the packed logits also folds the argmax
-        # in: the logits projection leaves per-workgroup candidates and
-        # skv_next_embed finishes them (no skv_argmax launches).
+        # Greedy up to 16 rows also folds the argmax in where the logits
+        # projection can leave per-workgroup candidates (skv_linear_packed,
+        # skv_linear_cand): skv_next_embed finishes them (no skv_argmax
+        # launches).
         self.fused = bool(fused_tail)
-        self.cand_mode = self.fused and self.greedy and B <= 16 and \
-            model._packed_logits() is not None
+        self.n_cand = model._n_cand(B) if self.fused and self.greedy else 0
+        self.cand_mode = self.n_cand > 0
         self.reset()
 
     def reset(self) -> None:
@@ -598,7 +617,7 @@ class Generator:
         _lib.check(L.skv_next_embed(bf.x.data_ptr() if embed else None, bf.ids.data_ptr(),
                                     self.seq.data_ptr(), bf.argmax.data_ptr(),
                                     bf.cand.data_ptr(),
-                                    bf.n_cand if self.cand_mode and self._cand_ready else 0,
+                                    self.n_cand if self._cand_ready else 0,
                                     self.prompt.data_ptr(), self.prompt_len.data_ptr(),
                                     c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
                                     self.seq.shape[1], m.emb.data_ptr() if embed else None,

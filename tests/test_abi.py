@@ -287,8 +287,8 @@ def test_memoised_plan_matches_the_query():
 
 def test_step_entry_points_reject_bad_arguments():
     """The decode step's fused entry points (LayerNorm-folded and packed
-    projections, argmax candidates + next token + embedding) fail validation
-    before any device work."""
+    projections, the skinny logits with candidates, argmax candidates + next
+    token + embedding) fail validation before any device work."""
     L = _lib.lib()
     fake = 4096  # never dereferenced
     # packed logits: M <= 16, K in {512, 768, 1024}, 16384 <= N <= 65536
@@ -300,6 +300,17 @@ def test_step_entry_points_reject_bad_arguments():
     assert L.skv_linear_packed(None, fake, fake, None, None, 16, 50304, 768, 0, None, None) == \
         _lib.SKV_E_INVALID
     assert L.skv_linear_packed_cand_bytes(16) == 16 * 256 * 8
+    # skinny logits with candidates: M <= 16, K a shape of the one-tile kernel
+    for M, K in [(17, 256), (16, 100), (1, 4096)]:
+        assert L.skv_linear_cand(fake, fake, fake, None, M, 256, K, fake, None, 0, None) == \
+            _lib.SKV_E_UNSUPPORTED, (M, K)
+        assert L.skv_linear_cand_bytes(M, 256, K) == 0
+    assert L.skv_linear_cand(fake, fake, fake, None, 1, 256, 256, None, None, 0, None) == \
+        _lib.SKV_E_INVALID  # candidates missing
+    assert L.skv_linear_cand(fake, fake, fake, None, 1, 0, 256, fake, None, 0, None) == \
+        _lib.SKV_E_INVALID
+    assert L.skv_linear_cand_bytes(1, 256, 256) == 16 * 8
+    assert L.skv_linear_cand_bytes(16, 300, 768) == 16 * 19 * 8
     # folded projections: up to 16 rows, K a shape of the one-tile kernel
     assert L.skv_linear_folded(fake, fake, fake, fake, fake, None, 1e-5, 17, 768, 768, 0, 0,
                                None) == _lib.SKV_E_UNSUPPORTED

@@ -273,6 +273,81 @@ def test_packed_argmax_candidates_and_next_embed(gpu_ctx, M, N, K):
     assert float(xo.abs().sum().item()) == 0.0
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 256, 256), (16, 300, 256), (5, 4000, 768),
+                                   (3, 1000, 1024), (2, 50, 3072)])
+def test_linear_cand_matches_skv_linear_and_argmax(gpu_ctx, M, N, K):
+    """skv_linear_cand: y equal to skv_linear's (the same kernel, unsplit or
+    split K alike: (3, 1000, 1024) splits 4 ways, (2, 50, 3072) 8 ways), and
+    every 16-column tile's candidate the first maximum of its columns (a tie
+    across tiles, a NaN column that never wins, a ragged last tile, a row
+    with its maximum in the last column); skv_next_embed over the
+    ceil(N / 16) candidates gives numpy's first argmax of every row."""
+    banner(f"linear candidates M={M} N={N} K={K}")
+    _lib = lib()
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    r = np.random.default_rng(N + M + K)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    w = (r.standard_normal((N, K)) * 0.05).astype(np.float32)
+    # columns 5 and N - 3 (other tiles for N > 24): the same weights and a +100
+    # bias, a tie at the top of every row (the first wins); row 1: column N - 1
+    # larger through x[1, 0]; column 7: NaN through its bias
+    x[:, 0] = 0.0
+    w[N - 3] = w[5]
+    bias = np.zeros(N, np.float32)
+    bias[5] = bias[N - 3] = 100.0
+    bias[7] = np.nan
+    if M > 1:
+        x[1, 0] = 100.0
+        w[N - 1, 0] = 50.0
+    xd, wd, biasd = dev(x), dev(w), dev(bias)
+    ws = torch.zeros(max(L.skv_linear_workspace_bytes(M, N, K), 4), dtype=torch.uint8,
+                     device="cuda")
+    cb = L.skv_linear_cand_bytes(M, N, K)
+    G = (N + 15) // 16
+    assert cb == M * G * 8
+    y = torch.empty((M, N), device="cuda")
+    y_ref = torch.empty((M, N), device="cuda")
+    cand = torch.full((cb // 4,), float("nan"), device="cuda")
+    for _ in range(2):  # the split's arrival counters are left at zero
+        _lib.check(L.skv_linear_cand(y.data_ptr(), xd.data_ptr(), wd.data_ptr(), biasd.data_ptr(),
+                                     M, N, K, cand.data_ptr(), ws.data_ptr(), ws.numel(), s),
+                   "skv_linear_cand")
+    _lib.check(L.skv_linear(y_ref.data_ptr(), xd.data_ptr(), wd.data_ptr(), biasd.data_ptr(),
+                            None, None, None, 0.0, M, N, K, 0, 0, ws.data_ptr(), ws.numel(), s),
+               "skv_linear")
+    yh = y.cpu().numpy()
+    np.testing.assert_array_equal(yh, y_ref.cpu().numpy())
+    want_y = x.astype(np.float64) @ w.T.astype(np.float64) + bias
+    np.testing.assert_allclose(yh, want_y, rtol=1e-4, atol=1e-4)
+    assert np.isnan(yh[:, 7]).all()
+    cv = cand[:M * G].cpu().numpy().reshape(M, G)
+    ci = cand[M * G:].cpu().view(torch.int32).numpy().reshape(M, G)
+    for m in range(M):
+        for j in range(G):
+            t = yh[m, 16 * j:16 * j + 16]
+            if np.isnan(t).all():
+                assert cv[m, j] == -np.inf and ci[m, j] == N
+                continue
+            k = int(np.nanargmax(t))
+            assert ci[m, j] == 16 * j + k and cv[m, j] == t[k], (m, j)
+    want = np.array([int(np.nanargmax(row)) for row in yh])
+    assert want[0] == 5
+    if M > 1:
+        assert want[1] == N - 1
+    T = 8
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    seq = torch.zeros((M, T), dtype=torch.int32, device="cuda")
+    pos = dev(np.full(M, 2, np.int32))
+    plen = dev(np.zeros(M, np.int32))
+    prompt = dev(np.zeros((M, 4), np.int32))
+    _lib.check(L.skv_next_embed(None, ids.data_ptr(), seq.data_ptr(), None, cand.data_ptr(), G,
+                                prompt.data_ptr(), plen.data_ptr(), pos.data_ptr(), M, 4, T, None,
+                                None, 0, N, T, s), "skv_next_embed")
+    np.testing.assert_array_equal(ids.cpu().numpy(), want)
+    np.testing.assert_array_equal(seq.cpu().numpy()[:, 2], want)
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 256, 768), (16, 2304, 768), (16, 3072, 768),
                                    (7, 1000, 1024), (16, 96, 3072), (3, 2304, 256)])
 def test_linear_folded_matches_numpy(gpu_ctx, M, N, K):
@@ -624,20 +699,24 @@ def test_prefill_then_decode_logits_match_oracle(gpu_ctx, shape, kv, tol):
         assert rel_rows(m.forward(toks), want) < tol
 
 
-@pytest.mark.parametrize("vocab", [16400, 16411])
-def test_fused_step_tail_generates_the_same_tokens(gpu_ctx, vocab):
+@pytest.mark.parametrize("vocab,d,heads", [(16400, 512, 8), (16411, 512, 8), (256, 256, 4),
+                                            (300, 256, 4)])
+def test_fused_step_tail_generates_the_same_tokens(gpu_ctx, vocab, d, heads):
     """Greedy generation with the fused step tail (argmax candidates from the
-    packed logits, skv_next_embed) gives the tokens of the unfused one
-    (skv_argmax, skv_next_tokens, skv_embed), graph-replayed and eager, and
-    a second run of the same generator repeats them; also for a vocabulary
-    that is not a multiple of the 16-column tile (padded columns never win)."""
-    banner(f"fused step tail vs unfused, vocab {vocab}")
+    logits projection: skv_linear_packed for the wide vocabularies,
+    skv_linear_cand for the narrow ones; skv_next_embed) gives the tokens of
+    the unfused one (skv_argmax, skv_next_tokens, skv_embed), graph-replayed
+    and eager, and a second run of the same generator repeats them; also for
+    vocabularies that are not a multiple of the 16-column tile (padded
+    columns never win)."""
+    banner(f"fused step tail vs unfused, vocab {vocab} d {d}")
     from simple_llm_amd import model as M
-    m, params = make_model(gpu_ctx, vocab, 512, 8, 2, 128, seed=3, std=0.05)
+    m, params = make_model(gpu_ctx, vocab, d, heads, 2, 128, seed=3, std=0.05)
     r = np.random.default_rng(9)
     prompts = [r.integers(0, vocab, n).tolist() for n in (5, 17, 30)]
     g = M.Generator(m, prompts, 70, use_graph=True)
     assert g.fused and g.cand_mode
+    assert g.n_cand == (256 if vocab >= 16384 else (vocab + 15) // 16)
     a = g.run()
     a2 = g.run()
     b = M.Generator(m, prompts, 70, use_graph=True, fused_tail=False)
