@@ -371,7 +371,7 @@ def run_c1(args, ctx):
                      "token), then 191 cached decode steps replayed from one HIP graph; value "
                      "= generated tokens / whole run (prefill included)",
          "batch": 1, "prompt": 64, "generated": 192},
-        {"bound": "launch latency", "note": "12.8 MB of weights per token; ~40 launches per "
+        {"bound": "launch latency", "note": "12.8 MB of weights per token; 26 kernels per "
                                             "step replayed from one HIP graph",
          "achieved": wbytes / (r["step_us"] * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": wbytes / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, "traffic": None},
