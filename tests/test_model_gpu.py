@@ -274,10 +274,11 @@ def test_packed_argmax_candidates_and_next_embed(gpu_ctx, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 256, 256), (16, 300, 256), (5, 4000, 768),
-                                   (3, 1000, 1024), (2, 50, 3072)])
+                                   (3, 1000, 1024), (2, 50, 3072), (4, 20011, 384)])
 def test_linear_cand_matches_skv_linear_and_argmax(gpu_ctx, M, N, K):
     """skv_linear_cand: y equal to skv_linear's (the same kernel, unsplit or
-    split K alike: (3, 1000, 1024) splits 4 ways, (2, 50, 3072) 8 ways), and
+    split K alike: (3, 1000, 1024) splits 4 ways, (2, 50, 3072) 8 ways; d = 384
+    with a wide vocabulary is a model shape outside skv_linear_packed), and
     every 16-column tile's candidate the first maximum of its columns (a tie
     across tiles, a NaN column that never wins, a ragged last tile, a row
     with its maximum in the last column); skv_next_embed over the
@@ -323,14 +324,15 @@ def test_linear_cand_matches_skv_linear_and_argmax(gpu_ctx, M, N, K):
     assert np.isnan(yh[:, 7]).all()
     cv = cand[:M * G].cpu().numpy().reshape(M, G)
     ci = cand[M * G:].cpu().view(torch.int32).numpy().reshape(M, G)
-    for m in range(M):
-        for j in range(G):
-            t = yh[m, 16 * j:16 * j + 16]
-            if np.isnan(t).all():
-                assert cv[m, j] == -np.inf and ci[m, j] == N
-                continue
-            k = int(np.nanargmax(t))
-            assert ci[m, j] == 16 * j + k and cv[m, j] == t[k], (m, j)
+    # per tile: the first maximum, NaN excluded (padded past N: never a winner)
+    yp = np.full((M, G * 16), np.nan, np.float32)
+    yp[:, :N] = yh
+    t = yp.reshape(M, G, 16)
+    none = np.isnan(t).all(axis=2)
+    k = np.nanargmax(np.where(none[..., None], 0.0, t), axis=2)
+    np.testing.assert_array_equal(ci, np.where(none, N, 16 * np.arange(G)[None, :] + k))
+    np.testing.assert_array_equal(
+        cv, np.where(none, -np.inf, np.take_along_axis(t, k[..., None], axis=2)[..., 0]))
     want = np.array([int(np.nanargmax(row)) for row in yh])
     assert want[0] == 5
     if M > 1:
