@@ -368,11 +368,22 @@ int skv_argmax(int32_t* out, const float* x, int M, int N, void* ws, size_t ws_b
  * probs_out (may be NULL): [M, V] fp32, the filtered distribution the draw
  * used (one-hot for greedy). Disabled filters: top_k = 0, top_p >= 1,
  * min_p = 0, repetition_penalty = 1.
+ * ws (may be NULL; 8-byte aligned) of skv_sample_workspace_bytes(M, V)
+ * bytes: an unfiltered draw (temperature > 0, no min-p, top-k or top-p, no
+ * probs_out; the penalty allowed) from rows of 8192 entries or more then
+ * runs split over 2048-entry slices (two launches, many workgroups per row)
+ * instead of one workgroup per row; its running sums are grouped by slice,
+ * so a u * sum within float rounding of a step may draw the neighbouring
+ * token. Calls that share ws must be stream ordered.
  */
 int skv_sample(int32_t* out, float* probs_out, const float* logits, const int32_t* seq,
                int seq_stride, const int32_t* lens, int M, int V, float temperature, int top_k,
                float top_p, float min_p, float repetition_penalty, int repetition_window,
-               unsigned long long seed, skv_stream_t stream);
+               unsigned long long seed, void* ws, size_t ws_bytes, skv_stream_t stream);
+
+/* Workspace of skv_sample's split path: M * ceil(V / 2048) * 8 bytes for
+ * 8192 <= V <= 65536, else 0 (the one-workgroup-per-row kernel). */
+size_t skv_sample_workspace_bytes(int M, int V);
 
 /* Next input token of each sequence (generate.py:29-69 with a cache):
  * ids[b] = prompt[b, pos[b]] while pos[b] < prompt_len[b], else

@@ -517,15 +517,196 @@ __global__ __launch_bounds__(NT) void k_sample(SampArgs a) {
 #undef SKV_KEEP_TOP_TIES
 #undef SKV_EACH
 
+// ---- split rows: unfiltered draws from wide rows ----------------------------
+// Without the min-p, top-k and top-p filters (the reference's defaults,
+// generate.py:8-18) a draw needs only each row's softmax sum and one pass
+// over the stretch where the running sum crosses u * sum. A row of 8192 or
+// more entries is cut into slices of kSliceV entries, one workgroup each:
+// k_sample_slices writes the slice's max and its sum of exp(x - max) (after
+// the penalty and the temperature, fixed order); then k_sample_pick, one
+// workgroup per row, weighs the slices by exp(max - row max) in slice order,
+// finds the slice where the running sum crosses u * sum, recomputes that
+// slice's entries alone and takes the first index, in index order, whose
+// running sum exceeds the target: the rule of k_sample, with the sums
+// grouped by slice (a draw within float rounding of a step of the running
+// sum may differ from k_sample's). A row of 50,304 entries is then 25
+// workgroups reading 8 KB each instead of one reading 200 KB at one CU's rate.
+constexpr int kSliceThreads = 256;
+constexpr int kSliceEPT = 8;                         // entries per thread
+constexpr int kSliceV = kSliceThreads * kSliceEPT;  // 2048
+constexpr int kSplitMinV = 8192;
+constexpr int kMaxSlices = kSampMaxV / kSliceV;     // 32
+
+// Penalty marks of the slice [lo, lo + kSliceV) of row m: bit j of mark is
+// set when token lo + j (< V) is among the row's last `window` tokens.
+__device__ void slice_marks(const SampArgs& a, int m, int L, int lo, uint32_t* mark) {
+  const int t = threadIdx.x;
+  if (t < kSliceV / 32) mark[t] = 0u;
+  __syncthreads();
+  for (int p = max(0, L - a.window) + t; p < L; p += kSliceThreads) {
+    const int tok = a.seq[(size_t)m * a.seq_stride + p];
+    const int j = tok - lo;
+    if (tok >= 0 && tok < a.V && j >= 0 && j < kSliceV) atomicOr(&mark[j >> 5], 1u << (j & 31));
+  }
+  __syncthreads();
+}
+
+// Grid (S, M): stats[m][s] = (max, sum of exp(x - max)) of slice s of row m,
+// x = logit (/ penalty) / temperature; a slice with no finite entry gives
+// (-inf, 0). Thread t holds entries lo + j * 256 + t (coalesced loads).
+__global__ __launch_bounds__(kSliceThreads) void k_sample_slices(SampArgs a,
+                                                                 float2* __restrict__ stats,
+                                                                 int S) {
+  __shared__ uint32_t mark[kSliceV / 32];
+  __shared__ float sh[kSliceThreads / 64];
+  const int s = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+  const int V = a.V, lo = s * kSliceV;
+  const float* row = a.logits + (size_t)m * V;
+  float x[kSliceEPT];
+#pragma unroll
+  for (int j = 0; j < kSliceEPT; ++j) {
+    const int i = lo + j * kSliceThreads + t;
+    const float y = row[min(i, V - 1)];
+    x[j] = i < V ? y : -INFINITY;
+  }
+  if (a.penalty != 1.f && a.window > 0) {
+    slice_marks(a, m, min(max(a.lens[m], 0), a.seq_stride), lo, mark);
+#pragma unroll
+    for (int j = 0; j < kSliceEPT; ++j) {
+      const int k = j * kSliceThreads + t;
+      if ((mark[k >> 5] >> (k & 31)) & 1u) x[j] = x[j] / a.penalty;
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kSliceEPT; ++j) {
+    x[j] = x[j] / a.temperature;
+    mx = fmaxf(mx, x[j]);
+  }
+  mx = block_maxf(mx, sh);
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < kSliceEPT; ++j) sum += x[j] == -INFINITY ? 0.f : expf(x[j] - mx);
+  sum = block_sumf(sum, sh);
+  if (t == 0) stats[(size_t)m * S + s] = make_float2(mx, sum);
+}
+
+// Grid (M): the draw of row m from the slice statistics (see above). Thread
+// t of the picked slice holds its entries lo + 8 t .. lo + 8 t + 7 (index
+// order within the thread, then across threads).
+__global__ __launch_bounds__(kSliceThreads) void k_sample_pick(SampArgs a,
+                                                               const float2* __restrict__ stats,
+                                                               int S) {
+  __shared__ uint32_t mark[kSliceV / 32];
+  __shared__ float sh[kSliceThreads / 64];
+  __shared__ float s_w[kMaxSlices], s_mx[kMaxSlices];
+  __shared__ int s_i[kSliceThreads / 64];
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int V = a.V;
+  const int L = min(max(a.lens[m], 0), a.seq_stride);
+  const float2 st = t < S ? stats[(size_t)m * S + t] : make_float2(-INFINITY, 0.f);
+  const float rmax = block_maxf(st.x, sh);
+  if (t < S) {
+    s_mx[t] = st.x;
+    // a slice without mass weighs 0 (also when no slice has any: rmax = -inf);
+    // a NaN sum stays NaN
+    s_w[t] = st.y == 0.f ? 0.f : st.y * expf(st.x - rmax);
+  }
+  __syncthreads();
+  float total = 0.f;
+  for (int q = 0; q < S; ++q) total += s_w[q];
+  const float target = splitmix_uniform(a.seed, m, L) * total;
+  int sel = -1;
+  float base = 0.f;
+  {
+    float run = 0.f;
+    for (int q = 0; q < S; ++q) {
+      if (sel < 0 && run + s_w[q] > target) {
+        sel = q;
+        base = run;
+      }
+      run += s_w[q];
+    }
+    if (sel < 0 && total == total) {  // rounding put the target at the very end
+      for (int q = 0; q < S; ++q)
+        if (s_w[q] > 0.f) {
+          sel = q;
+          base = run - s_w[q];  // not exact: only the last entry can then match
+        }
+    }
+  }
+  int tok = 0;  // no mass, or a NaN anywhere in the row: token 0, as k_sample
+  if (sel >= 0) {  // uniform
+    const int lo = sel * kSliceV;
+    const float* row = a.logits + (size_t)m * V;
+    const bool pen = a.penalty != 1.f && a.window > 0;
+    if (pen) slice_marks(a, m, L, lo, mark);
+    const float smx = s_mx[sel], scale = expf(smx - rmax);
+    float p[kSliceEPT];
+    float mine = 0.f;
+#pragma unroll
+    for (int j = 0; j < kSliceEPT; ++j) {
+      const int k = kSliceEPT * t + j, i = lo + k;
+      float x = row[min(i, V - 1)];
+      if (pen && ((mark[k >> 5] >> (k & 31)) & 1u)) x = x / a.penalty;
+      x = x / a.temperature;
+      p[j] = (i < V && x != -INFINITY) ? expf(x - smx) * scale : 0.f;
+      mine += p[j];
+    }
+    float all;
+    float r = base + block_excl_scan<float>(mine, sh, &all);
+    int found = 0x7fffffff, last = -1;
+#pragma unroll
+    for (int j = 0; j < kSliceEPT; ++j) {
+      const int i = lo + kSliceEPT * t + j;
+      if (p[j] > 0.f) {
+        if (found == 0x7fffffff && r <= target && target < r + p[j]) found = i;
+        last = i;
+      }
+      r += p[j];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      found = min(found, __shfl_xor(found, o));
+      last = max(last, __shfl_xor(last, o));
+    }
+    __syncthreads();
+    if (lane == 0) s_i[w] = found;
+    __syncthreads();
+    int f = 0x7fffffff;
+    for (int q = 0; q < kSliceThreads / 64; ++q) f = min(f, s_i[q]);
+    __syncthreads();
+    if (lane == 0) s_i[w] = last;
+    __syncthreads();
+    int lst = -1;
+    for (int q = 0; q < kSliceThreads / 64; ++q) lst = max(lst, s_i[q]);
+    // no crossing inside the slice (its recomputed sum fell short of the
+    // target by rounding): its last entry with mass
+    tok = f != 0x7fffffff ? f : (lst >= 0 ? lst : 0);
+  }
+  if (t == 0) a.out[m] = tok;
+}
+
+// Slices of a row for the split path, 0 when the row takes k_sample.
+int sample_slices(int V) {
+  return V >= kSplitMinV && V <= kSampMaxV ? (V + kSliceV - 1) / kSliceV : 0;
+}
+
 }  // namespace
 }  // namespace skv
 
 using namespace skv;
 
+extern "C" size_t skv_sample_workspace_bytes(int M, int V) {
+  const int S = sample_slices(V);
+  return M > 0 && S > 0 ? (size_t)M * S * sizeof(float2) : 0;
+}
+
 extern "C" int skv_sample(int32_t* out, float* probs_out, const float* logits, const int32_t* seq,
                           int seq_stride, const int32_t* lens, int M, int V, float temperature,
                           int top_k, float top_p, float min_p, float repetition_penalty,
-                          int repetition_window, unsigned long long seed, skv_stream_t stream) {
+                          int repetition_window, unsigned long long seed, void* ws,
+                          size_t ws_bytes, skv_stream_t stream) {
   const char* fn = "skv_sample";
   SKV_REQUIRE(out && logits && seq && lens, SKV_E_INVALID, "%s: null pointer argument", fn);
   SKV_REQUIRE(M > 0 && V > 0 && seq_stride > 0, SKV_E_INVALID, "%s: dims must be > 0", fn);
@@ -536,11 +717,20 @@ extern "C" int skv_sample(int32_t* out, float* probs_out, const float* logits, c
               SKV_E_INVALID, "%s: bad filter parameters", fn);
   SampArgs a{out, probs_out, logits, seq, seq_stride, lens, M, V, temperature, top_k, top_p,
              min_p, repetition_penalty, repetition_window, seed};
+  hipStream_t s = (hipStream_t)stream;
+  // Unfiltered draws from wide rows: the split path, given the workspace.
+  const int S = sample_slices(V);
+  if (temperature > 0.f && top_k == 0 && top_p >= 1.f && min_p == 0.f && probs_out == nullptr &&
+      S > 0 && ws != nullptr && ws_bytes >= skv_sample_workspace_bytes(M, V)) {
+    float2* stats = static_cast<float2*>(ws);
+    hipLaunchKernelGGL(k_sample_slices, dim3(S, M), dim3(kSliceThreads), 0, s, a, stats, S);
+    hipLaunchKernelGGL(k_sample_pick, dim3(M), dim3(kSliceThreads), 0, s, a, stats, S);
+    return check_launch(fn);
+  }
   // 1024 threads; entries per thread in registers (ER) and in LDS (EL):
   // 16 register columns fit without spilling, so rows up to 53248 entries
   // (GPT-2's 50304) keep 36 more columns in LDS; rows up to 65536 take 28
   // register columns and spill a little.
-  hipStream_t s = (hipStream_t)stream;
   const int per = (V + 1023) / 1024;
   if (per <= 4)
     hipLaunchKernelGGL((k_sample<4, 0, 1024>), dim3(M), dim3(1024), 0, s, a);

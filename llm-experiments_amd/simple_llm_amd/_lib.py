@@ -59,7 +59,8 @@ _SIGNATURES = {
     "skv_argmax_workspace_bytes": (_Z, [_I, _I]),
     "skv_argmax": (_I, [_P, _P, _I, _I, _P, _Z, _P]),
     "skv_sample": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _F, _I, _F, _F, _F, _I,
-                        ctypes.c_ulonglong, _P]),
+                        ctypes.c_ulonglong, _P, _Z, _P]),
+    "skv_sample_workspace_bytes": (_Z, [_I, _I]),
     "skv_flash_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
     "skv_flash_bwd_workspace_bytes": (_Z, [_I, _I, _I]),
     "skv_flash_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _Z,

@@ -132,6 +132,9 @@ class _Buffers:
         # skv_linear_cand's, whichever the model's sizes take
         cb = max(L.skv_linear_packed_cand_bytes(B), L.skv_linear_cand_bytes(B, vocab, d))
         self.cand = torch.zeros(max(cb // 4, 1), device=dev)
+        # slice statistics of skv_sample's split path (stream ordered)
+        self.samp_ws = torch.zeros(max(L.skv_sample_workspace_bytes(B, vocab), 8),
+                                   dtype=torch.uint8, device=dev)
 
 
 class _PrefillBuffers:
@@ -642,7 +645,7 @@ class Generator:
                                     self.seq.data_ptr(), self.seq.shape[1],
                                     c.layers[0].lens.data_ptr(), self.B,
                                     m.tm_params.vocab_size, T, k, p, mp, pen, win, self.seed,
-                                    s), "skv_sample")
+                                    bf.samp_ws.data_ptr(), bf.samp_ws.numel(), s), "skv_sample")
 
     def _one_step(self):
         L = _lib.lib()
@@ -744,7 +747,7 @@ class _WindowDecoder:
             _lib.check(L.skv_sample(bf.argmax.data_ptr(), None, bf.logits.data_ptr(),
                                     self.seq.data_ptr(), self.seq.shape[1], self.lens.data_ptr(),
                                     1, m.tm_params.vocab_size, T, k, p, mp, pen, win, self.seed,
-                                    s), "skv_sample")
+                                    bf.samp_ws.data_ptr(), bf.samp_ws.numel(), s), "skv_sample")
         return int(bf.argmax[0].item())
 
 

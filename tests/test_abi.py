@@ -141,7 +141,7 @@ def test_entry_points_reject_bad_arguments():
 def test_sample_rejects_bad_arguments():
     L = _lib.lib()
     fake = 4096  # never dereferenced: each call below fails validation first
-    args = [fake, None, fake, fake, 8, fake, 2, 100, 1.0, 0, 1.0, 0.0, 1.0, 64, 42, None]
+    args = [fake, None, fake, fake, 8, fake, 2, 100, 1.0, 0, 1.0, 0.0, 1.0, 64, 42, None, 0, None]
 
     def call(**kw):
         a = list(args)
@@ -154,6 +154,11 @@ def test_sample_rejects_bad_arguments():
     assert call(top_k=-3) == _lib.SKV_E_INVALID
     assert call(pen=0.0) == _lib.SKV_E_INVALID
     assert call(M=0) == _lib.SKV_E_INVALID
+    # the split path's workspace: rows of 8192..65536 entries, ceil(V / 2048) slices a row
+    assert L.skv_sample_workspace_bytes(16, 50304) == 16 * 25 * 8
+    assert L.skv_sample_workspace_bytes(3, 8192) == 3 * 4 * 8
+    assert L.skv_sample_workspace_bytes(3, 8191) == 0
+    assert L.skv_sample_workspace_bytes(3, 65537) == 0
 
 
 def test_flash_bwd_rejects_bad_arguments():

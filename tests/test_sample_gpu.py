@@ -27,7 +27,9 @@ def lib():
 
 
 def run_sample(logits, seq, lens, T=1.0, top_k=0, top_p=1.0, min_p=0.0, pen=1.0, window=64,
-               seed=42, probs=True):
+               seed=42, probs=True, ws=False):
+    """ws: pass skv_sample_workspace_bytes(M, V) bytes of workspace (the split
+    path of unfiltered draws from rows of >= 8192 entries, when probs is off)."""
     _lib = lib()
     L = _lib.lib()
     M, V = logits.shape
@@ -36,9 +38,12 @@ def run_sample(logits, seq, lens, T=1.0, top_k=0, top_p=1.0, min_p=0.0, pen=1.0,
     ln = torch.from_numpy(np.ascontiguousarray(lens, np.int32)).cuda()
     out = torch.full((M,), -7, dtype=torch.int32, device="cuda")
     pr = torch.full((M, V), float("nan"), device="cuda") if probs else None
+    wsb = L.skv_sample_workspace_bytes(M, V) if ws else 0
+    wst = torch.full((max(wsb, 8),), 0xFF, dtype=torch.uint8, device="cuda")  # stale bytes
     rc = L.skv_sample(out.data_ptr(), pr.data_ptr() if probs else None, lg.data_ptr(),
                       sq.data_ptr(), seq.shape[1], ln.data_ptr(), M, V, T, top_k, top_p, min_p,
-                      pen, window, seed, _lib.stream_handle())
+                      pen, window, seed, wst.data_ptr() if ws else None, wsb,
+                      _lib.stream_handle())
     _lib.check(rc, "skv_sample")
     return out.cpu().numpy(), (pr.cpu().numpy() if probs else None)
 
@@ -148,4 +153,90 @@ def test_draws_follow_the_distribution(gpu_ctx):
     want = so.sample_filter(row.astype(np.float64), 1.0, top_k=10)
     freq = np.bincount(tok, minlength=V) / M
     assert (freq[want == 0] == 0).all()
+    assert np.abs(freq - want).max() < 0.03
+
+
+SPLIT_CASES = [dict(T=1.0), dict(T=0.9, pen=1.3, window=64), dict(T=0.6, pen=0.7, window=200)]
+
+
+@pytest.mark.parametrize("V", [8192, 20000, 50304, 65536])
+@pytest.mark.parametrize("case", range(len(SPLIT_CASES)))
+def test_split_sample_matches_oracle(gpu_ctx, V, case):
+    """Unfiltered draws from wide rows on the split path (slice statistics,
+    then one workgroup per row): u * total lies within the drawn token's step
+    of the oracle's running sum (to 1e-5), and the token is the oracle's
+    inverse-CDF draw with the same u, and k_sample's, where u * total is not
+    within 1e-5 of a step; two calls give the same tokens."""
+    p = dict(pen=1.0, window=64)
+    p.update(SPLIT_CASES[case])
+    banner(f"split sample V={V} {p}")
+    L = lib().lib()
+    assert L.skv_sample_workspace_bytes(16, V) == 16 * ((V + 2047) // 2048) * 8
+    r = np.random.default_rng(V * 7 + case)
+    M, ctx = 16, 300
+    logits = (r.standard_normal((M, V)) * 2.5).astype(np.float32)
+    seq = r.integers(0, V, (M, ctx)).astype(np.int32)
+    lens = r.integers(1, ctx + 1, M)
+    seed = 99 + case
+    tok, _ = run_sample(logits, seq, lens, seed=seed, probs=False, ws=True, **p)
+    tok2, _ = run_sample(logits, seq, lens, seed=seed, probs=False, ws=True, **p)
+    one, _ = run_sample(logits, seq, lens, seed=seed, probs=False, ws=False, **p)
+    np.testing.assert_array_equal(tok, tok2)
+    for m in range(M):
+        want = oracle_row(logits[m], seq[m], int(lens[m]), p["T"], 0, 1.0, 0.0, p["pen"],
+                          p["window"])
+        u = so.splitmix_uniform(seed, m, int(lens[m]))
+        c = np.cumsum(want)
+        target = u * c[-1]
+        assert want[tok[m]] > 0
+        below = c[tok[m] - 1] if tok[m] > 0 else 0.0
+        assert below - 1e-5 <= target < c[tok[m]] + 1e-5, f"row {m}"
+        if np.abs(c - target).min() >= 1e-5:
+            assert tok[m] == so.sample_draw(want, u) == one[m], f"row {m}"
+
+
+def test_split_sample_edge_rows(gpu_ctx):
+    """Rows the split path must answer as k_sample does: no finite logit
+    (token 0), a NaN logit (token 0), a whole slice at -inf (never drawn),
+    the mass in the last entry of the last, ragged slice, and in entry 0."""
+    banner("split sample edge rows")
+    V, M = 20000, 6
+    r = np.random.default_rng(3)
+    logits = r.standard_normal((M, V)).astype(np.float32)
+    logits[0, :] = -np.inf
+    logits[1, 5] = np.nan
+    logits[2, 2048:4096] = -np.inf
+    logits[3, V - 1] = 200.0
+    logits[4, 0] = 200.0
+    seq = np.zeros((M, 4), np.int32)
+    lens = np.arange(1, M + 1)
+    for seed in (1, 2, 3):
+        tok, _ = run_sample(logits, seq, lens, seed=seed, probs=False, ws=True)
+        one, _ = run_sample(logits, seq, lens, seed=seed, probs=False, ws=False)
+        assert tok[0] == 0 and tok[1] == 0 and tok[3] == V - 1 and tok[4] == 0
+        assert not 2048 <= tok[2] < 4096
+        np.testing.assert_array_equal(tok[[0, 1, 3, 4]], one[[0, 1, 3, 4]])
+        want = so.sample_filter(logits[2].astype(np.float64), 1.0)
+        u = so.splitmix_uniform(seed, 2, 3)
+        if np.abs(np.cumsum(want) - u).min() >= 1e-5:
+            assert tok[2] == so.sample_draw(want, u) == one[2]
+
+
+def test_split_draws_follow_the_distribution(gpu_ctx):
+    """Many rows with the same logits and different positions, the mass
+    spread over entries of different slices: the split path's draw
+    frequencies follow the softmax (the slices are weighted correctly)."""
+    banner("split sample frequencies")
+    V, M = 8192, 3000
+    r = np.random.default_rng(11)
+    row = np.full(V, -30.0, np.float32)
+    hot = np.array([3, 2047, 2048, 4000, 4095, 6000, 8191])
+    row[hot] = r.standard_normal(len(hot)).astype(np.float32)
+    logits = np.tile(row, (M, 1))
+    seq = np.zeros((M, 1), np.int32)
+    lens = np.ones(M, np.int32)
+    tok, _ = run_sample(logits, seq, lens, T=1.0, probs=False, ws=True, seed=13)
+    want = so.sample_filter(row.astype(np.float64), 1.0)
+    freq = np.bincount(tok, minlength=V) / M
+    assert np.isin(tok, hot).all()
     assert np.abs(freq - want).max() < 0.03
