@@ -63,10 +63,12 @@ B, H, D, T_CAP, FILL = 4, 16, 128, 32768, 32000
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--workload", choices=["c4", "c1", "c2", "c3", "c5", "fb"], default="c4",
+    p.add_argument("--workload", choices=["c4", "c1", "c2", "c3", "c5", "fb", "sample"],
+                   default="c4",
                    help="BASELINE config: c4 (default, the headline line), c1 tiny LM "
                         "generate, c2 fp32 KV microbench, c3 GPT-2-small ragged batch, "
-                        "c5 GQA paged ragged decode; fb: flash-attention backward (fp32)")
+                        "c5 GQA paged ragged decode; fb: flash-attention backward (fp32); "
+                        "sample: next-token sampling at the C3 shape")
     p.add_argument("--steps", type=int, default=256)
     p.add_argument("--warmup", type=int, default=16)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -734,6 +736,82 @@ def run_fb(args, ctx):
         roof, cpu, forward=forward)
 
 
+def run_sample(args, ctx):
+    """Next-token sampling at the C3 decode shape: 16 rows of 50,304 fp32
+    logits with the reference's default parameters (temperature 1, no min-p,
+    top-k or top-p, no penalty: generate.py:8-18), one skv_sample call per
+    step with the split-row workspace (a new seed each call); the
+    one-workgroup-per-row kernel (no workspace) is timed the same way
+    beside it."""
+    import numpy as np
+    import torch
+
+    from simple_llm_amd import _lib
+
+    M, V, CTX = 16, 50304, 1024
+    dev = ctx.device
+    g = torch.Generator(device=dev).manual_seed(5)
+    logits = torch.randn((M, V), generator=g, device=dev) * 2.5
+    seq = torch.randint(0, V, (M, CTX), generator=g, device=dev, dtype=torch.int32)
+    lens = torch.full((M,), 512, dtype=torch.int32, device=dev)
+    out = torch.zeros(M, dtype=torch.int32, device=dev)
+    L = _lib.lib()
+    wsb = L.skv_sample_workspace_bytes(M, V)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def call(split, seed):
+        _lib.check(L.skv_sample(out.data_ptr(), None, logits.data_ptr(), seq.data_ptr(), CTX,
+                                lens.data_ptr(), M, V, 1.0, 0, 1.0, 0.0, 1.0, 64, seed,
+                                ws.data_ptr() if split else None, wsb if split else 0, stream),
+                   "skv_sample")
+
+    def timed(split):
+        for i in range(args.warmup):
+            call(split, i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for i in range(args.steps):
+            call(split, i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / args.steps, time.perf_counter() - t0
+
+    one_s, _ = timed(False)
+    call_s, wall = timed(True)
+    # the logits once, and the picked 2048-entry slice of each row again
+    nbytes = M * V * 4 + M * 2048 * 4
+    roof = {"bound": "launch latency", "achieved": nbytes / call_s / 1e9, "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": nbytes / call_s / 1e9 / HBM_PEAK_GBS, "traffic": None,
+            "kernel": "skv_sample split path (k_sample_slices + k_sample_pick), HIP events",
+            "mean_call_us": call_s * 1e6, "algorithmic_bytes": nbytes,
+            "note": "two launches of ~3 MB: each at the per-kernel floor"}
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the oracle's restatement of sample_token (float64 numpy), row by row
+        from oracle import sample_oracle as so
+        lg = logits.cpu().numpy().astype(np.float64)
+        n, t0 = 0, time.perf_counter()
+        while n == 0 or time.perf_counter() - t0 < min(args.cpu_seconds, 5.0):
+            m = n % M
+            so.sample_draw(so.sample_filter(lg[m], 1.0), so.splitmix_uniform(n, m, 512))
+            n += 1
+        dt = time.perf_counter() - t0
+        cpu = {"value": n / dt, "unit": "draws/s", "cores": 1, "kind": "port",
+               "sample": f"{n} draws from 50,304-entry rows by oracle/sample_oracle.py "
+                         f"(numpy float64 softmax + inverse-CDF draw), {dt:.1f} s"}
+    return _record(
+        "sampled draws/sec", M * args.steps / wall, "draws/s", args.steps, args.warmup,
+        wall / args.steps * 1e3, "fp32",
+        {"workload": "sampling at the C3 shape: 16 rows x 50,304 fp32 logits, temperature 1, "
+                     "no min-p/top-k/top-p, no penalty (the reference's defaults)",
+         "batch": M, "vocab": V},
+        roof, cpu, one_workgroup_per_row={"mean_call_us": one_s * 1e6,
+                                          "kernel": "k_sample, one 1024-thread workgroup a row"})
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -751,7 +829,7 @@ def main():
         ctx = gpu.context_create()
         ctx.config.decode_chunk_tokens = args.chunk_tokens
         rec = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c5": run_c5,
-               "fb": run_fb}[args.workload](args, ctx)
+               "fb": run_fb, "sample": run_sample}[args.workload](args, ctx)
         print(json.dumps(rec), flush=True)
         return
     if FILL + args.steps > T_CAP or args.steps < 1 or args.warmup < 0:
