@@ -388,10 +388,19 @@ size_t skv_sample_workspace_bytes(int M, int V);
 /* Next input token of each sequence (generate.py:29-69 with a cache):
  * ids[b] = prompt[b, pos[b]] while pos[b] < prompt_len[b], else
  * argmax_prev[b]; the token is also stored at seq[b, pos[b]] when
- * pos[b] < seq_cap. pos is the sequence's current fill (layer 0's lens). */
+ * 0 <= pos[b] < seq_cap. pos is the sequence's current fill (layer 0's
+ * lens). stop (may be NULL; then lens_all and n_layers are unused): per
+ * row, the length it is generated to. Once the token at position
+ * stop[b] - 1 is recorded, the row retires: lens_all[l * B + b] = -1 for
+ * every layer l < n_layers (lens_all: the n_layers per-layer fill arrays,
+ * contiguous, pos being the first). The decode kernels treat a negative
+ * fill as an empty row (no append, no advance, zero output), and the
+ * next-token calls record nothing for it, so a batch whose rows end at
+ * different lengths stops reading the cache of the rows that are done. */
 int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                     const int32_t* prompt, const int32_t* prompt_len, const int32_t* pos, int B,
-                    int max_prompt, int seq_cap, skv_stream_t stream);
+                    int max_prompt, int seq_cap, const int32_t* stop, int32_t* lens_all,
+                    int n_layers, skv_stream_t stream);
 
 /* Bytes of skv_linear_packed's argmax candidates for M rows: [M][256]
  * float values, then [M][256] int32 columns (one per workgroup). */
@@ -424,14 +433,16 @@ size_t skv_linear_cand_bytes(int M, int N, int K);
  * columns, as skv_linear_packed and skv_linear_cand write them; a row of
  * NaN only gives token 0), else argmax_prev[b]. Then ids[b] and seq as skv_next_tokens, and, when
  * embedding is not NULL, x[b, :] = embedding[ids[b], :] + pos_table[pos[b], :]
- * as skv_embed (ids and positions clamped into the tables). No counterpart
+ * as skv_embed (ids and positions clamped into the tables); stop, lens_all
+ * and n_layers retire finished rows as in skv_next_tokens. No counterpart
  * in the reference, whose generate loop picks and embeds on the host side
  * (generate.py:29-69, jax_backend.py:144, 466-469). */
 int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                    const float* cand, int n_cand, const int32_t* prompt,
                    const int32_t* prompt_len, const int32_t* pos, int B, int max_prompt,
                    int seq_cap, const float* embedding, const float* pos_table, int d, int vocab,
-                   int ctx, skv_stream_t stream);
+                   int ctx, const int32_t* stop, int32_t* lens_all, int n_layers,
+                   skv_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Training-side attention in fp32: causal FlashAttention forward and backward.

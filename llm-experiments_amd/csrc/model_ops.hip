@@ -1055,20 +1055,34 @@ __global__ __launch_bounds__(64) void k_argmax_pick(int32_t* __restrict__ out,
 // sequence is still inside its prompt, else the previous step's argmax. The
 // chosen token is also recorded at its position in the sequence buffer.
 // ---------------------------------------------------------------------------
+// Retirement of a finished row (stop given): once the token at position
+// stop[b] - 1 is recorded, every layer's fill of row b becomes -1, which the
+// decode kernels treat as an empty row with no append and no advance, and
+// the next-token kernels as a row that records nothing: the rest of the
+// batch's steps read none of its cache.
+__device__ __forceinline__ void retire_row(const int32_t* __restrict__ stop,
+                                           int32_t* __restrict__ lens_all, int n_layers, int B,
+                                           int b, int p) {
+  if (stop != nullptr && p >= 0 && p >= stop[b] - 1)
+    for (int li = 0; li < n_layers; ++li) lens_all[(size_t)li * B + b] = -1;
+}
+
 __global__ void k_next_tokens(int32_t* __restrict__ ids, int32_t* __restrict__ seq,
                               const int32_t* __restrict__ argmax_prev,
                               const int32_t* __restrict__ prompt,
                               const int32_t* __restrict__ prompt_len,
                               const int32_t* __restrict__ pos, int B, int max_prompt,
-                              int seq_cap) {
+                              int seq_cap, const int32_t* __restrict__ stop,
+                              int32_t* __restrict__ lens_all, int n_layers) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
   const int p = pos[b];
   int t;
-  if (p < prompt_len[b]) t = prompt[(size_t)b * max_prompt + min(p, max_prompt - 1)];
+  if (p < prompt_len[b]) t = prompt[(size_t)b * max_prompt + min(max(p, 0), max_prompt - 1)];
   else t = argmax_prev[b];
   ids[b] = t;
   if (p >= 0 && p < seq_cap) seq[(size_t)b * seq_cap + p] = t;
+  retire_row(stop, lens_all, n_layers, B, b, p);
 }
 
 // k_next_tokens and k_embed in one launch, with the argmax's last step: row
@@ -1081,7 +1095,8 @@ __global__ __launch_bounds__(256) void k_next_embed(
     const int32_t* __restrict__ argmax_prev, const float* __restrict__ cand, int n_cand,
     const int32_t* __restrict__ prompt, const int32_t* __restrict__ prompt_len,
     const int32_t* __restrict__ pos, int B, int max_prompt, int seq_cap,
-    const float* __restrict__ emb, const float* __restrict__ pe, int d, int vocab, int ctx) {
+    const float* __restrict__ emb, const float* __restrict__ pe, int d, int vocab, int ctx,
+    const int32_t* __restrict__ stop, int32_t* __restrict__ lens_all, int n_layers) {
   __shared__ int s_t;
   __shared__ float s_bv[4];
   __shared__ int s_bi[4];
@@ -1131,6 +1146,7 @@ __global__ __launch_bounds__(256) void k_next_embed(
     ids[b] = t;
     if (p >= 0 && p < seq_cap) seq[(size_t)b * seq_cap + p] = t;
     s_t = t;
+    retire_row(stop, lens_all, n_layers, B, b, p);
   }
   if (emb == nullptr) return;  // uniform
   __syncthreads();
@@ -1474,9 +1490,12 @@ extern "C" int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_
                               const int32_t* prompt_len, const int32_t* pos, int B,
                               int max_prompt, int seq_cap, const float* embedding,
                               const float* pos_table, int d, int vocab, int ctx,
+                              const int32_t* stop, int32_t* lens_all, int n_layers,
                               skv_stream_t stream) {
   SKV_REQUIRE(ids && seq && prompt && prompt_len && pos, SKV_E_INVALID,
               "skv_next_embed: null pointer argument");
+  SKV_REQUIRE(stop == nullptr || (lens_all != nullptr && n_layers > 0), SKV_E_INVALID,
+              "skv_next_embed: retiring rows needs lens_all and n_layers > 0");
   SKV_REQUIRE(B > 0 && max_prompt > 0 && seq_cap > 0 && vocab > 0 && n_cand >= 0, SKV_E_INVALID,
               "skv_next_embed: bad sizes");
   SKV_REQUIRE(n_cand > 0 ? cand != nullptr : argmax_prev != nullptr, SKV_E_INVALID,
@@ -1485,19 +1504,23 @@ extern "C" int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_
               "skv_next_embed: embedding needs x, pos_table, d and ctx");
   hipLaunchKernelGGL(k_next_embed, dim3(B), dim3(256), 0, (hipStream_t)stream, x, ids, seq,
                      argmax_prev, cand, n_cand, prompt, prompt_len, pos, B, max_prompt, seq_cap,
-                     embedding, pos_table, d, vocab, ctx);
+                     embedding, pos_table, d, vocab, ctx, stop, lens_all, n_layers);
   return check_launch("skv_next_embed");
 }
 
 extern "C" int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                                const int32_t* prompt, const int32_t* prompt_len,
                                const int32_t* pos, int B, int max_prompt, int seq_cap,
+                               const int32_t* stop, int32_t* lens_all, int n_layers,
                                skv_stream_t stream) {
   SKV_REQUIRE(ids && seq && argmax_prev && prompt && prompt_len && pos, SKV_E_INVALID,
               "skv_next_tokens: null pointer argument");
   SKV_REQUIRE(B > 0 && max_prompt > 0 && seq_cap > 0, SKV_E_INVALID,
               "skv_next_tokens: dims must be > 0");
+  SKV_REQUIRE(stop == nullptr || (lens_all != nullptr && n_layers > 0), SKV_E_INVALID,
+              "skv_next_tokens: retiring rows needs lens_all and n_layers > 0");
   hipLaunchKernelGGL(k_next_tokens, dim3((B + 255) / 256), dim3(256), 0, (hipStream_t)stream, ids,
-                     seq, argmax_prev, prompt, prompt_len, pos, B, max_prompt, seq_cap);
+                     seq, argmax_prev, prompt, prompt_len, pos, B, max_prompt, seq_cap, stop,
+                     lens_all, n_layers);
   return check_launch("skv_next_tokens");
 }

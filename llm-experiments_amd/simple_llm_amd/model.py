@@ -542,7 +542,8 @@ class Generator:
                  total_len: Sequence[int] | int, use_graph: bool = False,
                  temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
                  min_p: float = 0.0, repetition_penalty: float = 1.0,
-                 repetition_window: int = 64, seed: int = 42, fused_tail: bool = True):
+                 repetition_window: int = 64, seed: int = 42, fused_tail: bool = True,
+                 retire_rows: bool = True):
         tm = model.tm_params
         self.model = model
         B = len(prompts)
@@ -577,6 +578,15 @@ class Generator:
         self.prompt_len = torch.from_numpy(plen).to(dev)
         self.seq = torch.zeros((B, tm.context_size), dtype=torch.int32, device=dev)
         self.cache = model.new_cache(B)
+        # Every layer's fills in one [n_layers, B] array, so that the step's
+        # next-token kernel can retire a row once its last token is recorded
+        # (all its fills to -1: the decode kernels then skip it); the rows of
+        # a ragged batch that are done stop costing attention reads.
+        self.retire = bool(retire_rows)
+        self.lens_all = torch.zeros((tm.n_layers, B), dtype=torch.int32, device=dev)
+        for li, layer in enumerate(self.cache.layers):
+            layer.lens = self.lens_all[li]
+        self.stop = torch.from_numpy(tot.astype(np.int32)).to(dev)
         self.bufs = model.buffers(B)
         # decode steps after the prefill: the step at position p produces token p + 1
         self.steps = max(int((tot - 1 - plen).max()), 0)
@@ -625,7 +635,15 @@ class Generator:
                                     c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
                                     self.seq.shape[1], m.emb.data_ptr() if embed else None,
                                     m.pe.data_ptr() if embed else None, tm.embedding_dim,
-                                    tm.vocab_size, m.pe.shape[0], s), "skv_next_embed")
+                                    tm.vocab_size, m.pe.shape[0], *self._retire_args(), s),
+                   "skv_next_embed")
+
+    def _retire_args(self):
+        """(stop, lens_all, n_layers) of the next-token calls: retire finished
+        rows, or nothing."""
+        if not self.retire:
+            return None, None, 0
+        return self.stop.data_ptr(), self.lens_all.data_ptr(), self.lens_all.shape[0]
 
     def _pick(self) -> None:
         """Next token of every sequence from the logits buffer into argmax."""
@@ -662,7 +680,8 @@ class Generator:
         _lib.check(L.skv_next_tokens(bf.ids.data_ptr(), self.seq.data_ptr(), bf.argmax.data_ptr(),
                                      self.prompt.data_ptr(), self.prompt_len.data_ptr(),
                                      c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
-                                     self.seq.shape[1], s), "skv_next_tokens")
+                                     self.seq.shape[1], *self._retire_args(), s),
+                   "skv_next_tokens")
         m._launch_step(c, bf)
         self._pick()
 
@@ -673,8 +692,10 @@ class Generator:
         self._pick()
 
     def run(self) -> List[List[int]]:
-        """Prefill, then all decode steps; returns every sequence's tokens
-        (prompt + output)."""
+        """From the start (reset(): an empty cache, the prompts only), the
+        prefill, then all decode steps; returns every sequence's tokens
+        (prompt + output). Repeated calls reuse the captured graph."""
+        self.reset()
         self.prefill()
         steps = self.steps
         if steps > 0:
@@ -702,8 +723,8 @@ class Generator:
                                          self.bufs.argmax.data_ptr(), self.prompt.data_ptr(),
                                          self.prompt_len.data_ptr(),
                                          self.cache.layers[0].lens.data_ptr(), self.B,
-                                         self.prompt.shape[1], self.seq.shape[1], s),
-                       "skv_next_tokens")
+                                         self.prompt.shape[1], self.seq.shape[1],
+                                         *self._retire_args(), s), "skv_next_tokens")
         for layer in self.cache.layers:
             layer.host_lens = layer.lens.cpu().numpy().astype(np.int64)
         seq = self.seq.cpu().numpy()

@@ -329,11 +329,12 @@ def test_step_entry_points_reject_bad_arguments():
 
     def ne(**kw):
         a = dict(x=fake, argmax_prev=fake, cand=None, n_cand=0, B=4, emb=fake, d=64, vocab=100,
-                 ctx=32)
+                 ctx=32, stop=None, lens_all=None, n_layers=0)
         a.update(kw)
         return L.skv_next_embed(a["x"], fake, fake, a["argmax_prev"], a["cand"], a["n_cand"],
                                 fake, fake, fake, a["B"], 8, 64, a["emb"], fake, a["d"],
-                                a["vocab"], a["ctx"], None)
+                                a["vocab"], a["ctx"], a["stop"], a["lens_all"], a["n_layers"],
+                                None)
 
     assert ne(B=0) == _lib.SKV_E_INVALID
     assert ne(n_cand=-1) == _lib.SKV_E_INVALID
@@ -342,3 +343,9 @@ def test_step_entry_points_reject_bad_arguments():
     assert ne(argmax_prev=None) == _lib.SKV_E_INVALID
     assert ne(x=None) == _lib.SKV_E_INVALID  # an embedding needs x
     assert ne(d=0) == _lib.SKV_E_INVALID
+    # retiring rows needs every layer's fills
+    assert ne(stop=fake) == _lib.SKV_E_INVALID
+    assert ne(stop=fake, lens_all=fake, n_layers=0) == _lib.SKV_E_INVALID
+    assert b"retiring rows" in L.skv_last_error()
+    assert L.skv_next_tokens(fake, fake, fake, fake, fake, fake, 4, 8, 64, fake, None, 2,
+                             None) == _lib.SKV_E_INVALID

@@ -254,7 +254,8 @@ def test_packed_argmax_candidates_and_next_embed(gpu_ctx, M, N, K):
     _lib.check(L.skv_next_embed(xo.data_ptr(), ids.data_ptr(), seq.data_ptr(),
                                 argmax_prev.data_ptr(), cand.data_ptr(), n_cand,
                                 promptd.data_ptr(), plend.data_ptr(), posd.data_ptr(), M, 4, T,
-                                embd.data_ptr(), ped.data_ptr(), D, V, T, s), "skv_next_embed")
+                                embd.data_ptr(), ped.data_ptr(), D, V, T, None, None, 0, s),
+               "skv_next_embed")
     tok = want.copy()
     tok[M - 1] = 11  # pos < prompt_len: the prompt token
     np.testing.assert_array_equal(ids.cpu().numpy(), tok)
@@ -266,7 +267,7 @@ def test_packed_argmax_candidates_and_next_embed(gpu_ctx, M, N, K):
     xo.zero_()
     _lib.check(L.skv_next_embed(None, ids.data_ptr(), seq.data_ptr(), argmax_prev.data_ptr(),
                                 None, 0, promptd.data_ptr(), plend.data_ptr(), posd.data_ptr(), M,
-                                4, T, None, None, D, V, T, s), "skv_next_embed")
+                                4, T, None, None, D, V, T, None, None, 0, s), "skv_next_embed")
     tok2 = np.arange(M) + 1000
     tok2[M - 1] = 11
     np.testing.assert_array_equal(ids.cpu().numpy(), tok2)
@@ -345,7 +346,7 @@ def test_linear_cand_matches_skv_linear_and_argmax(gpu_ctx, M, N, K):
     prompt = dev(np.zeros((M, 4), np.int32))
     _lib.check(L.skv_next_embed(None, ids.data_ptr(), seq.data_ptr(), None, cand.data_ptr(), G,
                                 prompt.data_ptr(), plen.data_ptr(), pos.data_ptr(), M, 4, T, None,
-                                None, 0, N, T, s), "skv_next_embed")
+                                None, 0, N, T, None, None, 0, s), "skv_next_embed")
     np.testing.assert_array_equal(ids.cpu().numpy(), want)
     np.testing.assert_array_equal(seq.cpu().numpy()[:, 2], want)
 
@@ -484,10 +485,24 @@ def test_next_tokens(gpu_ctx):
     p_d, pl_d, pos_d, a_d = dev(prompt), dev(plen), dev(pos), dev(arg)
     _lib.check(_lib.lib().skv_next_tokens(ids.data_ptr(), seq.data_ptr(), a_d.data_ptr(),
                                           p_d.data_ptr(), pl_d.data_ptr(), pos_d.data_ptr(), 3, 4,
-                                          8, _lib.stream_handle()), "next")
+                                          8, None, None, 0, _lib.stream_handle()), "next")
     assert ids.cpu().tolist() == [6, 71, 72]
     s = seq.cpu().numpy()
     assert s[0, 1] == 6 and s[1, 1] == 71 and not s[2].any()  # pos 9 >= cap 8: not recorded
+    # retirement: 3 layers' fills, layer 0's row the positions; stop = 3, 2, 7:
+    # row 1 records its last token (position 1 = stop - 1) and retires, row 0
+    # (position 1 < 2) goes on; row 2 retired before (-1) records nothing
+    lens_all = dev(np.array([[1, 1, -1], [1, 1, -1], [1, 1, -1]], np.int32))
+    stop = dev(np.array([3, 2, 7], np.int32))
+    seq.zero_()
+    _lib.check(_lib.lib().skv_next_tokens(ids.data_ptr(), seq.data_ptr(), a_d.data_ptr(),
+                                          p_d.data_ptr(), pl_d.data_ptr(), lens_all.data_ptr(), 3,
+                                          4, 8, stop.data_ptr(), lens_all.data_ptr(), 3,
+                                          _lib.stream_handle()), "next")
+    assert lens_all.cpu().numpy().tolist() == [[1, -1, -1]] * 3
+    s = seq.cpu().numpy()
+    assert s[0, 1] == 6 and s[1, 1] == 71 and not s[2].any()
+    assert ids.cpu().tolist()[2] == 1  # a retired row reads its first prompt token, in bounds
 
 
 # ---------------------------------------------------------------------------
@@ -727,6 +742,32 @@ def test_fused_step_tail_generates_the_same_tokens(gpu_ctx, vocab, d, heads):
     c = M.Generator(m, prompts, 70, use_graph=False).run()
     assert a == bb == c == a2
     assert all(len(o) == 70 and o[:len(p)] == p for o, p in zip(a, prompts))
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_retired_rows_keep_the_tokens(gpu_ctx, fused):
+    """A ragged batch whose rows end at different lengths: retiring each row
+    once its last token is recorded (every layer's fill to -1, so the decode
+    kernels skip it) gives the tokens of the run without retirement, graph-
+    replayed and eager, fused and unfused; the finished rows end retired and
+    nothing is recorded past a row's length."""
+    banner(f"retired rows, fused={fused}")
+    from simple_llm_amd import model as M
+    m, params = make_model(gpu_ctx, 300, 128, 4, 2, 96, seed=8, std=0.1)
+    r = np.random.default_rng(21)
+    prompts = [r.integers(0, 300, n).tolist() for n in (3, 40, 11, 25)]
+    tot = [90, 60, 96, 41]
+    g = M.Generator(m, prompts, tot, use_graph=True, fused_tail=fused)
+    a = g.run()
+    # every row records its last token at some call (the longest ones at the
+    # one after the last step) and retires there
+    assert (g.lens_all.cpu().numpy() == -1).all()
+    sq = g.seq.cpu().numpy()
+    assert not sq[1, 60:].any() and not sq[3, 41:].any()
+    b = M.Generator(m, prompts, tot, use_graph=True, fused_tail=fused, retire_rows=False).run()
+    c = M.Generator(m, prompts, tot, use_graph=False, fused_tail=fused).run()
+    assert a == b == c
+    assert [len(o) for o in a] == tot
 
 
 @pytest.mark.parametrize("temperature", [0.0, 0.8])
