@@ -536,6 +536,10 @@ class Generator:
     previous token (skv_next_tokens), so the loop never waits for the host.
     With use_graph the decode step is captured once into a HIP graph
     (torch.cuda.CUDAGraph over the library's launches) and replayed.
+    With retire_rows (the default) a sequence is retired once its last token
+    is recorded: every layer's fill of its row becomes -1, so the remaining
+    steps read none of its cache (the fills in self.cache read -1 after
+    run(); run() starts from reset() each time).
     """
 
     def __init__(self, model: TransformerModel, prompts: Sequence[Sequence[int]],
