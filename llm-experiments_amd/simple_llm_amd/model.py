@@ -622,6 +622,7 @@ class Generator:
         # with candidates, skv_next_embed reads the previous step's, or the
         # prefill's argmax before the first step
         self._cand_ready = False
+        self._fresh = True
 
     def _next_embed(self, embed: bool) -> None:
         """skv_next_embed: the previous token from the candidates (after a
@@ -692,6 +693,7 @@ class Generator:
     def prefill(self) -> None:
         """Every prompt through the model at once; the first new token of
         each sequence goes to the argmax buffer."""
+        self._fresh = False
         self.model.prefill(self.cache, self.prompt_host, self.plen)
         self._pick()
 
@@ -699,7 +701,8 @@ class Generator:
         """From the start (reset(): an empty cache, the prompts only), the
         prefill, then all decode steps; returns every sequence's tokens
         (prompt + output). Repeated calls reuse the captured graph."""
-        self.reset()
+        if not self._fresh:  # an explicit reset() since the last run or prefill is enough
+            self.reset()
         self.prefill()
         steps = self.steps
         if steps > 0:
