@@ -395,12 +395,16 @@ def run_c3(args, ctx):
     prompts = [r.integers(0, 50304, int(n)).tolist() for n in plen]
     params, model, runs, wbytes = _model_workload(args, ctx, tm, prompts, 1024, "c3",
                                                   [torch.float32, torch.bfloat16])
-    # per step: all weights + every sequence's K and V prefix (mean fill over the run)
-    mean_fill = 1024 / 2
+    # per step: all weights + the K and V prefixes the step reads, averaged over the run's
+    # steps. Decode step s reads sequence b's fill plen_b + s plus its new token while
+    # plen_b + s < 1023; from the step that records its last token (position 1023) on, the
+    # sequence is retired and reads nothing.
+    fill = plen[None, :] + np.arange(runs["float32"]["steps"])[:, None]
+    mean_tokens = float(np.where(fill < 1023, fill + 1, 0).sum(axis=1).mean())
     kv = {"float32": 4, "bfloat16": 2}
     roof = {}
     for k, run in runs.items():
-        by = wbytes + 16 * 12 * 2 * mean_fill * 768 * kv[k]
+        by = wbytes + 12 * 2 * mean_tokens * 768 * kv[k]
         roof[k] = by / (run["step_us"] * 1e-6) / 1e9
     cpu = cpu_cached = None
     if not args.no_cpu_baseline:
@@ -427,7 +431,9 @@ def run_c3(args, ctx):
          "batch": 16, "prompt_lens": plen.tolist()},
         {"bound": "hbm", "achieved": roof["float32"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": roof["float32"] / HBM_PEAK_GBS, "traffic": None,
-         "note": "per step: all weights + mean K/V prefix of 16 sequences, over step time",
+         "note": "per step: all weights + the K/V prefixes of the sequences not yet "
+                 "finished (mean over the run's steps), over step time",
+         "mean_kv_tokens_per_step": mean_tokens,
          "achieved_bf16_kv": roof["bfloat16"]},
         cpu, runs=runs, cpu_cached_baseline=cpu_cached)
 
