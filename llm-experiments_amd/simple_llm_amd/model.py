@@ -156,6 +156,10 @@ class _PrefillBuffers:
         self.attn = torch.zeros((M, d), device=dev)
         self.ff = torch.zeros((M, mlp), device=dev)
         self.x_last = torch.zeros((B, d), device=dev)
+        # row maps of a packed (ragged) prefill: packed q, k, v -> [B, C] rows
+        # (three planes), and the attention output's valid rows -> packed
+        self.gather_pad = torch.zeros(3 * M, dtype=torch.int32, device=dev)
+        self.gather_pk = torch.zeros(M, dtype=torch.int32, device=dev)
         L = _lib.lib()
         lin = max(L.skv_linear_workspace_bytes(M, n, k)
                   for n, k in ((3 * d, d), (d, d), (mlp, d), (d, mlp)))
@@ -430,11 +434,37 @@ class TransformerModel:
         d, H, D, T = tm.embedding_dim, tm.n_heads, self.head_dim, cache.max_seq_len
         M = B * C
         pos = start[:, None] + np.arange(C)[None, :]
-        pb.ids.copy_(torch.from_numpy(tokens.reshape(-1).astype(np.int32)))
-        pb.pos.copy_(torch.from_numpy(np.minimum(pos, T - 1).reshape(-1).astype(np.int32)))
         pb.n_new.copy_(torch.from_numpy(n_host.astype(np.int32)))
-        pb.last.copy_(torch.from_numpy(
-            (np.arange(B) * C + np.maximum(n_host - 1, 0)).astype(np.int32)))
+        # Ragged prompts: the projections run over the valid rows only, packed
+        # (row off_b + i is token i of sequence b); q, k, v are gathered into
+        # the [B, C] layout of the chunk append and the attention, and the
+        # attention output back. Each projection row is computed alone, so the
+        # valid rows' values are the padded layout's, bit for bit.
+        Mp = int(n_host.sum())
+        # (packed q, k, v are staged in ff's space: 3 Mp d <= M mlp)
+        packed = (not all_logits and 0 < Mp <= (3 * M) // 4
+                  and 3 * Mp * d <= M * self.mlp_dim)
+        if packed:
+            off = np.concatenate([[0], np.cumsum(n_host)[:-1]]).astype(np.int64)
+            bi = np.repeat(np.arange(B), n_host)
+            ii = np.arange(Mp) - np.repeat(off, n_host)
+            pb.ids[:Mp].copy_(torch.from_numpy(tokens[bi, ii].astype(np.int32)))
+            pb.pos[:Mp].copy_(torch.from_numpy(np.minimum(start[bi] + ii, T - 1).astype(np.int32)))
+            # padded row b*C + i <- packed row off_b + min(i, n_b - 1) (rows past
+            # n_b are padding the attention masks), for the q, k and v planes
+            pad = off[:, None] + np.minimum(np.arange(C)[None, :],
+                                            np.maximum(n_host - 1, 0)[:, None])
+            to_pad = (np.arange(3)[:, None] * Mp + pad.reshape(1, -1)).reshape(-1)
+            pb.gather_pad[:3 * M].copy_(torch.from_numpy(to_pad.astype(np.int32)))
+            pb.gather_pk[:Mp].copy_(torch.from_numpy((bi * C + ii).astype(np.int32)))
+            pb.last.copy_(torch.from_numpy(
+                (off + np.maximum(n_host - 1, 0)).astype(np.int32)))
+        else:
+            pb.ids.copy_(torch.from_numpy(tokens.reshape(-1).astype(np.int32)))
+            pb.pos.copy_(torch.from_numpy(np.minimum(pos, T - 1).reshape(-1).astype(np.int32)))
+            pb.last.copy_(torch.from_numpy(
+                (np.arange(B) * C + np.maximum(n_host - 1, 0)).astype(np.int32)))
+        Mr = Mp if packed else M  # rows of the projections
         L = _lib.lib()
         s = _lib.stream_handle(self.ctx.device)
         chk = _lib.check
@@ -452,14 +482,19 @@ class TransformerModel:
         pws_ptr = pws.data_ptr() if pws is not None else None
         pws_n = pws.numel() if pws is not None else 0
         chk(L.skv_embed(x, pb.ids.data_ptr(), pb.pos.data_ptr(), self.emb.data_ptr(),
-                        self.pe.data_ptr(), M, d, tm.vocab_size, self.pe.shape[0], s), "skv_embed")
+                        self.pe.data_ptr(), Mr, d, tm.vocab_size, self.pe.shape[0], s),
+            "skv_embed")
         for lw, layer in zip(self.layers, cache.layers):
             kc, vc = layer.k_cache.buffer.data_ptr(), layer.v_cache.buffer.data_ptr()
             lens = layer.lens.data_ptr()
             # q, k, v = LN1(x) . [Wq Wk Wv] over every prompt row: [3][B, C, H, D]
-            chk(L.skv_linear(qkv, x, lw["wqkv_t"].data_ptr(), None, None, lw["g1"].data_ptr(),
-                             lw["be1"].data_ptr(), 1e-5, M, 3 * d, d, 0, d, ws, wn, s),
-                "skv_linear")
+            # (packed: [3][Mp, d] into ff's space, then gathered into the layout)
+            chk(L.skv_linear(ff if packed else qkv, x, lw["wqkv_t"].data_ptr(), None, None,
+                             lw["g1"].data_ptr(), lw["be1"].data_ptr(), 1e-5, Mr, 3 * d, d, 0, d,
+                             ws, wn, s), "skv_linear")
+            if packed:
+                chk(L.skv_gather_rows(qkv, ff, pb.gather_pad.data_ptr(), 3 * M, d, 3 * Mp, s),
+                    "skv_gather_rows")
             # the chunk's k, v at each sequence's fill, then causal attention of
             # its queries over prefix + chunk; then the fill moves past the chunk
             chk(L.skv_append_chunk(kc, vc, k_ptr, v_ptr, lens, n_ptr, B, C, H, D, T, cdt,
@@ -468,14 +503,19 @@ class TransformerModel:
                                    ns.value, pws_ptr, pws_n, cdt, _lib.F32, _lib.F32, s),
                 "skv_prefill_attn")
             chk(L.skv_advance(lens, n_ptr, C, B, T, s), "skv_advance")
+            a_rows = attn
+            if packed:  # the valid rows of the attention output, packed, into qkv's space
+                chk(L.skv_gather_rows(qkv, attn, pb.gather_pk.data_ptr(), Mp, d, M, s),
+                    "skv_gather_rows")
+                a_rows = qkv
             # x += attn . Wo; ff = gelu(LN2(x) . W1 + b1); x += ff . W2 + b2
-            chk(L.skv_linear(x, attn, lw["wo_t"].data_ptr(), None, x, None, None, 0.0, M, d, d, 0,
-                             0, ws, wn, s), "skv_linear")
+            chk(L.skv_linear(x, a_rows, lw["wo_t"].data_ptr(), None, x, None, None, 0.0, Mr, d, d,
+                             0, 0, ws, wn, s), "skv_linear")
             chk(L.skv_linear(ff, x, lw["w1_t"].data_ptr(), lw["b1"].data_ptr(), None,
-                             lw["g2"].data_ptr(), lw["be2"].data_ptr(), 1e-5, M, self.mlp_dim, d,
+                             lw["g2"].data_ptr(), lw["be2"].data_ptr(), 1e-5, Mr, self.mlp_dim, d,
                              1, 0, ws, wn, s), "skv_linear")
             chk(L.skv_linear(x, ff, lw["w2_t"].data_ptr(), lw["b2"].data_ptr(), x, None, None, 0.0,
-                             M, d, self.mlp_dim, 0, 0, ws, wn, s), "skv_linear")
+                             Mr, d, self.mlp_dim, 0, 0, ws, wn, s), "skv_linear")
         for layer in cache.layers:
             layer.host_lens = np.minimum(start + n_host, T)
         if all_logits:
@@ -488,7 +528,7 @@ class TransformerModel:
             return out
         # the logits of each sequence's last new row (generate.py:52 takes logits[0, -1])
         bf = self.buffers(B)
-        chk(L.skv_gather_rows(pb.x_last.data_ptr(), x, pb.last.data_ptr(), B, d, M, s),
+        chk(L.skv_gather_rows(pb.x_last.data_ptr(), x, pb.last.data_ptr(), B, d, Mr, s),
             "skv_gather_rows")
         chk(L.skv_linear(bf.logits.data_ptr(), pb.x_last.data_ptr(), self.emb.data_ptr(), None,
                          None, None, None, 0.0, B, tm.vocab_size, d, 0, 0, bf.lin_ws.data_ptr(),
