@@ -790,6 +790,31 @@ def test_next_embed_step_generates_the_same_tokens(gpu_ctx, temperature):
     assert a == b == c
 
 
+def test_split_row_sampling_in_the_graph(gpu_ctx):
+    """Sampling with the reference's defaults (temperature 1, no filters) from
+    a 16400-entry vocabulary takes skv_sample's split-row path (slice
+    statistics, then one pick per row) inside the replayed step: the tokens
+    equal those of the eager run and of the unfused step, every token is in
+    the vocabulary, and another seed draws other tokens."""
+    banner("split-row sampling in the graph")
+    from simple_llm_amd import _lib
+    from simple_llm_amd import model as M
+    m, params = make_model(gpu_ctx, 16400, 512, 8, 2, 128, seed=5, std=0.05)
+    assert _lib.lib().skv_sample_workspace_bytes(3, 16400) > 0
+    r = np.random.default_rng(17)
+    prompts = [r.integers(0, 16400, n).tolist() for n in (6, 21, 13)]
+    kw = dict(temperature=1.0, seed=11)
+    g = M.Generator(m, prompts, 60, use_graph=True, **kw)
+    assert g.fused and not g.cand_mode
+    a = g.run()
+    b = M.Generator(m, prompts, 60, use_graph=False, **kw).run()
+    c = M.Generator(m, prompts, 60, use_graph=True, fused_tail=False, **kw).run()
+    assert a == b == c == g.run()
+    assert all(0 <= t < 16400 for o in a for t in o)
+    d = M.Generator(m, prompts, 60, use_graph=True, temperature=1.0, seed=12).run()
+    assert d != a
+
+
 def test_prefill_graph_generate_equals_eager_and_decode_only(gpu_ctx):
     """Prefill + graph-replayed decode gives the tokens of the eager run, and
     the same tokens as feeding the prompt through decode steps (the logits of
