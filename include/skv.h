@@ -396,11 +396,32 @@ size_t skv_sample_workspace_bytes(int M, int V);
  * contiguous, pos being the first). The decode kernels treat a negative
  * fill as an empty row (no append, no advance, zero output), and the
  * next-token calls record nothing for it, so a batch whose rows end at
- * different lengths stops reading the cache of the rows that are done. */
+ * different lengths stops reading the cache of the rows that are done.
+ * adv (may be NULL; int32 [B], zero after a prefill): the deferred fill
+ * advance of skv_append_decode_attn_direct. Where adv[b] is set, every
+ * layer's fill of row b first moves one past the previous step's token
+ * (up to seq_cap, none for a negative fill), and pos[b] is that fill; adv[b]
+ * is then set for this step's append. */
 int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                     const int32_t* prompt, const int32_t* prompt_len, const int32_t* pos, int B,
                     int max_prompt, int seq_cap, const int32_t* stop, int32_t* lens_all,
-                    int n_layers, skv_stream_t stream);
+                    int n_layers, int32_t* adv, skv_stream_t stream);
+
+/* skv_append_decode_attn for one query head per kv head (MHA), a
+ * contiguous cache and head_dim 64 or 128, WITHOUT the fill advance: one
+ * workgroup per (sequence, head) reads the head's whole filled row, folds in
+ * the new token (stored at lens[b] when lens[b] in [0, T_cap)) and writes
+ * the output; no split, no workspace, no merge pass. lens is left as it
+ * was: the caller advances it before the next step (skv_next_embed with
+ * advance set does, for every layer). A negative fill is an empty row
+ * (output 0, nothing stored). The reference's attention_with_kv_cache
+ * (gpu_kv_cache.py:194-289) with its kv_cache_update (:130-192), for the
+ * decode step's one token per sequence; sums run in another order than the
+ * split kernels', so the bits may differ within fp32 rounding. */
+int skv_append_decode_attn_direct(void* out, const void* q, void* k_cache, void* v_cache,
+                                  const void* new_k, const void* new_v, const int32_t* lens,
+                                  int B, int H, int D, int T_cap, float scale, int cache_dtype,
+                                  int in_dtype, int q_dtype, int out_dtype, skv_stream_t stream);
 
 /* Bytes of skv_linear_packed's argmax candidates for M rows: [M][256]
  * float values, then [M][256] int32 columns (one per workgroup). */
@@ -433,15 +454,16 @@ size_t skv_linear_cand_bytes(int M, int N, int K);
  * columns, as skv_linear_packed and skv_linear_cand write them; a row of
  * NaN only gives token 0), else argmax_prev[b]. Then ids[b] and seq as skv_next_tokens, and, when
  * embedding is not NULL, x[b, :] = embedding[ids[b], :] + pos_table[pos[b], :]
- * as skv_embed (ids and positions clamped into the tables); stop, lens_all
- * and n_layers retire finished rows as in skv_next_tokens. No counterpart
+ * as skv_embed (ids and positions clamped into the tables); stop, lens_all,
+ * n_layers and adv retire finished rows and advance the fills as in
+ * skv_next_tokens. No counterpart
  * in the reference, whose generate loop picks and embeds on the host side
  * (generate.py:29-69, jax_backend.py:144, 466-469). */
 int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                    const float* cand, int n_cand, const int32_t* prompt,
                    const int32_t* prompt_len, const int32_t* pos, int B, int max_prompt,
                    int seq_cap, const float* embedding, const float* pos_table, int d, int vocab,
-                   int ctx, const int32_t* stop, int32_t* lens_all, int n_layers,
+                   int ctx, const int32_t* stop, int32_t* lens_all, int n_layers, int32_t* adv,
                    skv_stream_t stream);
 
 /* ------------------------------------------------------------------------

@@ -16,7 +16,7 @@ LIB = os.path.join(HERE, "libskv.so")
 
 SOURCES = ["skv_api.hip", "append.hip", "decode_attn.hip", "decode_attn_generic.hip",
            "decode_attn_generic_paged.hip", "decode_gqa_mfma.hip",
-           "prefill_attn.hip", "model_ops.hip", "gemm.hip",
+           "decode_direct.hip", "prefill_attn.hip", "model_ops.hip", "gemm.hip",
            "sample.hip", "flash_fp32.hip", "bpe_tokenizer.cpp"]
 
 HIPCC_FLAGS = [

@@ -1067,16 +1067,33 @@ __device__ __forceinline__ void retire_row(const int32_t* __restrict__ stop,
     for (int li = 0; li < n_layers; ++li) lens_all[(size_t)li * B + b] = -1;
 }
 
+// Deferred fill advance (adv given): when the previous step's attention
+// appended without advancing (adv[b] = 1), every layer's fill of row b moves
+// past that token here, before anything of this step reads it; adv[b] is then
+// set for this step's append. Returns the row's fill.
+__device__ __forceinline__ int advance_row(int32_t* __restrict__ adv,
+                                           int32_t* __restrict__ lens_all, int n_layers, int B,
+                                           int b, int p, int cap) {
+  if (adv[b] != 0 && p >= 0 && p < cap) {
+    ++p;
+    for (int li = 0; li < n_layers; ++li) lens_all[(size_t)li * B + b] = p;
+  }
+  adv[b] = 1;
+  return p;
+}
+
 __global__ void k_next_tokens(int32_t* __restrict__ ids, int32_t* __restrict__ seq,
                               const int32_t* __restrict__ argmax_prev,
                               const int32_t* __restrict__ prompt,
                               const int32_t* __restrict__ prompt_len,
                               const int32_t* __restrict__ pos, int B, int max_prompt,
                               int seq_cap, const int32_t* __restrict__ stop,
-                              int32_t* __restrict__ lens_all, int n_layers) {
+                              int32_t* __restrict__ lens_all, int n_layers,
+                              int32_t* __restrict__ adv) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
-  const int p = pos[b];
+  int p = pos[b];
+  if (adv != nullptr) p = advance_row(adv, lens_all, n_layers, B, b, p, seq_cap);
   int t;
   if (p < prompt_len[b]) t = prompt[(size_t)b * max_prompt + min(max(p, 0), max_prompt - 1)];
   else t = argmax_prev[b];
@@ -1096,7 +1113,8 @@ __global__ __launch_bounds__(256) void k_next_embed(
     const int32_t* __restrict__ prompt, const int32_t* __restrict__ prompt_len,
     const int32_t* __restrict__ pos, int B, int max_prompt, int seq_cap,
     const float* __restrict__ emb, const float* __restrict__ pe, int d, int vocab, int ctx,
-    const int32_t* __restrict__ stop, int32_t* __restrict__ lens_all, int n_layers) {
+    const int32_t* __restrict__ stop, int32_t* __restrict__ lens_all, int n_layers,
+    int32_t* __restrict__ adv) {
   __shared__ int s_t;
   __shared__ float s_bv[4];
   __shared__ int s_bi[4];
@@ -1105,7 +1123,11 @@ __global__ __launch_bounds__(256) void k_next_embed(
   // together, for every row (one inside its prompt ignores the candidates):
   // the candidates then arrive with the fill instead of one round trip after
   // it.
-  const int p = pos[b];
+  // the fill after a deferred advance (every thread computes it; thread 0
+  // writes it back after the block's last read of pos and adv)
+  const int p0 = pos[b];
+  const bool moves = adv != nullptr && adv[b] != 0 && p0 >= 0 && p0 < seq_cap;
+  const int p = moves ? p0 + 1 : p0;
   const int plen = prompt_len[b];
   float bv = -INFINITY;
   int bi = vocab;
@@ -1131,7 +1153,13 @@ __global__ __launch_bounds__(256) void k_next_embed(
     }
     __syncthreads();
   }
+  if (adv != nullptr) __syncthreads();  // uniform: every thread has read pos[b] and adv[b]
   if (tid == 0) {
+    if (adv != nullptr) {
+      if (moves)
+        for (int li = 0; li < n_layers; ++li) lens_all[(size_t)li * B + b] = p;
+      adv[b] = 1;
+    }
     int t;
     if (in_prompt) {
       t = prompt[(size_t)b * max_prompt + min(max(p, 0), max_prompt - 1)];
@@ -1491,11 +1519,12 @@ extern "C" int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_
                               int max_prompt, int seq_cap, const float* embedding,
                               const float* pos_table, int d, int vocab, int ctx,
                               const int32_t* stop, int32_t* lens_all, int n_layers,
-                              skv_stream_t stream) {
+                              int32_t* adv, skv_stream_t stream) {
   SKV_REQUIRE(ids && seq && prompt && prompt_len && pos, SKV_E_INVALID,
               "skv_next_embed: null pointer argument");
-  SKV_REQUIRE(stop == nullptr || (lens_all != nullptr && n_layers > 0), SKV_E_INVALID,
-              "skv_next_embed: retiring rows needs lens_all and n_layers > 0");
+  SKV_REQUIRE((stop == nullptr && adv == nullptr) || (lens_all != nullptr && n_layers > 0),
+              SKV_E_INVALID,
+              "skv_next_embed: retiring rows or advancing fills needs lens_all and n_layers > 0");
   SKV_REQUIRE(B > 0 && max_prompt > 0 && seq_cap > 0 && vocab > 0 && n_cand >= 0, SKV_E_INVALID,
               "skv_next_embed: bad sizes");
   SKV_REQUIRE(n_cand > 0 ? cand != nullptr : argmax_prev != nullptr, SKV_E_INVALID,
@@ -1504,7 +1533,7 @@ extern "C" int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_
               "skv_next_embed: embedding needs x, pos_table, d and ctx");
   hipLaunchKernelGGL(k_next_embed, dim3(B), dim3(256), 0, (hipStream_t)stream, x, ids, seq,
                      argmax_prev, cand, n_cand, prompt, prompt_len, pos, B, max_prompt, seq_cap,
-                     embedding, pos_table, d, vocab, ctx, stop, lens_all, n_layers);
+                     embedding, pos_table, d, vocab, ctx, stop, lens_all, n_layers, adv);
   return check_launch("skv_next_embed");
 }
 
@@ -1512,15 +1541,16 @@ extern "C" int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax
                                const int32_t* prompt, const int32_t* prompt_len,
                                const int32_t* pos, int B, int max_prompt, int seq_cap,
                                const int32_t* stop, int32_t* lens_all, int n_layers,
-                               skv_stream_t stream) {
+                               int32_t* adv, skv_stream_t stream) {
   SKV_REQUIRE(ids && seq && argmax_prev && prompt && prompt_len && pos, SKV_E_INVALID,
               "skv_next_tokens: null pointer argument");
   SKV_REQUIRE(B > 0 && max_prompt > 0 && seq_cap > 0, SKV_E_INVALID,
               "skv_next_tokens: dims must be > 0");
-  SKV_REQUIRE(stop == nullptr || (lens_all != nullptr && n_layers > 0), SKV_E_INVALID,
-              "skv_next_tokens: retiring rows needs lens_all and n_layers > 0");
+  SKV_REQUIRE((stop == nullptr && adv == nullptr) || (lens_all != nullptr && n_layers > 0),
+              SKV_E_INVALID,
+              "skv_next_tokens: retiring rows or advancing fills needs lens_all and n_layers > 0");
   hipLaunchKernelGGL(k_next_tokens, dim3((B + 255) / 256), dim3(256), 0, (hipStream_t)stream, ids,
                      seq, argmax_prev, prompt, prompt_len, pos, B, max_prompt, seq_cap, stop,
-                     lens_all, n_layers);
+                     lens_all, n_layers, adv);
   return check_launch("skv_next_tokens");
 }

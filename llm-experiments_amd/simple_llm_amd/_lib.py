@@ -52,10 +52,12 @@ _SIGNATURES = {
     "skv_linear_pack": (_I, [_P, _P, _I, _I, _P]),
     "skv_linear_packed": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P]),
     "skv_linear_packed_cand_bytes": (_Z, [_I]),
+    "skv_append_decode_attn_direct": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I,
+                                           _I, _I, _I, _P]),
     "skv_linear_cand": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P, _Z, _P]),
     "skv_linear_cand_bytes": (_Z, [_I, _I, _I]),
     "skv_next_embed": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _I, _I, _I,
-                            _P, _P, _I, _P]),
+                            _P, _P, _I, _P, _P]),
     "skv_argmax_workspace_bytes": (_Z, [_I, _I]),
     "skv_argmax": (_I, [_P, _P, _I, _I, _P, _Z, _P]),
     "skv_sample": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _F, _I, _F, _F, _F, _I,
@@ -67,7 +69,7 @@ _SIGNATURES = {
                            _P]),
     "skv_bpe_train": (_I, [_P, _Z, _I, _P, _I, ctypes.POINTER(_I)]),
     "skv_bpe_encode": (_I, [_P, _Z, _P, _I, _P, ctypes.POINTER(_Z)]),
-    "skv_next_tokens": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P]),
+    "skv_next_tokens": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _I, _P, _P]),
     "skv_gather_rows": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "skv_decode_attn": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _P, _Z,
                              _I, _I, _I, _P]),

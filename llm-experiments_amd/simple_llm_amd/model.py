@@ -327,12 +327,20 @@ class TransformerModel:
         V, d = self.emb.shape
         return L.skv_linear_cand_bytes(B, V, d) // (8 * B)
 
+    def _direct_ok(self) -> bool:
+        """Whether the decode step can take skv_append_decode_attn_direct:
+        head_dim 64 or 128 and contexts up to 1024 tokens (past them the
+        split attention spreads a long row over more CUs and is faster)."""
+        return self.head_dim in (64, 128) and self.tm_params.context_size <= 1024
+
     def _launch_step(self, cache: KVCache, bf: _Buffers, embedded: bool = False,
-                     cand: bool = False) -> None:
+                     cand: bool = False, direct: bool = False) -> None:
         """One decode step's launches. embedded: x already holds the step's
         input rows (skv_next_embed ran). cand: the logits projection also
         writes the argmax candidates into bf.cand (skv_next_embed finishes
-        them at the next step); needs _n_cand(B) > 0."""
+        them at the next step); needs _n_cand(B) > 0. direct: the attention
+        appends without advancing the fills (skv_append_decode_attn_direct;
+        the next step's next-token kernel advances them)."""
         L = _lib.lib()
         tm = self.tm_params
         B, d, H, D, T = cache.batch_size, tm.embedding_dim, tm.n_heads, self.head_dim, \
@@ -364,10 +372,16 @@ class TransformerModel:
                                  lw["g1"].data_ptr(), lw["be1"].data_ptr(), 1e-5, B, 3 * d, d,
                                  0, d, lw_ws, lw_n, s), "skv_linear")
             # append k, v at each sequence's fill and attend [0, fill] (one call)
-            chk(L.skv_append_decode_attn(attn, q_ptr, kc, vc, k_ptr, v_ptr, layer.lens.data_ptr(),
-                                         B, H, H, D, T, scale, chunk, n_chunks, ws.data_ptr(),
-                                         ws.numel(), cdt, _lib.F32, _lib.F32, _lib.F32, s),
-                "skv_append_decode_attn")
+            if direct:
+                chk(L.skv_append_decode_attn_direct(attn, q_ptr, kc, vc, k_ptr, v_ptr,
+                                                    layer.lens.data_ptr(), B, H, D, T, scale,
+                                                    cdt, _lib.F32, _lib.F32, _lib.F32, s),
+                    "skv_append_decode_attn_direct")
+            else:
+                chk(L.skv_append_decode_attn(attn, q_ptr, kc, vc, k_ptr, v_ptr,
+                                             layer.lens.data_ptr(), B, H, H, D, T, scale, chunk,
+                                             n_chunks, ws.data_ptr(), ws.numel(), cdt, _lib.F32,
+                                             _lib.F32, _lib.F32, s), "skv_append_decode_attn")
             # x += attn . Wo
             chk(L.skv_linear(x, attn, lw["wo_t"].data_ptr(), None, x, None, None, 0.0, B, d, d, 0,
                              0, lw_ws, lw_n, s), "skv_linear")
@@ -587,7 +601,7 @@ class Generator:
                  temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
                  min_p: float = 0.0, repetition_penalty: float = 1.0,
                  repetition_window: int = 64, seed: int = 42, fused_tail: bool = True,
-                 retire_rows: bool = True):
+                 retire_rows: bool = True, direct_attention: bool = True):
         tm = model.tm_params
         self.model = model
         B = len(prompts)
@@ -631,6 +645,8 @@ class Generator:
         for li, layer in enumerate(self.cache.layers):
             layer.lens = self.lens_all[li]
         self.stop = torch.from_numpy(tot.astype(np.int32)).to(dev)
+        # per-row flags of the deferred fill advance (direct attention)
+        self.adv = torch.zeros(B, dtype=torch.int32, device=dev)
         self.bufs = model.buffers(B)
         # decode steps after the prefill: the step at position p produces token p + 1
         self.steps = max(int((tot - 1 - plen).max()), 0)
@@ -650,6 +666,12 @@ class Generator:
         self.fused = bool(fused_tail)
         self.n_cand = model._n_cand(B) if self.fused and self.greedy else 0
         self.cand_mode = self.n_cand > 0
+        # Greedy steps of contexts up to 1024 take the direct attention (one
+        # workgroup per sequence and head, no merge pass): the step's append
+        # leaves the fill where it was and the next step's next-token kernel
+        # advances it. Sampling keeps the split attention, whose advance gives
+        # skv_sample the fill that includes the step's token.
+        self.direct = bool(direct_attention) and self.greedy and model._direct_ok()
         self.reset()
 
     def reset(self) -> None:
@@ -659,6 +681,7 @@ class Generator:
         self.seq.zero_()
         self.seq[:, :self.prompt.shape[1]].copy_(self.prompt)
         self.bufs.argmax.zero_()
+        self.adv.zero_()
         # with candidates, skv_next_embed reads the previous step's, or the
         # prefill's argmax before the first step
         self._cand_ready = False
@@ -684,11 +707,13 @@ class Generator:
                    "skv_next_embed")
 
     def _retire_args(self):
-        """(stop, lens_all, n_layers) of the next-token calls: retire finished
-        rows, or nothing."""
-        if not self.retire:
-            return None, None, 0
-        return self.stop.data_ptr(), self.lens_all.data_ptr(), self.lens_all.shape[0]
+        """(stop, lens_all, n_layers, adv) of the next-token calls: retire
+        finished rows, and advance the fills deferred by the direct attention."""
+        stop = self.stop.data_ptr() if self.retire else None
+        adv = self.adv.data_ptr() if self.direct else None
+        if stop is None and adv is None:
+            return None, None, 0, None
+        return stop, self.lens_all.data_ptr(), self.lens_all.shape[0], adv
 
     def _pick(self) -> None:
         """Next token of every sequence from the logits buffer into argmax."""
@@ -716,7 +741,7 @@ class Generator:
         s = _lib.stream_handle(m.ctx.device)
         if self.fused:
             self._next_embed(embed=True)
-            m._launch_step(c, bf, embedded=True, cand=self.cand_mode)
+            m._launch_step(c, bf, embedded=True, cand=self.cand_mode, direct=self.direct)
             if self.cand_mode:
                 self._cand_ready = True
             else:
@@ -727,7 +752,7 @@ class Generator:
                                      c.layers[0].lens.data_ptr(), self.B, self.prompt.shape[1],
                                      self.seq.shape[1], *self._retire_args(), s),
                    "skv_next_tokens")
-        m._launch_step(c, bf)
+        m._launch_step(c, bf, direct=self.direct)
         self._pick()
 
     def prefill(self) -> None:

@@ -334,7 +334,7 @@ def test_step_entry_points_reject_bad_arguments():
         return L.skv_next_embed(a["x"], fake, fake, a["argmax_prev"], a["cand"], a["n_cand"],
                                 fake, fake, fake, a["B"], 8, 64, a["emb"], fake, a["d"],
                                 a["vocab"], a["ctx"], a["stop"], a["lens_all"], a["n_layers"],
-                                None)
+                                a.get("adv"), None)
 
     assert ne(B=0) == _lib.SKV_E_INVALID
     assert ne(n_cand=-1) == _lib.SKV_E_INVALID
@@ -348,4 +348,10 @@ def test_step_entry_points_reject_bad_arguments():
     assert ne(stop=fake, lens_all=fake, n_layers=0) == _lib.SKV_E_INVALID
     assert b"retiring rows" in L.skv_last_error()
     assert L.skv_next_tokens(fake, fake, fake, fake, fake, fake, 4, 8, 64, fake, None, 2,
-                             None) == _lib.SKV_E_INVALID
+                             None, None) == _lib.SKV_E_INVALID
+    assert ne(adv=fake) == _lib.SKV_E_INVALID  # a deferred advance needs every layer's fills
+    # the direct decode attention: MHA, head_dim 64 or 128
+    assert L.skv_append_decode_attn_direct(fake, fake, fake, fake, fake, fake, fake, 2, 4, 48,
+                                           64, 0.1, 0, 0, 0, 0, None) == _lib.SKV_E_UNSUPPORTED
+    assert L.skv_append_decode_attn_direct(fake, fake, fake, fake, None, fake, fake, 2, 4, 64,
+                                           64, 0.1, 0, 0, 0, 0, None) == _lib.SKV_E_INVALID

@@ -254,7 +254,7 @@ def test_packed_argmax_candidates_and_next_embed(gpu_ctx, M, N, K):
     _lib.check(L.skv_next_embed(xo.data_ptr(), ids.data_ptr(), seq.data_ptr(),
                                 argmax_prev.data_ptr(), cand.data_ptr(), n_cand,
                                 promptd.data_ptr(), plend.data_ptr(), posd.data_ptr(), M, 4, T,
-                                embd.data_ptr(), ped.data_ptr(), D, V, T, None, None, 0, s),
+                                embd.data_ptr(), ped.data_ptr(), D, V, T, None, None, 0, None, s),
                "skv_next_embed")
     tok = want.copy()
     tok[M - 1] = 11  # pos < prompt_len: the prompt token
@@ -267,7 +267,7 @@ def test_packed_argmax_candidates_and_next_embed(gpu_ctx, M, N, K):
     xo.zero_()
     _lib.check(L.skv_next_embed(None, ids.data_ptr(), seq.data_ptr(), argmax_prev.data_ptr(),
                                 None, 0, promptd.data_ptr(), plend.data_ptr(), posd.data_ptr(), M,
-                                4, T, None, None, D, V, T, None, None, 0, s), "skv_next_embed")
+                                4, T, None, None, D, V, T, None, None, 0, None, s), "skv_next_embed")
     tok2 = np.arange(M) + 1000
     tok2[M - 1] = 11
     np.testing.assert_array_equal(ids.cpu().numpy(), tok2)
@@ -346,7 +346,7 @@ def test_linear_cand_matches_skv_linear_and_argmax(gpu_ctx, M, N, K):
     prompt = dev(np.zeros((M, 4), np.int32))
     _lib.check(L.skv_next_embed(None, ids.data_ptr(), seq.data_ptr(), None, cand.data_ptr(), G,
                                 prompt.data_ptr(), plen.data_ptr(), pos.data_ptr(), M, 4, T, None,
-                                None, 0, N, T, None, None, 0, s), "skv_next_embed")
+                                None, 0, N, T, None, None, 0, None, s), "skv_next_embed")
     np.testing.assert_array_equal(ids.cpu().numpy(), want)
     np.testing.assert_array_equal(seq.cpu().numpy()[:, 2], want)
 
@@ -485,7 +485,7 @@ def test_next_tokens(gpu_ctx):
     p_d, pl_d, pos_d, a_d = dev(prompt), dev(plen), dev(pos), dev(arg)
     _lib.check(_lib.lib().skv_next_tokens(ids.data_ptr(), seq.data_ptr(), a_d.data_ptr(),
                                           p_d.data_ptr(), pl_d.data_ptr(), pos_d.data_ptr(), 3, 4,
-                                          8, None, None, 0, _lib.stream_handle()), "next")
+                                          8, None, None, 0, None, _lib.stream_handle()), "next")
     assert ids.cpu().tolist() == [6, 71, 72]
     s = seq.cpu().numpy()
     assert s[0, 1] == 6 and s[1, 1] == 71 and not s[2].any()  # pos 9 >= cap 8: not recorded
@@ -497,7 +497,7 @@ def test_next_tokens(gpu_ctx):
     seq.zero_()
     _lib.check(_lib.lib().skv_next_tokens(ids.data_ptr(), seq.data_ptr(), a_d.data_ptr(),
                                           p_d.data_ptr(), pl_d.data_ptr(), lens_all.data_ptr(), 3,
-                                          4, 8, stop.data_ptr(), lens_all.data_ptr(), 3,
+                                          4, 8, stop.data_ptr(), lens_all.data_ptr(), 3, None,
                                           _lib.stream_handle()), "next")
     assert lens_all.cpu().numpy().tolist() == [[1, -1, -1]] * 3
     s = seq.cpu().numpy()
@@ -742,6 +742,76 @@ def test_fused_step_tail_generates_the_same_tokens(gpu_ctx, vocab, d, heads):
     c = M.Generator(m, prompts, 70, use_graph=False).run()
     assert a == bb == c == a2
     assert all(len(o) == 70 and o[:len(p)] == p for o, p in zip(a, prompts))
+
+
+@pytest.mark.parametrize("B,H,D,T,dt", [(1, 4, 64, 256, "f32"), (16, 12, 64, 1024, "f32"),
+                                         (16, 12, 64, 1024, "bf16"), (3, 8, 128, 512, "bf16"),
+                                         (5, 4, 128, 300, "f32")])
+def test_direct_attention_matches_split(gpu_ctx, B, H, D, T, dt):
+    """skv_append_decode_attn_direct against skv_append_decode_attn on the same
+    inputs (ragged fills, an empty row, a full row, a retired row): outputs
+    within 1e-5, the same bits stored for the new token, and the fills left
+    where they were (the split call advances its own copy)."""
+    banner(f"direct attention B={B} H={H} D={D} T={T} {dt}")
+    from simple_llm_amd.gpu import gpu_kv_cache as kvc
+    _lib = lib()
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    cdt = _lib.BF16 if dt == "bf16" else _lib.F32
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    r = np.random.default_rng(B * 100 + D + T)
+    fills = r.integers(0, T, B)
+    fills[0] = 0
+    if B > 2:
+        fills[1], fills[2] = T, -1  # full (no append), retired (empty)
+    kc = torch.from_numpy(r.standard_normal(B * T * H * D).astype(np.float32)).cuda().to(tdt)
+    vc = torch.from_numpy(r.standard_normal(B * T * H * D).astype(np.float32)).cuda().to(tdt)
+    q, nk, nv = (dev(r.standard_normal(B * H * D).astype(np.float32)) for _ in range(3))
+    lens = dev(fills.astype(np.int32))
+    kc2, vc2, lens2 = kc.clone(), vc.clone(), lens.clone()
+    chunk, n = kvc.decode_plan(gpu_ctx, B, H, H, T, 0, head_dim=D, dtype=tdt)
+    ws = torch.empty(L.skv_decode_workspace_bytes(B, H, D, n), dtype=torch.uint8, device="cuda")
+    want = torch.zeros(B * H * D, device="cuda")
+    got = torch.full((B * H * D,), float("nan"), device="cuda")
+    sc = D ** -0.5
+    _lib.check(L.skv_append_decode_attn(want.data_ptr(), q.data_ptr(), kc2.data_ptr(),
+                                        vc2.data_ptr(), nk.data_ptr(), nv.data_ptr(),
+                                        lens2.data_ptr(), B, H, H, D, T, sc, chunk, n,
+                                        ws.data_ptr(), ws.numel(), cdt, _lib.F32, _lib.F32,
+                                        _lib.F32, s), "split")
+    _lib.check(L.skv_append_decode_attn_direct(got.data_ptr(), q.data_ptr(), kc.data_ptr(),
+                                               vc.data_ptr(), nk.data_ptr(), nv.data_ptr(),
+                                               lens.data_ptr(), B, H, D, T, sc, cdt, _lib.F32,
+                                               _lib.F32, _lib.F32, s), "direct")
+    g, w = got.cpu().numpy(), want.cpu().numpy()
+    np.testing.assert_allclose(g, w, rtol=1e-5, atol=1e-5 * np.abs(w).max())
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    np.testing.assert_array_equal(lens.cpu().numpy(), fills)
+    if B > 2:
+        assert not g.reshape(B, -1)[2].any()  # a retired row gives 0
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_direct_attention_generates_the_same_tokens(gpu_ctx, fused):
+    """Greedy generation with the direct attention (the fills advanced by the
+    next step's next-token kernel) gives the tokens of the split attention,
+    graph-replayed and eager, and the fills end where the split run's do."""
+    banner(f"direct attention generate, fused={fused}")
+    from simple_llm_amd import model as M
+    m, params = make_model(gpu_ctx, 300, 256, 4, 2, 96, seed=13, std=0.1)
+    r = np.random.default_rng(31)
+    prompts = [r.integers(0, 300, n).tolist() for n in (9, 30, 2)]
+    tot = [96, 70, 50]
+    g = M.Generator(m, prompts, tot, use_graph=True, fused_tail=fused, retire_rows=False)
+    assert g.direct
+    a = g.run()
+    b_ = M.Generator(m, prompts, tot, use_graph=True, fused_tail=fused, retire_rows=False,
+                     direct_attention=False)
+    assert not b_.direct
+    bb = b_.run()
+    c = M.Generator(m, prompts, tot, use_graph=False, fused_tail=fused).run()
+    assert a == bb == c
+    np.testing.assert_array_equal(g.lens_all.cpu().numpy(), b_.lens_all.cpu().numpy())
 
 
 @pytest.mark.parametrize("fused", [True, False])
