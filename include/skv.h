@@ -415,7 +415,7 @@ int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
  * was: the caller advances it before the next step (skv_next_embed with
  * advance set does, for every layer). A negative fill is an empty row
  * (output 0, nothing stored). The reference's attention_with_kv_cache
- * (gpu_kv_cache.py:194-289) with its kv_cache_update (:130-192), for the
+ * (gpu_kv_cache.py:194-289) with its kv_cache_update (:113-186), for the
  * decode step's one token per sequence; sums run in another order than the
  * split kernels', so the bits may differ within fp32 rounding. */
 int skv_append_decode_attn_direct(void* out, const void* q, void* k_cache, void* v_cache,
