@@ -111,6 +111,99 @@ def algorithmic_bytes(lens, h_q=H, h_kv=H, d=D, s_kv=2, s_q=4, s_o=4) -> int:
     return int(sum(2 * h_kv * int(L) * d * s_kv + h_q * d * (s_q + s_o) for L in lens))
 
 
+def rel_err_rows(got, want) -> float:
+    """max over rows (all axes but the last) of ||got - want|| / ||want||."""
+    import numpy as np
+
+    got = np.asarray(got, np.float64).reshape(-1, np.shape(got)[-1])
+    want = np.asarray(want, np.float64).reshape(-1, np.shape(want)[-1])
+    num = np.linalg.norm(got - want, axis=1)
+    den = np.maximum(np.linalg.norm(want, axis=1), 1e-30)
+    live = np.linalg.norm(want, axis=1) > 0
+    if not live.any():
+        return 0.0
+    return float((num / den)[live].max())
+
+
+def replay_outputs(step, n, reset, out):
+    """The outputs of steps 0..n-1 of an attention workload, run again from
+    its start fills (reset()) after the timed region: the kernels are
+    deterministic and the plan is the timed run's, so these are the timed
+    steps' outputs bit for bit (the appends rewrite the same rows)."""
+    import torch
+
+    reset()
+    outs = []
+    for i in range(n):
+        step(i)
+        outs.append(out.detach().clone())
+    torch.cuda.synchronize()
+    return [o.cpu().numpy() for o in outs]
+
+
+def accuracy_record(gpu_outs, oracle_outs, tol, against):
+    errs = [rel_err_rows(g, w) for g, w in zip(gpu_outs, oracle_outs)]
+    worst = max(errs) if errs else None
+    return {"max_rel_err": worst, "tolerance": tol, "steps_checked": len(errs),
+            "pass": worst is not None and worst <= tol, "against": against,
+            "norm": "per (sequence, head) row: ||gpu - oracle||_2 / ||oracle||_2, max over rows "
+                    "and steps"}
+
+
+def sclk_sampler():
+    """A thread that samples the GPU's current shader clock (the level marked
+    '*' in sysfs pp_dpm_sclk of the card torch runs on) every 2 ms until
+    stopped; returns (start, stop) where stop() gives the MHz samples. Empty
+    when the file is not readable."""
+    import glob
+    import threading
+
+    paths = sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
+    samples, done = [], threading.Event()
+    path = None
+    for pth in paths:  # the first card whose file is readable (one GPU per box)
+        try:
+            with open(pth) as f:
+                f.read()
+            path = pth
+            break
+        except OSError:
+            continue
+
+    def read():
+        try:
+            with open(path) as f:
+                for line in f:
+                    if "*" in line:
+                        m = re.search(r"(\d+)\s*[Mm]hz", line)
+                        if m:
+                            return int(m.group(1))
+        except OSError:
+            return None
+        return None
+
+    def loop():
+        while not done.is_set():
+            v = read()
+            if v is not None:
+                samples.append(v)
+            time.sleep(0.002)
+
+    th = threading.Thread(target=loop, daemon=True)
+
+    def start():
+        if path is not None:
+            th.start()
+
+    def stop():
+        done.set()
+        if path is not None:
+            th.join()
+        return samples
+
+    return start, stop, path
+
+
 def measured_traffic(workload: str = "c4"):
     """HBM bytes per decode-attention call from the committed rocprofv3 PMC
     summary of the workload (profiles/decode_attn_<workload>_pmc.md), or None
@@ -157,18 +250,57 @@ def time_prefill(ctx, cache, reps: int):
     ms = np.array([a.elapsed_time(b) for a, b in evs])
     fl = prefill_flops(start)
     mean_s = float(ms.mean()) * 1e-3
+    # the shader clock while the same call runs back to back for ~0.3 s (sysfs
+    # pp_dpm_sclk, sampled by a host thread): the box's clock under this load
+    start_clk, stop_clk, clk_path = sclk_sampler()
+    n_clk = max(int(0.3 / max(mean_s, 1e-5)), 1)
+    start_clk()
+    t0 = time.perf_counter()
+    for _ in range(n_clk):
+        cache.current_len = start
+        gpu.kv_cache_prefill(ctx, cache, 0, kn, vn, q, out)
+    torch.cuda.synchronize()
+    burst_us = (time.perf_counter() - t0) / n_clk * 1e6
+    mhz = stop_clk()
+    # accuracy of the last call: sampled query rows against the float64
+    # oracle over the device cache's own bf16 values (prefix + chunk)
+    from oracle import kv_oracle as ko
+
+    got = out.cpu().numpy()
+    qh = q.cpu().numpy()
+    kvw = cache.layers[0].k_cache.buffer.view(B, T_CAP, H, D)
+    vvw = cache.layers[0].v_cache.buffer.view(B, T_CAP, H, D)
+    errs = []
+    for b, i, h in ((0, 0, 0), (1, 255, 7), (2, 511, 15), (3, 100, 3)):
+        n = start + i + 1
+        kh = kvw[b, :n, h].float().cpu().numpy()[None, :, None, :]
+        vh = vvw[b, :n, h].float().cpu().numpy()[None, :, None, :]
+        want = ko.decode_attention(qh[b:b + 1, i, h:h + 1], kh, vh, [n])
+        errs.append(rel_err_rows(got[b, i, h][None], want[0]))
     return {
         "chunk_tokens": PREFILL_C, "start_fill": start, "reps": reps,
         "mean_us": mean_s * 1e6, "tflops": fl / mean_s / 1e12,
         "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
         "frac": fl / mean_s / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "flops": fl,
+        "per_rep_us": [round(float(x) * 1e3, 1) for x in ms],
+        "median_us": float(np.median(ms)) * 1e3, "min_us": float(ms.min()) * 1e3,
+        "clock": {"source": clk_path, "back_to_back_calls": n_clk,
+                  "wall_us_per_call": burst_us, "samples": len(mhz),
+                  "sclk_mhz_median": float(np.median(mhz)) if mhz else None,
+                  "sclk_mhz_min": min(mhz) if mhz else None,
+                  "sclk_mhz_max": max(mhz) if mhz else None},
+        "accuracy": {"max_rel_err": max(errs), "tolerance": 2e-2, "rows_checked": len(errs),
+                     "pass": max(errs) <= 2e-2,
+                     "against": "float64 oracle (kv_oracle) over the cache's bf16 values, "
+                                "sampled (sequence, query row, head) of the last call"},
         "includes": "chunk append + MFMA attention + split merge + fill advance",
     }
 
 
-def cpu_baseline(args, k_dev, v_dev, q_all, k_all, v_all):
-    """Time the CPU restatement on the first steps of the same workload."""
+def cpu_baseline(args, k_dev, v_dev, q_all, k_all, v_all, outs=None):
+    """Time the CPU restatement on the first steps of the same workload;
+    the oracle's output of each step goes to outs (a list) when given."""
     import numpy as np
     import torch
 
@@ -189,7 +321,9 @@ def cpu_baseline(args, k_dev, v_dev, q_all, k_all, v_all):
             kc[b, lens[b]] = ks[steps, b]
             vc[b, lens[b]] = vs[steps, b]
         lens += 1
-        c_oracle.decode_attn(qs[steps], kc, vc, lens, cache_bf16=True)
+        o = c_oracle.decode_attn(qs[steps], kc, vc, lens, cache_bf16=True)
+        if outs is not None:
+            outs.append(o)
         steps += 1
     dt = time.perf_counter() - t0
     return {
@@ -292,11 +426,12 @@ def _time_reference_generate(params, prompt, n_heads, context, budget_s, max_tok
     return n, dt
 
 
-def _model_workload(args, ctx, tm, prompts, total_len, label, kv_dtypes):
+def _model_workload(args, ctx, tm, prompts, total_len, label, kv_dtypes, acc_rows, acc_last):
     """Greedy generation of `prompts` to `total_len` tokens: one prefill of
     every prompt, then the decode steps with HIP-graph replay; per KV dtype,
     the mean of 3 timed runs after a warm-up run, and the prefill alone over
-    3 more runs."""
+    3 more runs; then the logits of the last acc_last decode steps of rows
+    acc_rows against the float64 oracle."""
     import numpy as np
     import torch
 
@@ -328,13 +463,59 @@ def _model_workload(args, ctx, tm, prompts, total_len, label, kv_dtypes):
             pre.append(time.perf_counter() - t0)
         gen = sum(total_len - len(p) for p in prompts)
         run_s, pre_s = float(np.mean(times)), float(np.mean(pre))
+        acc, again = _model_accuracy(g, params, tm.n_heads, acc_rows, acc_last,
+                                     1e-4 if kvd == torch.float32 else 2e-2)
+        assert again == out  # the accuracy run made the timed run's tokens
         runs[str(kvd).replace("torch.", "")] = {
             "run_s": run_s, "prefill_s": pre_s, "prompt_tokens": int(sum(len(p) for p in prompts)),
             "steps": g.steps, "generated_tokens": gen, "tokens_per_s": gen / run_s,
-            "step_us": (run_s - pre_s) / max(g.steps, 1) * 1e6}
+            "step_us": (run_s - pre_s) / max(g.steps, 1) * 1e6,
+            "direct_attention": bool(g.direct), "accuracy": acc}
     d, L, V = tm.embedding_dim, tm.n_layers, tm.vocab_size
     weight_bytes = 4 * (V * d + L * (4 * d * d + 2 * d * model.mlp_dim + model.mlp_dim + 7 * d))
     return params, model, runs, weight_bytes
+
+
+def _model_accuracy(g, params, n_heads, rows, last_k, tol):
+    """Same-run accuracy of a greedy generate workload: the logits of the last
+    last_k decode steps of each row in `rows`, from one more run of the timed
+    Generator (deterministic kernels: the timed run's values), against the
+    float64 forward of oracle/model_oracle.py over the tokens that run made
+    (teacher forced)."""
+    import numpy as np
+
+    from oracle import model_oracle as mo
+
+    plen, tot = g.plen.astype(np.int64), g.tot.astype(np.int64)
+    want = {}  # decode step -> rows whose logits that step are checked
+    for b in rows:
+        last = int(tot[b]) - 2  # position of the row's last decode step
+        for p in range(max(last - last_k + 1, int(plen[b])), last + 1):
+            want.setdefault(p - int(plen[b]), []).append(b)
+    got = {}
+
+    def on_step(j, logits):
+        for b in want.get(j, ()):
+            got[(b, j)] = logits[b].detach().clone()
+
+    g.reset()
+    seqs = g.run(on_step=on_step)
+    errs = []
+    for b in rows:
+        last = int(tot[b]) - 2
+        first = max(last - last_k + 1, int(plen[b]))
+        ref = mo.forward(params, np.array([seqs[b][:last + 1]]), n_heads,
+                         last=last - first + 1)[0]
+        gl = np.stack([got[(b, p - int(plen[b]))].cpu().numpy() for p in range(first, last + 1)])
+        num = np.linalg.norm(gl - ref, axis=1)
+        errs.append(float((num / np.linalg.norm(ref, axis=1)).max()))
+    worst = max(errs)
+    return {"max_rel_err": worst, "tolerance": tol, "pass": worst <= tol,
+            "rows_checked": [int(b) for b in rows], "positions_per_row": last_k,
+            "against": "float64 forward (oracle/model_oracle.py) over the tokens the timed "
+                       "run generated (teacher forced), the logits of each checked row's last "
+                       "decode steps",
+            "norm": "per logits row: ||gpu - oracle||_2 / ||oracle||_2, max over rows"}, seqs
 
 
 def run_c1(args, ctx):
@@ -349,7 +530,7 @@ def run_c1(args, ctx):
     tm = M.TransformerModelParams(256, 256, 256, 4, 4)
     prompt = np.random.default_rng(1).integers(0, 256, 64).tolist()
     params, model, runs, wbytes = _model_workload(args, ctx, tm, [prompt], 256, "c1",
-                                                  [torch.float32])
+                                                  [torch.float32], [0], 191)
     r = runs["float32"]
     cpu = cpu_cached = None
     if not args.no_cpu_baseline:
@@ -373,11 +554,12 @@ def run_c1(args, ctx):
                      "token), then 191 cached decode steps replayed from one HIP graph; value "
                      "= generated tokens / whole run (prefill included)",
          "batch": 1, "prompt": 64, "generated": 192},
-        {"bound": "launch latency", "note": "12.8 MB of weights per token; 26 kernels per "
+        {"bound": "launch latency", "note": "12.8 MB of weights per token; 22 kernels per "
                                             "step replayed from one HIP graph",
          "achieved": wbytes / (r["step_us"] * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": wbytes / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, "traffic": None},
-        cpu, runs=runs, cpu_cached_baseline=cpu_cached)
+        cpu, max_rel_err=r["accuracy"]["max_rel_err"], accuracy=r["accuracy"], runs=runs,
+        cpu_cached_baseline=cpu_cached)
 
 
 def run_c3(args, ctx):
@@ -394,7 +576,7 @@ def run_c3(args, ctx):
     plen = r.integers(32, 513, 16)
     prompts = [r.integers(0, 50304, int(n)).tolist() for n in plen]
     params, model, runs, wbytes = _model_workload(args, ctx, tm, prompts, 1024, "c3",
-                                                  [torch.float32, torch.bfloat16])
+                                                  [torch.float32, torch.bfloat16], [0, 9], 16)
     # per step: all weights + the K and V prefixes the step reads, averaged over the run's
     # steps. Decode step s reads sequence b's fill plen_b + s plus its new token while
     # plen_b + s < 1023; from the step that records its last token (position 1023) on, the
@@ -435,7 +617,8 @@ def run_c3(args, ctx):
                  "finished (mean over the run's steps), over step time",
          "mean_kv_tokens_per_step": mean_tokens,
          "achieved_bf16_kv": roof["bfloat16"]},
-        cpu, runs=runs, cpu_cached_baseline=cpu_cached)
+        cpu, max_rel_err=r32["accuracy"]["max_rel_err"], accuracy=r32["accuracy"], runs=runs,
+        cpu_cached_baseline=cpu_cached)
 
 
 def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt, label):
@@ -506,7 +689,11 @@ def _attention_workload(args, ctx, cache, lens0, steps, Hq, Hkv, Dh, s_kv, q_dt,
             "mean_call_us": mean_s * 1e6, "algorithmic_bytes_per_call": byts,
             "split_k": {"chunk_tokens": chunk, "n_chunks": n_chunks},
             "warmup_settle_s": round(roofline_settle, 3)}
-    return wall, active, roof, (q_all, k_all, v_all)
+
+    def replay(n):
+        return replay_outputs(step, n, lambda: set_lens(lens0), out)
+
+    return wall, active, roof, (q_all, k_all, v_all), replay
 
 
 def run_c5(args, ctx):
@@ -542,10 +729,11 @@ def run_c5(args, ctx):
         for i in range(0, buf.shape[0], 1 << 16):
             chunk = buf[i:i + (1 << 16)]
             chunk.copy_(torch.randn(chunk.shape, generator=g, device=ctx.device))
-    wall, active, roof, (q_all, k_all, v_all) = _attention_workload(
+    wall, active, roof, (q_all, k_all, v_all), replay = _attention_workload(
         args, ctx, cache, lens0, steps, Hq, Hkv, Dh, 2, 0, "c5")
     cpu = None
-    if not args.no_cpu_baseline:
+    oracle_outs = []
+    if True:  # the CPU leg: timed unless --no-cpu-baseline; its outputs check the GPU's
         from oracle import c_oracle
 
         # the pool gathered into a contiguous [B, T, H_kv, D] cache on the host (the
@@ -564,19 +752,25 @@ def run_c5(args, ctx):
         lens = lens0.astype(np.int32).copy()
         c_oracle.decode_attn(qs[0], kc, vc, lens, cache_bf16=True)  # warm-up (pages, threads)
         n, tok, t0 = 0, 0, time.perf_counter()
-        while n < steps and time.perf_counter() - t0 < args.cpu_seconds:
+        n_max = 2 if args.no_cpu_baseline else steps
+        while n < n_max and (n == 0 or time.perf_counter() - t0 < args.cpu_seconds):
             for b in range(B):  # host append at lens[b]
                 kc[b, lens[b]], vc[b, lens[b]] = ks[n, b], vs[n, b]
             lens += 1
             tok += B
-            c_oracle.decode_attn(qs[n], kc, vc, lens, cache_bf16=True)
+            oracle_outs.append(c_oracle.decode_attn(qs[n], kc, vc, lens, cache_bf16=True))
             n += 1
         dt = time.perf_counter() - t0
-        cpu = {"value": tok / dt, "unit": "tokens/s", "cores": c_oracle.threads(),
-               "kind": "port",
-               "sample": f"first {n} of the {steps} C5 steps (append + GQA decode attention "
-                         f"over the pool gathered into a contiguous bf16 cache), "
-                         f"oracle/c/kv_attn_ref.c with OpenMP, {dt:.1f} s"}
+        if not args.no_cpu_baseline:
+            cpu = {"value": tok / dt, "unit": "tokens/s", "cores": c_oracle.threads(),
+                   "kind": "port",
+                   "sample": f"first {n} of the {steps} C5 steps (append + GQA decode attention "
+                             f"over the pool gathered into a contiguous bf16 cache), "
+                             f"oracle/c/kv_attn_ref.c with OpenMP, {dt:.1f} s"}
+    accuracy = accuracy_record(replay(len(oracle_outs)), oracle_outs, 2e-2,
+                               "oracle/c/kv_attn_ref.c on the pool gathered into a contiguous "
+                               "cache (the same bf16 values, fp32 math), the first steps of the "
+                               "timed run")
     return _record(
         "decode tokens/sec", active / wall, "tokens/s", steps, args.warmup, wall / steps * 1e3,
         "bf16",
@@ -585,7 +779,7 @@ def run_c5(args, ctx):
                      "lognormal lengths median 1500 sigma 0.8 in [16, 8192], 128 steps of "
                      "append + decode attention",
          "batch": B, "mean_len": float(lens0.mean()), "pages": n_blocks},
-        roof, cpu)
+        roof, cpu, max_rel_err=accuracy["max_rel_err"], accuracy=accuracy)
 
 
 def run_c2(args, ctx):
@@ -606,11 +800,12 @@ def run_c2(args, ctx):
                                            device=ctx.device))
     layer.v_cache.buffer.copy_(torch.randn(layer.v_cache.buffer.shape, generator=g,
                                            device=ctx.device))
-    wall, active, roof, (q_all, k_all, v_all) = _attention_workload(
+    wall, active, roof, (q_all, k_all, v_all), replay = _attention_workload(
         args, ctx, cache, lens0, steps, H, H, Dh, 4, 0, "c2")
     roof["note"] = "the 67 MB cache fits in the 256 MB Infinity Cache: not an HBM figure"
     cpu = None
-    if not args.no_cpu_baseline:
+    oracle_outs = []
+    if True:  # the CPU leg: timed unless --no-cpu-baseline; its first pass checks the GPU
         from oracle import c_oracle
 
         kc = layer.k_cache.buffer.cpu().numpy().reshape(B, T, H, Dh).copy()
@@ -619,7 +814,8 @@ def run_c2(args, ctx):
         # whole passes over the 256 steps (each restarts from the start lengths and
         # re-appends the same rows) until the time budget is spent
         passes, tok, t0 = 0, 0, time.perf_counter()
-        while passes == 0 or time.perf_counter() - t0 < args.cpu_seconds:
+        while passes == 0 or (not args.no_cpu_baseline
+                              and time.perf_counter() - t0 < args.cpu_seconds):
             lens = lens0.astype(np.int32).copy()
             for n in range(steps):
                 for b in range(B):
@@ -627,18 +823,24 @@ def run_c2(args, ctx):
                         kc[b, lens[b]], vc[b, lens[b]] = ks[n, b], vs[n, b]
                         lens[b] += 1
                         tok += 1
-                c_oracle.decode_attn(qs[n], kc, vc, lens, cache_bf16=False)
+                o = c_oracle.decode_attn(qs[n], kc, vc, lens, cache_bf16=False)
+                if passes == 0:
+                    oracle_outs.append(o)
             passes += 1
         dt = time.perf_counter() - t0
-        cpu = {"value": tok / dt, "unit": "tokens/s", "cores": c_oracle.threads(),
-               "kind": "port", "sample": f"{passes} passes over the {steps} C2 steps, "
-                                         f"oracle/c/kv_attn_ref.c with OpenMP, {dt:.1f} s"}
+        if not args.no_cpu_baseline:
+            cpu = {"value": tok / dt, "unit": "tokens/s", "cores": c_oracle.threads(),
+                   "kind": "port", "sample": f"{passes} passes over the {steps} C2 steps, "
+                                             f"oracle/c/kv_attn_ref.c with OpenMP, {dt:.1f} s"}
+    accuracy = accuracy_record(replay(len(oracle_outs)), oracle_outs, 1e-4,
+                               "oracle/c/kv_attn_ref.c on the same fp32 cache, every step of "
+                               "the timed run")
     return _record(
         "decode tokens/sec", active / wall, "tokens/s", steps, args.warmup, wall / steps * 1e3,
         "fp32",
         {"workload": "C2 KV microbench fp32: cache [8, 8, 2048, 64], start lengths U[1,2047], "
                      "256 steps of append + attention, full sequences retire", "batch": B},
-        roof, cpu)
+        roof, cpu, max_rel_err=accuracy["max_rel_err"], accuracy=accuracy)
 
 
 MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
@@ -715,6 +917,22 @@ def run_fb(args, ctx):
             "unit": "TFLOP/s", "frac": flops / call_s / 1e12 / MFMA_FP32_PEAK_TFLOPS,
             "traffic": None, "kernel": "skv_flash_bwd (k_fbwd_dq + k_fbwd_dkv), HIP events",
             "mean_call_us": call_s * 1e6, "algorithmic_flops": flops}
+    # same-run accuracy: the gradients of two (sequence, head) pairs against
+    # float64 autograd on the CPU over the same q, k, v, dO (norm-wise per tensor)
+    errs = []
+    for b, h in ((0, 0), (B_ - 1, H_ - 1)):
+        xs = [x.view(B_, N, H_, Dh)[b, :, h].double().cpu() for x in (q, k, v, do)]
+        qh, kh, vh = (x.clone().requires_grad_(True) for x in xs[:3])
+        mask = torch.ones(N, N, dtype=torch.bool).tril()
+        oh = torch.softmax((qh @ kh.T * sc).masked_fill(~mask, float("-inf")), -1) @ vh
+        want = torch.autograd.grad(oh, (qh, kh, vh), xs[3])
+        for gt, wt in zip((dq, dk, dv), want):
+            gh = gt.view(B_, N, H_, Dh)[b, :, h].double().cpu()
+            errs.append(float((gh - wt).norm() / wt.norm()))
+    accuracy = {"max_rel_err": max(errs), "tolerance": 1e-4, "pass": max(errs) <= 1e-4,
+                "against": "torch float64 autograd on the CPU, (sequence, head) (0, 0) and "
+                           "(7, 15) of the last timed call",
+                "norm": "||gpu - oracle||_F / ||oracle||_F per gradient tensor (dq, dk, dv)"}
     cpu = None
     if not args.no_cpu_baseline:
         # the reference's CPU path differentiates attention with JAX autodiff; the
@@ -739,7 +957,7 @@ def run_fb(args, ctx):
         args.warmup, wall / args.steps * 1e3, "fp32",
         {"workload": "FB causal flash-attention backward fp32: B=8, N=2048, H=16, D=64 "
                      "(O, L, M from skv_flash_fwd)", "batch": B_},
-        roof, cpu, forward=forward)
+        roof, cpu, forward=forward, max_rel_err=accuracy["max_rel_err"], accuracy=accuracy)
 
 
 def run_sample(args, ctx):
@@ -787,6 +1005,28 @@ def run_sample(args, ctx):
 
     one_s, _ = timed(False)
     call_s, wall = timed(True)
+    # same-run accuracy: the last timed call's draws (seed steps - 1) against
+    # the oracle's inverse-CDF draw from sample_token's distribution with the
+    # same uniform; a draw whose u * total lies within 1e-5 of a step of the
+    # running sum may take either neighbour
+    from oracle import sample_oracle as so
+    got = out.cpu().numpy()
+    lgh = logits.cpu().numpy().astype(np.float64)
+    seed = args.steps - 1
+    equal = ambiguous = 0
+    for m in range(M):
+        pr = so.sample_filter(lgh[m], 1.0)
+        u = so.splitmix_uniform(seed, m, 512)
+        c = np.cumsum(pr)
+        if int(got[m]) == so.sample_draw(pr, u):
+            equal += 1
+        elif np.abs(c - u * c[-1]).min() < 1e-5 * c[-1]:
+            ambiguous += 1
+    accuracy = {"max_rel_err": None, "draws": M, "draws_equal_oracle": equal,
+                "draws_at_a_rounding_step": ambiguous, "pass": equal + ambiguous == M,
+                "against": "oracle/sample_oracle.py (float64 sample_token filter + the same "
+                           "uniform), the last timed call's 16 draws; a draw is a token id, "
+                           "so it is checked for equality, not a relative error"}
     # the logits once, and the picked 2048-entry slice of each row again
     nbytes = M * V * 4 + M * 2048 * 4
     roof = {"bound": "launch latency", "achieved": nbytes / call_s / 1e9, "peak": HBM_PEAK_GBS,
@@ -815,7 +1055,8 @@ def run_sample(args, ctx):
                      "no min-p/top-k/top-p, no penalty (the reference's defaults)",
          "batch": M, "vocab": V},
         roof, cpu, one_workgroup_per_row={"mean_call_us": one_s * 1e6,
-                                          "kernel": "k_sample, one 1024-thread workgroup a row"})
+                                          "kernel": "k_sample, one 1024-thread workgroup a row"},
+        max_rel_err=None, accuracy=accuracy)
 
 
 def main():
@@ -917,11 +1158,21 @@ def main():
                 "mean_us": float(per.mean()), "median_us": float(np.median(per)),
                 "min_us": float(per.min()), "max_us": float(per.max()),
                 "first5_us": [round(float(x), 1) for x in per[:5]]}
-    prefill = None if args.no_prefill else time_prefill(ctx, cache, reps=10)
+    oracle_outs = []
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args, layer.k_cache.buffer, layer.v_cache.buffer, q_all, k_all,
-                           v_all)
+                           v_all, outs=oracle_outs)
+    else:  # no timing, but the same-run accuracy check still runs 2 steps of the oracle
+        short = argparse.Namespace(**{**vars(args), "steps": min(args.steps, 2)})
+        cpu_baseline(short, layer.k_cache.buffer, layer.v_cache.buffer, q_all, k_all, v_all,
+                     outs=oracle_outs)
+    gpu_outs = replay_outputs(step, len(oracle_outs), lambda: setattr(cache, "current_len", FILL),
+                              out)
+    accuracy = accuracy_record(gpu_outs, oracle_outs, 2e-2,
+                               "oracle/c/kv_attn_ref.c on the same bf16 cache values (fp32 "
+                               "math), the first steps of the timed run")
+    prefill = None if args.no_prefill else time_prefill(ctx, cache, reps=10)
 
     traffic = measured_traffic()
     rec = {
@@ -960,6 +1211,8 @@ def main():
             "per_call": per_call,
         },
         "cpu_baseline": _with_cpu_model(cpu),
+        "max_rel_err": accuracy["max_rel_err"],
+        "accuracy": accuracy,
         "prefill": prefill,
     }
     print(json.dumps(rec), flush=True)

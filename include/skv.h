@@ -374,7 +374,9 @@ int skv_argmax(int32_t* out, const float* x, int M, int N, void* ws, size_t ws_b
  * runs split over 2048-entry slices (two launches, many workgroups per row)
  * instead of one workgroup per row; its running sums are grouped by slice,
  * so a u * sum within float rounding of a step may draw the neighbouring
- * token. Calls that share ws must be stream ordered.
+ * token: the same seed and logits can therefore give a different token with
+ * ws than without it (only at such rounding boundaries; both draw from the
+ * same filtered distribution). Calls that share ws must be stream ordered.
  */
 int skv_sample(int32_t* out, float* probs_out, const float* logits, const int32_t* seq,
                int seq_stride, const int32_t* lens, int M, int V, float temperature, int top_k,
@@ -408,7 +410,8 @@ int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
                     int n_layers, int32_t* adv, skv_stream_t stream);
 
 /* skv_append_decode_attn for one query head per kv head (MHA), a
- * contiguous cache and head_dim 64 or 128, WITHOUT the fill advance: one
+ * contiguous cache (16-byte aligned for fp32, 8-byte for bf16; otherwise
+ * SKV_E_UNSUPPORTED) and head_dim 64 or 128, WITHOUT the fill advance: one
  * workgroup per (sequence, head) reads the head's whole filled row, folds in
  * the new token (stored at lens[b] when lens[b] in [0, T_cap)) and writes
  * the output; no split, no workspace, no merge pass. lens is left as it

@@ -200,6 +200,11 @@ extern "C" int skv_append_decode_attn_direct(void* out, const void* q, void* k_c
                   (q_dtype == SKV_F32 || q_dtype == SKV_BF16) &&
                   (out_dtype == SKV_F32 || out_dtype == SKV_BF16),
               SKV_E_INVALID, "%s: bad dtype", fn);
+  // the cache rows are read as 16-byte (fp32) or 8-byte (bf16) vectors
+  const uintptr_t al = cache_dtype == SKV_F32 ? 15 : 7;
+  SKV_REQUIRE((((uintptr_t)k_cache | (uintptr_t)v_cache) & al) == 0, SKV_E_UNSUPPORTED,
+              "%s: k_cache and v_cache must be %d-byte aligned for this cache dtype", fn,
+              (int)al + 1);
   DirectArgs a{out, q, k_cache, v_cache, new_k, new_v, lens, B, H, T_cap,
                scale * 1.4426950408889634f, q_dtype, in_dtype, out_dtype};
   hipStream_t s = (hipStream_t)stream;

@@ -234,19 +234,31 @@ class TransformerModel:
 
     # -- one decode step -----------------------------------------------------
 
-    def forward_step(self, cache: KVCache, ids: torch.Tensor) -> torch.Tensor:
+    def forward_step(self, cache: KVCache, ids: torch.Tensor, direct: bool = False) -> torch.Tensor:
         """Run token ids[b] of every sequence at its current fill through all
         layers, appending its K/V to the cache; returns logits [B, V] (a
         buffer reused by the next call). ids: int32 device tensor [B].
         Sequences whose cache is full are not appended to (their logits are
-        not meaningful)."""
+        not meaningful). direct: the attention of Generator's greedy steps
+        (skv_append_decode_attn_direct, which leaves the fills in place),
+        followed here by the fill advance of every layer that Generator's
+        next-token kernel does at the start of the following step."""
         B = cache.batch_size
         if cache.n_kv_heads != cache.n_heads or cache.paged:
             raise ValueError("the model path uses a contiguous multi-head cache")
+        if direct and not self._direct_ok():
+            raise ValueError("the direct attention takes head_dim 64 or 128 and contexts up "
+                             "to 1024 tokens")
         bf = self.buffers(B)
         if ids.data_ptr() != bf.ids.data_ptr():
             bf.ids.copy_(ids)
-        self._launch_step(cache, bf)
+        self._launch_step(cache, bf, direct=direct)
+        if direct:
+            L = _lib.lib()
+            s = _lib.stream_handle(self.ctx.device)
+            for layer in cache.layers:
+                _lib.check(L.skv_advance(layer.lens.data_ptr(), None, 1, B, cache.max_seq_len,
+                                         s), "skv_advance")
         # host mirror: every layer appended where the sequence had room
         for layer in cache.layers:
             layer.host_lens = np.minimum(layer.host_lens + 1, cache.max_seq_len)
@@ -452,8 +464,10 @@ class TransformerModel:
         # Ragged prompts: the projections run over the valid rows only, packed
         # (row off_b + i is token i of sequence b); q, k, v are gathered into
         # the [B, C] layout of the chunk append and the attention, and the
-        # attention output back. Each projection row is computed alone, so the
-        # valid rows' values are the padded layout's, bit for bit.
+        # attention output back. The projections then run over Mp rows instead
+        # of B * C, which can select another skv_linear kernel (it picks one by
+        # row count), so the valid rows agree with the padded layout's within
+        # fp32 rounding, not necessarily bit for bit.
         Mp = int(n_host.sum())
         # (packed q, k, v are staged in ff's space: 3 Mp d <= M mlp)
         packed = (not all_logits and 0 < Mp <= (3 * M) // 4
@@ -762,10 +776,14 @@ class Generator:
         self.model.prefill(self.cache, self.prompt_host, self.plen)
         self._pick()
 
-    def run(self) -> List[List[int]]:
+    def run(self, on_step=None) -> List[List[int]]:
         """From the start (reset(): an empty cache, the prompts only), the
         prefill, then all decode steps; returns every sequence's tokens
-        (prompt + output). Repeated calls reuse the captured graph."""
+        (prompt + output). Repeated calls reuse the captured graph.
+        on_step(j, logits) (optional) is called after decode step j with the
+        step's logits buffer [B, V] (stream ordered: copy it on the device,
+        it is overwritten by the next step); row b's step j ran the token at
+        position prompt_len[b] + j."""
         if not self._fresh:  # an explicit reset() since the last run or prefill is enough
             self.reset()
         self.prefill()
@@ -773,6 +791,8 @@ class Generator:
         if steps > 0:
             if self.use_graph:
                 self._one_step()  # eager first step: workspaces exist before capture
+                if on_step is not None:
+                    on_step(0, self.bufs.logits)
                 torch.cuda.synchronize()
                 if self.graph is None and steps > 1:
                     # stream capture records the launches without running them
@@ -780,11 +800,15 @@ class Generator:
                     with torch.cuda.graph(g):
                         self._one_step()
                     self.graph = g
-                for _ in range(steps - 1):
+                for j in range(1, steps):
                     self.graph.replay()
+                    if on_step is not None:
+                        on_step(j, self.bufs.logits)
             else:
-                for _ in range(steps):
+                for j in range(steps):
                     self._one_step()
+                    if on_step is not None:
+                        on_step(j, self.bufs.logits)
         # record the last new token at its position
         L = _lib.lib()
         s = _lib.stream_handle(self.model.ctx.device)
@@ -797,6 +821,16 @@ class Generator:
                                          self.cache.layers[0].lens.data_ptr(), self.B,
                                          self.prompt.shape[1], self.seq.shape[1],
                                          *self._retire_args(), s), "skv_next_tokens")
+        # The fills left behind are the cache's real contents: retired rows
+        # (-1 on the device) get back the positions they hold, every token but
+        # the last one recorded (the prompt's when nothing was generated), and
+        # no deferred advance stays pending, so forward_step or prefill on
+        # self.cache continue from there.
+        if self.retire:
+            held = np.minimum(np.maximum(self.tot - 1, self.plen), self.cache.max_seq_len)
+            self.lens_all.copy_(torch.from_numpy(
+                np.broadcast_to(held.astype(np.int32), self.lens_all.shape).copy()))
+        self.adv.zero_()
         for layer in self.cache.layers:
             layer.host_lens = layer.lens.cpu().numpy().astype(np.int64)
         seq = self.seq.cpu().numpy()

@@ -355,3 +355,13 @@ def test_step_entry_points_reject_bad_arguments():
                                            64, 0.1, 0, 0, 0, 0, None) == _lib.SKV_E_UNSUPPORTED
     assert L.skv_append_decode_attn_direct(fake, fake, fake, fake, None, fake, fake, 2, 4, 64,
                                            64, 0.1, 0, 0, 0, 0, None) == _lib.SKV_E_INVALID
+    # the cache rows are read as vectors: 16-byte (fp32) or 8-byte (bf16)
+    # aligned caches only (rejected before any launch)
+    for cdt, off in ((0, 8), (0, 4), (1, 4), (1, 2)):
+        rc = L.skv_append_decode_attn_direct(fake, fake, fake + off, fake, fake, fake, fake, 2, 4,
+                                             64, 64, 0.1, cdt, 0, 0, 0, None)
+        assert rc == _lib.SKV_E_UNSUPPORTED, (cdt, off)
+        assert b"aligned" in L.skv_last_error()
+        rc = L.skv_append_decode_attn_direct(fake, fake, fake, fake + off, fake, fake, fake, 2, 4,
+                                             128, 64, 0.1, cdt, 0, 0, 0, None)
+        assert rc == _lib.SKV_E_UNSUPPORTED, (cdt, off)

@@ -27,3 +27,44 @@ def test_paged_cache_without_a_table_is_rejected():
         _check_layer(cache, -1)
     cache.block_table = object()
     _check_layer(cache, 0)
+
+
+def test_backend_forward_rejects_shapes_before_any_device_work():
+    """forward() (jax_backend.py:143-148's drop-in) checks n_heads * head_dim
+    against the embedding and n_layers against the params first."""
+    from simple_llm_amd import backend
+    from oracle import model_oracle as mo
+
+    params = mo.init_params(50, 64, 2, 16, seed=0)
+    toks = np.zeros((1, 4), np.int32)
+    with pytest.raises(ValueError, match="does not match the embedding dim 64"):
+        backend.forward(params, toks, 2, 3, 16)
+    with pytest.raises(ValueError, match="params hold 2 layers, n_layers=3"):
+        backend.forward(params, toks, 3, 4, 16)
+    with pytest.raises(ValueError, match="missing"):
+        backend.forward({"embedding": params["embedding"]}, toks, 2, 4, 16)
+    assert not backend._models  # nothing was built
+
+
+def test_backend_sample_token_rejects_bad_parameters():
+    from simple_llm_amd import backend
+
+    lg = np.zeros(10, np.float32)
+    for args in ((-1.0, 0, 1.0, 0.0, 1.0), (1.0, -2, 1.0, 0.0, 1.0), (1.0, 0, 1.0, -0.1, 1.0),
+                 (1.0, 0, 1.0, 0.0, 0.0)):
+        with pytest.raises(ValueError, match="bad sampling parameters"):
+            backend.sample_token(0, lg, *args, [])
+    with pytest.raises(ValueError, match="at least one entry"):
+        backend.sample_token(0, np.zeros(0, np.float32), 1.0, 0, 1.0, 0.0, 1.0, [])
+
+
+def test_backend_seed_of_keys():
+    """An int key is the seed; an array key (a PRNG key's words) folds to a
+    64-bit seed that depends on every word."""
+    from simple_llm_amd.backend import _seed_of
+
+    assert _seed_of(42) == 42 and _seed_of(-1) == (1 << 64) - 1
+    a = _seed_of(np.array([0, 42], np.uint32))
+    assert a == _seed_of([0, 42]) and 0 <= a < (1 << 64)
+    assert a != _seed_of(np.array([0, 43], np.uint32))
+    assert a != _seed_of(np.array([1, 42], np.uint32))

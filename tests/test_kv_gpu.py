@@ -624,3 +624,189 @@ def test_c2_full_run_every_step_matches_c_oracle(gpu_ctx, variant):
     retired = int((lens == T).sum())
     print(f"worst rel_err over {steps} steps = {worst:.3e}; sequences retired: {retired}")
     assert retired == (0 if variant == "bench" else 4)
+
+
+# ---------------------------------------------------------------------------
+# The exact calls the benchmarks time, at their full sizes
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("B,H,D,T,dt", [(1, 4, 64, 256, "f32"), (1, 4, 64, 256, "bf16"),
+                                         (16, 12, 64, 1024, "f32"), (16, 12, 64, 1024, "bf16")])
+def test_direct_attention_matches_oracle(gpu_ctx, B, H, D, T, dt):
+    """skv_append_decode_attn_direct, the attention of the C1 (B=1, 4 x 64,
+    context 256) and C3 (B=16, 12 x 64, context 1024) greedy steps, against
+    the float64 oracle over a host mirror of the cache: empty, ragged, last
+    free position, full (no append) and retired (negative fill: zero output)
+    rows; the appended rows bit-exact and the fills left in place."""
+    banner(f"direct attention vs oracle B={B} H={H} D={D} T={T} {dt}")
+    from simple_llm_amd import _lib
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    cdt = _lib.BF16 if dt == "bf16" else _lib.F32
+    r = np.random.default_rng(B * 7 + T)
+    kc = torch.from_numpy(r.standard_normal((B, T, H, D)).astype(np.float32)).cuda().to(tdt)
+    vc = torch.from_numpy(r.standard_normal((B, T, H, D)).astype(np.float32)).cuda().to(tdt)
+    kw = kc.float().cpu().numpy()
+    vw = vc.float().cpu().numpy()
+    # B = 1: one call per kind of row; B = 16: every kind in one call
+    special = [0, int(r.integers(1, T - 1)), T - 1, T, -1]
+    calls = ([np.array([f]) for f in special] if B == 1 else
+             [np.concatenate([special, r.integers(0, T, B - len(special))])])
+    for fills in calls:
+        q, kn, vn = (r.standard_normal((B, H, D)).astype(np.float32) for _ in range(3))
+        lens = to_dev(fills.astype(np.int32), torch.int32)
+        out = torch.full((B, H, D), float("nan"), device="cuda")
+        qd, knd, vnd = to_dev(q), to_dev(kn), to_dev(vn)  # held: the call reads them later
+        _lib.check(L.skv_append_decode_attn_direct(
+            out.data_ptr(), qd.data_ptr(), kc.data_ptr(), vc.data_ptr(), knd.data_ptr(),
+            vnd.data_ptr(), lens.data_ptr(), B, H, D, T, D ** -0.5, cdt, _lib.F32, _lib.F32,
+            _lib.F32, s), "skv_append_decode_attn_direct")
+        torch.cuda.synchronize()
+        att = np.zeros(B, np.int64)
+        for b, f in enumerate(fills):
+            if 0 <= f < T:
+                kw[b, f] = ko.storage_round(kn[b], "bf16" if dt == "bf16" else "fp32")
+                vw[b, f] = ko.storage_round(vn[b], "bf16" if dt == "bf16" else "fp32")
+                att[b] = f + 1
+            elif f >= T:
+                att[b] = T
+        np.testing.assert_array_equal(lens.cpu().numpy(), fills)  # no advance
+        np.testing.assert_array_equal(kc.float().cpu().numpy(), kw)
+        np.testing.assert_array_equal(vc.float().cpu().numpy(), vw)
+        got = out.cpu().numpy()
+        want = ko.decode_attention(q, kw, vw, att)
+        live = att > 0
+        err = rel_err(got[live], want[live]) if live.any() else 0.0
+        print(f"fills={fills.tolist()[:6]} rel_err={err:.3e}")
+        assert err < FP32_TOL  # the same (rounded) cache values on both sides
+        assert not got[~live].any()  # retired rows give 0
+
+
+def _c4_bench_cache(gpu, ctx):
+    """The C4 cache as bench.py builds it: [4, 32768, 16, 128] bf16, each
+    sequence filled to 32000 with N(0, 1) from torch generator seed 0."""
+    B, T, H, D, fill = 4, 32768, 16, 128, 32000
+    cache = gpu.kv_cache_create(ctx, gpu.KVCacheConfig(B, T, 1, H, D, dtype=torch.bfloat16))
+    layer = cache.layers[0]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    kv = layer.k_cache.buffer.view(B, T, H, D)
+    vv = layer.v_cache.buffer.view(B, T, H, D)
+    for b in range(B):
+        kv[b, :fill].copy_(torch.randn((fill, H, D), generator=g, device="cuda"))
+        vv[b, :fill].copy_(torch.randn((fill, H, D), generator=g, device="cuda"))
+    cache.current_len = fill
+    return cache, kv, vv
+
+
+def test_append_attend_full_size_c4_bench_plan(gpu_ctx):
+    """Three steps of kv_cache_append_attend at C4's full size with the plan
+    of bench.py's C4 line (max_len = 32000 + 256 steps), the call the
+    headline number times: the fills, the appended rows (bit-exact) and the
+    output of sampled (sequence, head) pairs against the float64 oracle over
+    the device cache's own bf16 values."""
+    banner("append+attend C4 full size, bench plan")
+    gpu = _gpu()
+    B, T, H, D, fill = 4, 32768, 16, 128, 32000
+    cache, kv, vv = _c4_bench_cache(gpu, gpu_ctx)
+    chunk, n_chunks = gpu.decode_plan(gpu_ctx, B, H, H, fill + 256, head_dim=D,
+                                      dtype=torch.bfloat16)
+    print(f"plan: chunk_tokens={chunk} n_chunks={n_chunks}")
+    g = torch.Generator(device="cuda").manual_seed(2)
+    out = torch.empty((B, H, D), device="cuda")
+    pairs = [(0, 0), (0, 15), (1, 7), (2, 3), (2, 12), (3, 9)]
+    worst = 0.0
+    for step in range(3):
+        q, kn, vn = (torch.randn((B, H, D), generator=g, device="cuda") for _ in range(3))
+        fills = gpu.kv_cache_append_attend(gpu_ctx, cache, 0, kn, vn, q, out, max_len=fill + 256)
+        n = fill + step + 1
+        np.testing.assert_array_equal(fills, [n] * B)
+        assert cache.layers[0].lens.cpu().tolist() == [n] * B
+        np.testing.assert_array_equal(kv[:, n - 1].float().cpu().numpy(),
+                                      ko.bf16_round(kn.cpu().numpy()))
+        np.testing.assert_array_equal(vv[:, n - 1].float().cpu().numpy(),
+                                      ko.bf16_round(vn.cpu().numpy()))
+        got, qh = out.cpu().numpy(), q.cpu().numpy()
+        for b, h in pairs:
+            kh = kv[b, :n, h].float().cpu().numpy()[None, :, None, :]
+            vh = vv[b, :n, h].float().cpu().numpy()[None, :, None, :]
+            want = ko.decode_attention(qh[b:b + 1, h:h + 1], kh, vh, [n])
+            worst = max(worst, rel_err(got[b:b + 1, h:h + 1], want))
+    print(f"worst rel_err over 3 steps x {len(pairs)} heads = {worst:.3e}")
+    assert worst < FP32_TOL  # the same bf16 values, fp32 accumulation
+
+
+def test_append_attend_full_size_c5_bench_plan(gpu_ctx):
+    """Three steps of the paged kv_cache_append_attend at C5's full size, built
+    as bench.py's C5 line builds it (64 sequences, 32 query heads over 8 kv
+    heads, D=128, bf16 16-token pages under the seeded page table, lognormal
+    lengths, max_len = longest + 128 steps: the matrix-core plan): every
+    output against the C restatement of the oracle over a host copy of the
+    pool gathered into a contiguous cache and updated by the append rule, and
+    the appended rows bit-exact."""
+    banner("append+attend C5 full size, bench plan")
+    from oracle import c_oracle
+    gpu = _gpu()
+    B, Hq, Hkv, D, bs, steps = 64, 32, 8, 128, 16, 128
+    r = np.random.default_rng(0)
+    lens0 = np.clip(np.exp(r.normal(np.log(1500), 0.8, B)), 16, 8192).astype(np.int64)
+    max_seq = 8192 + steps
+    max_blocks = -(-max_seq // bs)
+    need = -(-(lens0 + steps) // bs)
+    n_blocks = int(need.sum())
+    cache = gpu.kv_cache_create(gpu_ctx, gpu.KVCacheConfig(B, max_seq, 1, Hq, D, n_kv_heads=Hkv,
+                                                           dtype=torch.bfloat16, block_size=bs,
+                                                           n_blocks=n_blocks))
+    perm = r.permutation(n_blocks).astype(np.int32)
+    table = np.zeros((B, max_blocks), np.int32)
+    o = 0
+    for b in range(B):
+        table[b, :need[b]] = perm[o:o + need[b]]
+        o += need[b]
+    gpu.kv_cache_set_block_table(cache, torch.from_numpy(table))
+    layer = cache.layers[0]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for buf in (layer.k_cache.buffer, layer.v_cache.buffer):
+        for i in range(0, buf.shape[0], 1 << 16):
+            part = buf[i:i + (1 << 16)]
+            part.copy_(torch.randn(part.shape, generator=g, device="cuda"))
+    layer.lens.copy_(torch.from_numpy(lens0.astype(np.int32)))
+    layer.host_lens = lens0.copy()
+    max_len = int(min(lens0.max() + steps, max_blocks * bs))
+    chunk, n_chunks = gpu.decode_plan(gpu_ctx, B, Hq, Hkv, max_len, int(lens0.sum()),
+                                      head_dim=D, dtype=torch.bfloat16)
+    print(f"plan: chunk_tokens={chunk} n_chunks={n_chunks}")
+    nb = int(need.max())
+    tab = torch.from_numpy(table[:, :nb].astype(np.int64)).cuda()
+
+    def gather(buf):
+        x = buf.view(n_blocks, bs, Hkv, D)[tab].reshape(B, nb * bs, Hkv, D)
+        return x.view(torch.int16).cpu().numpy().view(np.uint16).copy()
+
+    kc, vc = gather(layer.k_cache.buffer), gather(layer.v_cache.buffer)
+    g2 = torch.Generator(device="cuda").manual_seed(2)
+    out = torch.empty((B, Hq, D), device="cuda")
+    lens = lens0.copy()
+    bits = lambda x: x.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+    for step in range(3):
+        q = torch.randn((B, Hq, D), generator=g2, device="cuda")
+        kn = torch.randn((B, Hkv, D), generator=g2, device="cuda")
+        vn = torch.randn((B, Hkv, D), generator=g2, device="cuda")
+        fills = gpu.kv_cache_append_attend(gpu_ctx, cache, 0, kn, vn, q, out, max_len=max_len)
+        kb, vb = bits(kn), bits(vn)
+        for b in range(B):
+            kc[b, lens[b]], vc[b, lens[b]] = kb[b], vb[b]
+        lens += 1
+        np.testing.assert_array_equal(fills, lens)
+        # the appended rows in the pool (row lens-1 of each sequence's pages)
+        t = lens - 1
+        rows = torch.from_numpy((table[np.arange(B), t // bs].astype(np.int64) * bs + t % bs)).cuda()
+        pk = layer.k_cache.buffer.view(-1, Hkv, D)[rows]
+        pv = layer.v_cache.buffer.view(-1, Hkv, D)[rows]
+        np.testing.assert_array_equal(pk.view(torch.int16).cpu().numpy().view(np.uint16), kb)
+        np.testing.assert_array_equal(pv.view(torch.int16).cpu().numpy().view(np.uint16), vb)
+        want = c_oracle.decode_attn(q.cpu().numpy(), kc, vc, lens, cache_bf16=True)
+        err = rel_err(out.cpu().numpy(), want)
+        print(f"step {step}: rel_err={err:.3e}")
+        assert err < FP32_TOL  # the same bf16 values, fp32 accumulation on both sides

@@ -668,10 +668,11 @@ def test_model_loaded_from_checkpoint_dir(gpu_ctx, tmp_path):
 # ---------------------------------------------------------------------------
 
 
-def _prefill_decode_logits(m, tokens, plen, n_prefill_pad=None):
+def _prefill_decode_logits(m, tokens, plen, n_prefill_pad=None, direct=False):
     """Logits of every position of each sequence computed as generate does:
     one ragged prefill of the prompts (logits of every prompt row), then one
-    cached decode step per position, teacher forced. tokens [B, T]."""
+    cached decode step per position, teacher forced. tokens [B, T]. direct:
+    the steps take the direct attention of Generator's greedy steps."""
     B, T = tokens.shape
     V = m.tm_params.vocab_size
     cache = m.new_cache(B)
@@ -683,7 +684,7 @@ def _prefill_decode_logits(m, tokens, plen, n_prefill_pad=None):
     pos = np.array(plen, np.int64)
     while (pos < T).any():
         ids = tokens[np.arange(B), np.minimum(pos, T - 1)].astype(np.int32)
-        lg = m.forward_step(cache, dev(ids)).cpu().numpy()
+        lg = m.forward_step(cache, dev(ids), direct=direct).cpu().numpy()
         for b in range(B):
             if pos[b] < T:
                 out[b, pos[b]] = lg[b]
@@ -691,14 +692,17 @@ def _prefill_decode_logits(m, tokens, plen, n_prefill_pad=None):
     return out
 
 
+@pytest.mark.parametrize("direct", [False, True])
 @pytest.mark.parametrize("shape", ["c1", "c3"])
 @pytest.mark.parametrize("kv,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, 2e-2)])
-def test_prefill_then_decode_logits_match_oracle(gpu_ctx, shape, kv, tol):
+def test_prefill_then_decode_logits_match_oracle(gpu_ctx, shape, kv, tol, direct):
     """Ragged prompts prefilled at once, then teacher-forced decode: the
     logits at every position equal the float64 forward (1e-4 with an fp32
     cache, 2e-2 with a bf16 one). C1's model (4 x 256, vocab 256) and C3's
-    (12 x 768, vocab 50304), N(0, 0.02) from seed 0."""
-    banner(f"prefill then decode {shape} kv={kv}")
+    (12 x 768, vocab 50304), N(0, 0.02) from seed 0. direct: the decode steps
+    take skv_append_decode_attn_direct, the attention the C1 and C3 benches
+    time (their greedy Generator steps), with the fill advance after it."""
+    banner(f"prefill then decode {shape} kv={kv} direct={direct}")
     if shape == "c1":
         m, params = make_model(gpu_ctx, 256, 256, 4, 4, 256, seed=0, std=0.02, kv=kv)
         n_heads, T, plen = 4, 120, [64, 9, 100]
@@ -707,12 +711,13 @@ def test_prefill_then_decode_logits_match_oracle(gpu_ctx, shape, kv, tol):
         n_heads, T, plen = 12, 90, [70, 33]
     V = m.tm_params.vocab_size
     toks = np.random.default_rng(11).integers(0, V, (len(plen), T))
-    got = _prefill_decode_logits(m, toks, plen)
+    assert not direct or m._direct_ok()
+    got = _prefill_decode_logits(m, toks, plen, direct=direct)
     want = mo.forward(params, toks, n_heads)
     err = rel_rows(got, want)
     print(f"rel_err={err:.3e}")
     assert err < tol
-    if kv == torch.float32:  # prefill alone, every row (the reference's forward)
+    if kv == torch.float32 and not direct:  # prefill alone, every row (the reference's forward)
         assert rel_rows(m.forward(toks), want) < tol
 
 
@@ -828,10 +833,23 @@ def test_retired_rows_keep_the_tokens(gpu_ctx, fused):
     prompts = [r.integers(0, 300, n).tolist() for n in (3, 40, 11, 25)]
     tot = [90, 60, 96, 41]
     g = M.Generator(m, prompts, tot, use_graph=True, fused_tail=fused)
-    a = g.run()
+    fills_at = {}
+
+    def on_step(j, logits):
+        if j in (0, g.steps - 1):
+            fills_at[j] = g.lens_all.cpu().numpy().copy()
+
+    a = g.run(on_step=on_step)
     # every row records its last token at some call (the longest ones at the
-    # one after the last step) and retires there
-    assert (g.lens_all.cpu().numpy() == -1).all()
+    # one after the last step) and retires there: at the last step only the
+    # longest-running row (0: 87 new tokens) is live, the others read -1 in
+    # every layer
+    last = fills_at[g.steps - 1]
+    assert (last[:, [1, 2, 3]] == -1).all() and (last[:, 0] >= 0).all()
+    assert (fills_at[0] >= 0).all()
+    # after run() the fills are the positions each row holds (retired rows too)
+    held = np.maximum(np.array(tot) - 1, [len(p) for p in prompts])
+    np.testing.assert_array_equal(g.lens_all.cpu().numpy(), np.broadcast_to(held, last.shape))
     sq = g.seq.cpu().numpy()
     assert not sq[1, 60:].any() and not sq[3, 41:].any()
     b = M.Generator(m, prompts, tot, use_graph=True, fused_tail=fused, retire_rows=False).run()
@@ -974,3 +992,85 @@ def test_c3_bench_generate_long_positions(gpu_ctx, kv, tol):
         err = rel_rows(got, want[j])
         print(f"sequence {i} (prompt {plen[i]}): rel_err={err:.3e}")
         assert err < tol
+
+
+def _packs(m, B, C, n_new):
+    """The condition under which TransformerModel.prefill packs the valid
+    rows (restated from its host logic)."""
+    M, Mp = B * C, int(np.sum(n_new))
+    return 0 < Mp <= (3 * M) // 4 and 3 * Mp * m.tm_params.embedding_dim <= M * m.mlp_dim
+
+
+@pytest.mark.parametrize("shape", ["c1", "c3"])
+def test_packed_ragged_prefill_rows_match_oracle(gpu_ctx, shape):
+    """A ragged prefill without all_logits packs the valid rows (projections
+    over them only, q/k/v gathered into the [B, C] layout and the attention
+    output back): each sequence's returned logits row equals the float64
+    forward's last prompt row and the unpacked prefill's, for prompts of C,
+    1 and 0 tokens; then a decode step on the packed prefill's cache matches
+    the oracle too (its K/V went in at the right rows)."""
+    banner(f"packed ragged prefill {shape}")
+    if shape == "c1":
+        m, params = make_model(gpu_ctx, 256, 256, 4, 4, 256, seed=0, std=0.02)
+        heads, C, n_new = 4, 40, [40, 1, 0, 17]
+    else:
+        m, params = make_model(gpu_ctx, 50304, 768, 12, 12, 1024, seed=0, std=0.02)
+        heads, C, n_new = 12, 48, [48, 1, 0, 20]
+    B, V = len(n_new), m.tm_params.vocab_size
+    assert _packs(m, B, C, n_new)
+    toks = np.random.default_rng(21).integers(0, V, (B, C + 1))
+    cache = m.new_cache(B)
+    got = m.prefill(cache, toks[:, :C], np.array(n_new)).cpu().numpy()
+    np.testing.assert_array_equal(cache.layers[0].lens.cpu().numpy(), n_new)
+    ref = m.prefill(m.new_cache(B), toks[:, :C], np.array(n_new), all_logits=True).cpu().numpy()
+    for b, n in enumerate(n_new):
+        if n == 0:
+            continue
+        want = mo.forward(params, toks[b:b + 1, :n], heads, last=1)[0]
+        e1, e2 = rel_rows(got[b:b + 1], want), rel_rows(got[b:b + 1], ref[b, n - 1:n])
+        print(f"row {b} (n={n}): vs oracle {e1:.3e}, vs unpacked {e2:.3e}")
+        assert e1 < FP32_TOL and e2 < FP32_TOL
+    # one decode step on top: token n_new[b] of each sequence at position n_new[b]
+    ids = toks[np.arange(B), n_new].astype(np.int32)
+    lg = m.forward_step(cache, dev(ids)).cpu().numpy()
+    for b, n in enumerate(n_new):
+        want = mo.forward(params, toks[b:b + 1, :n + 1], heads, last=1)[0]
+        assert rel_rows(lg[b:b + 1], want) < FP32_TOL, b
+
+
+@pytest.mark.parametrize("retire", [True, False])
+@pytest.mark.parametrize("direct", [True, False])
+def test_cache_after_run_continues(gpu_ctx, retire, direct):
+    """After Generator.run() the cache holds what the run put in it: with
+    retired rows, every layer's fill is the row's last recorded token's
+    position (the prompt length when nothing was generated), without
+    retirement the prompt plus every step; no deferred advance is pending.
+    A forward_step on g.cache then continues each sequence: its logits equal
+    the float64 forward over the sequence's recorded tokens."""
+    banner(f"cache after run retire={retire} direct={direct}")
+    from simple_llm_amd import model as M
+    m, params = make_model(gpu_ctx, 61, 128, 2, 2, 80, seed=5, std=0.2)
+    r = np.random.default_rng(8)
+    plen, tot = np.array([5, 20, 12]), np.array([30, 25, 12])
+    prompts = [r.integers(0, 61, n).tolist() for n in plen]
+    g = M.Generator(m, prompts, tot, use_graph=True, retire_rows=retire,
+                    direct_attention=direct)
+    assert g.direct == direct
+    out = g.run()
+    steps = int((tot - 1 - plen).max())
+    want_fill = (np.maximum(tot - 1, plen) if retire
+                 else np.minimum(plen + steps, m.tm_params.context_size))
+    for layer in g.cache.layers:
+        np.testing.assert_array_equal(layer.lens.cpu().numpy(), want_fill)
+        np.testing.assert_array_equal(layer.host_lens, want_fill)
+    assert not g.adv.any()
+    assert g.cache.current_len == int(want_fill.max())
+    seq = g.seq.cpu().numpy()
+    for b in range(3):
+        assert out[b] == seq[b, :tot[b]].tolist()
+    live = [b for b in range(3) if retire is False or tot[b] > plen[b]]
+    ids = np.array([seq[b, want_fill[b]] if b in live else 0 for b in range(3)], np.int32)
+    lg = m.forward_step(g.cache, dev(ids)).cpu().numpy()
+    for b in live:
+        want = mo.forward(params, seq[b:b + 1, :want_fill[b] + 1], 2, last=1)[0]
+        assert rel_rows(lg[b:b + 1], want) < FP32_TOL, b

@@ -83,11 +83,12 @@ def test_noalloc_rejects_plans_above_the_maximum(gpu_ctx):
     from simple_llm_amd import _lib
     L = _lib.lib()
     # a plan of 64 sequences x 64 heads x 2049 slots needs ~2.2 GB: rejected
-    # by the size check, before any pointer is used
+    # by the size check, before any pointer is used (the pointers are NULL, so
+    # the null-pointer check would stop the call before any launch even if the
+    # size check did not)
     B, Hq, D, n = 64, 64, 128, 2049
     assert L.skv_decode_workspace_bytes(B, Hq, D, n) > MAX_BYTES
-    fake = 4096
-    rc = L.skv_decode_attn_noalloc(fake, fake, fake, fake, fake, B, Hq, Hq, D, 1 << 20, 0.1, 512,
+    rc = L.skv_decode_attn_noalloc(None, None, None, None, None, B, Hq, Hq, D, 1 << 20, 0.1, 512,
                                    n, 1, 0, 0, None)
     assert rc == _lib.SKV_E_WORKSPACE
     assert b"maximum" in L.skv_last_error()
