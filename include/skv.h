@@ -131,9 +131,11 @@ size_t skv_decode_workspace_bytes(int B, int H_q, int D, int n_chunks_max);
  *                  . V[b, 0:lens[b], h/G, :],           G = H_q / H_kv.
  * No length cap (the reference caps lens at 256). lens[b] == 0 gives zeros.
  * q, out: [B, H_q, D] of q_dt / out_dt. G in {1, 2, 4, 8}. D: any head dim
- * from 1 to 256 (the reference takes any, gpu_kernels.py:2846); 64 and 128
- * run kernels tuned per shape, others the same kernels at the head dim
- * padded to 32, 64, 128 or 256; G = 8 takes D <= 128.
+ * (the reference takes any, gpu_kernels.py:2846) up to 2048 for G <= 2,
+ * 1024 for G = 4 and 512 for G = 8; 64 and 128 run kernels tuned per shape,
+ * others the same kernels at the head dim padded to a power of two from 32
+ * (rows of 16 lanes up to 256, 128 with G = 8; rows of a whole wavefront
+ * past that). Larger head dims return SKV_E_UNSUPPORTED.
  * Split-K: pass 1 writes per-piece (max, sum, unnormalised o) partials into
  * ws; pass 2 merges them. n_chunks_max >= 2. A sequence whose tokens lie
  * past the first B * (n_chunks_max - 1) * chunk_tokens tokens of the flat
@@ -221,12 +223,13 @@ size_t skv_prefill_workspace_bytes(int B, int C, int H_q, int D, int n_splits);
  * q, out: [B, C, H_q, D] of q_dt / out_dt; n_new may be NULL (C for all).
  * Requires start[b] + n_new[b] <= T_cap.
  * bf16 cache: Q, K, V and the probabilities enter v_mfma_f32_32x32x16_bf16
- * as bf16, accumulation and softmax are fp32; D from 1 to 128 (64 and 128
- * as they are, others padded to 32, 64 or 128 with zeros); G = H_q / H_kv
- * in {1, 2, 4, 8}; split over the prefix by n_splits; out, q, the caches and
- * ws 16-byte aligned.
+ * as bf16, accumulation and softmax are fp32; D from 1 to 256 (64, 128 and
+ * 256 as they are, others padded to 32, 64, 128 or 256 with zeros; the
+ * reference's largest flash_attn_max_head_dim is 256, gpu_device.py:468-471);
+ * G = H_q / H_kv in {1, 2, 4, 8}; split over the prefix by n_splits; out, q,
+ * the caches and ws 16-byte aligned.
  * fp32 cache: q and out fp32, every product in fp32 (v_mfma_f32_32x32x2_f32,
- * the kernel of skv_flash_fwd); D from 1 to 128, any G; n_splits and the
+ * the kernel of skv_flash_fwd); D from 1 to 256, any G; n_splits and the
  * workspace are not used.
  */
 int skv_prefill_attn(void* out, const void* q, const void* k_cache, const void* v_cache,
@@ -481,9 +484,10 @@ int skv_next_embed(float* x, int32_t* ids, int32_t* seq, const int32_t* argmax_p
  *   M = row max of S, L = sum exp(S - M), out = softmax(S) V.
  * q, k, v, out: [B, N, H, D] fp32 (the reference's [B*N, H*D] buffers),
  * 16-byte aligned; L, M: [B, N, H] fp32, or NULL to skip them.
- * D from 1 to 128 (the reference's default flash_attn_max_head_dim;
- * gpu_types.py:93): the kernels run at D padded to a multiple of 16, with
- * zeros past D. Products on v_mfma_f32_32x32x2_f32 (fp32).
+ * D from 1 to 256 (the reference's flash_attn_max_head_dim is 128 by
+ * default, gpu_types.py:93, and at most 256, gpu_device.py:468-471): the
+ * kernel runs at D padded to a multiple of 16 up to 128, to 192 or 256
+ * past it, with zeros past D. Products on v_mfma_f32_32x32x2_f32 (fp32).
  */
 int skv_flash_fwd(float* out, float* L, float* M, const float* q, const float* k, const float* v,
                   int B, int N, int H, int D, float scale, skv_stream_t stream);
@@ -502,7 +506,9 @@ size_t skv_flash_bwd_workspace_bytes(int B, int N, int H);
  * q, k, v, o, dout, dq, dk, dv: [B, N, H, D] fp32 (the reference's
  * [B*N, H*D] buffers), 16-byte aligned; L, M: [B, N, H] fp32, the forward's
  * softmax sums and row maxima of the scaled scores (the reference's L and M
- * buffers). The outputs must not overlap the inputs. D from 1 to 128.
+ * buffers). The outputs must not overlap the inputs. D from 1 to 128 (past
+ * it SKV_E_UNSUPPORTED: the kernels keep two 32-row operands and an
+ * accumulator of the head dim in each wavefront's registers).
  * Products run on v_mfma_f32_32x32x2_f32 (fp32); no atomics, so results are
  * bitwise reproducible.
  */

@@ -57,12 +57,13 @@ __device__ __forceinline__ void merge_pieces(const float* __restrict__ ws_o,
   }
 }
 
-// Pass 2: grid (Hq, B), 256 threads = 8 piece streams x 32 lanes; lane i of a
-// stream owns elements [i*D/32, (i+1)*D/32). Sequence b's pieces are the
-// slots w + b for the workgroups w its token range [cum[b], cum[b+1])
-// overlaps. Each stream merges pieces n = stream, stream + 8, ... online;
-// the 8 streams merge in LDS.
-template <int D, bool MASK>
+// Pass 2: grid (Hq, B), 256 threads = NS piece streams x 256/NS lanes; lane
+// i of a stream owns elements [i*EPL, (i+1)*EPL), EPL = D*NS/256 (8 streams
+// of 32 lanes up to a head dim of 256, 2 streams of 128 lanes past it).
+// Sequence b's pieces are the slots w + b for the workgroups w its token
+// range [cum[b], cum[b+1]) overlaps. Each stream merges pieces n = stream,
+// stream + NS, ... online; the NS streams merge in LDS.
+template <int D, bool MASK, int NS = 8>
 __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, int out_dt,
                                                       const long long* __restrict__ cum,
                                                       const float* __restrict__ ws_o,
@@ -70,8 +71,9 @@ __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, in
                                                       int chunk, int n_wg, int n_slots,
                                                       int32_t* __restrict__ lens_inc, int cap,
                                                       int Dr) {
-  constexpr int NS = 8;
-  constexpr int EPL = D / 32;
+  constexpr int LS = 256 / NS;  // lanes per stream
+  constexpr int EPL = D / LS;
+  static_assert(EPL * LS == D, "the padded head dim splits evenly over a stream's lanes");
   const int RS = MASK ? Dr : D;  // head dim (D is its padded size when MASK)
   const int hq = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   // fused append: the sequence's length moves past its new token once pass 1
@@ -80,15 +82,15 @@ __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, in
     const int p = lens_inc[b];
     if (p >= 0 && p < cap) lens_inc[b] = p + 1;
   }
-  const int st = tid >> 5, li = tid & 31;
+  const int st = tid / LS, li = tid % LS;
   const size_t obase = ((size_t)b * Hq + hq) * RS;
   const long long c0 = cum[b], c1 = cum[b + 1];
   if (c1 <= c0) {
-    if (tid < RS) store_elem(out, obase + tid, out_dt, 0.f);
+    for (int d = tid; d < RS; d += 256) store_elem(out, obase + d, out_dt, 0.f);
     return;
   }
   if (c1 > (long long)n_wg * chunk) {  // plan too small for these lengths: flag, never read past it
-    if (tid < RS) store_elem(out, obase + tid, out_dt, __builtin_nanf(""));
+    for (int d = tid; d < RS; d += 256) store_elem(out, obase + d, out_dt, __builtin_nanf(""));
     return;
   }
   const long long wf = c0 / chunk;
@@ -108,7 +110,10 @@ __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, in
   // sequences (C1: at most two per stream) take 2, which measured 1.2 us per
   // step faster there than loading 8 clamped copies (np is uniform in the
   // workgroup, so the branch is too).
-  if (np > 2 * NS) merge_pieces<8, NS, D, EPL, MASK>(ws_o, ws_ml, base, np, st, li, M, L, O, RS);
+  // (Past a head dim of 256, EPL is 4 to 16 floats: U = 2 keeps the loads of
+  // a round trip within a lane's registers.)
+  constexpr int UL = EPL > 8 ? 2 : 8;
+  if (np > 2 * NS) merge_pieces<UL, NS, D, EPL, MASK>(ws_o, ws_ml, base, np, st, li, M, L, O, RS);
   else merge_pieces<2, NS, D, EPL, MASK>(ws_o, ws_ml, base, np, st, li, M, L, O, RS);
   __shared__ float sm_ml[NS][2];
   __shared__ float sm_o[NS][D];
@@ -119,18 +124,18 @@ __global__ __launch_bounds__(256) void k_decode_merge(void* __restrict__ out, in
 #pragma unroll
   for (int e = 0; e < EPL; ++e) sm_o[st][li * EPL + e] = O[e];
   __syncthreads();
-  if (tid < RS) {
-    float MM = -INFINITY;
+  float MM = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) MM = fmaxf(MM, sm_ml[s][0]);
+  for (int s = 0; s < NS; ++s) MM = fmaxf(MM, sm_ml[s][0]);
+  for (int d = tid; d < RS; d += 256) {
     float LL = 0.f, OO = 0.f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const float w = fast_exp2(sm_ml[s][0] - MM);  // streams with no piece: w = 0
       LL = fmaf(w, sm_ml[s][1], LL);
-      OO = fmaf(w, sm_o[s][tid], OO);
+      OO = fmaf(w, sm_o[s][d], OO);
     }
-    store_elem(out, obase + tid, out_dt, OO / LL);
+    store_elem(out, obase + d, out_dt, OO / LL);
   }
 }
 
@@ -191,7 +196,7 @@ WsLayout ws_layout(int B, int Hq, int D, int n_chunks_max) {
   return w;
 }
 
-// Padded head dim of the masked kernels: a power of two in [32, 256].
+// Padded head dim of the masked kernels: a power of two in [32, 2048].
 int padded_dim(int D) {
   int p = 32;
   while (p < D) p <<= 1;
@@ -226,7 +231,9 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
   SKV_REQUIRE(B <= 65535, SKV_E_UNSUPPORTED, "%s: B=%d exceeds the grid limit", fn, B);
   SKV_REQUIRE(PAGED || T_cap > 0, SKV_E_INVALID, "%s: T_cap must be > 0", fn);
   SKV_REQUIRE(Hq % Hkv == 0, SKV_E_INVALID, "%s: H_q=%d not a multiple of H_kv=%d", fn, Hq, Hkv);
-  SKV_REQUIRE(D <= 256, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 256)", fn, D);
+  SKV_REQUIRE(Hq % Hkv != 0 || D <= dec::max_head_dim(Hq / Hkv), SKV_E_UNSUPPORTED,
+              "%s: head_dim %d with %d query heads per kv head (supported: 1 to %d)", fn, D,
+              Hq / Hkv, dec::max_head_dim(Hq / Hkv));
   SKV_REQUIRE(dt_ok(cache_dt) && dt_ok(q_dt) && dt_ok(out_dt), SKV_E_INVALID, "%s: bad dtype",
               fn);
   SKV_REQUIRE(chunk > 0 && chunk % 16 == 0, SKV_E_INVALID,
@@ -278,14 +285,21 @@ int decode_common(void* out, const void* q, const void* k, const void* v, const 
 #define SKV_MERGE(DD, MM)                                                                      \
   hipLaunchKernelGGL((k_decode_merge<DD, MM>), dim3(Hq, B), dim3(256), 0, s, out, out_dt, a.cum, \
                      a.ws_o, a.ws_ml, Hq, chunk, a.n_wg, a.n_slots, lens_inc, a.cap, D)
+#define SKV_MERGE_WIDE(DD)                                                                       \
+  hipLaunchKernelGGL((k_decode_merge<DD, true, 2>), dim3(Hq, B), dim3(256), 0, s, out, out_dt,    \
+                     a.cum, a.ws_o, a.ws_ml, Hq, chunk, a.n_wg, a.n_slots, lens_inc, a.cap, D)
   const int DP = padded_dim(D);
   if (D == 64) SKV_MERGE(64, false);
   else if (D == 128) SKV_MERGE(128, false);
   else if (DP == 32) SKV_MERGE(32, true);
   else if (DP == 64) SKV_MERGE(64, true);
   else if (DP == 128) SKV_MERGE(128, true);
-  else SKV_MERGE(256, true);
+  else if (DP == 256) SKV_MERGE(256, true);
+  else if (DP == 512) SKV_MERGE_WIDE(512);
+  else if (DP == 1024) SKV_MERGE_WIDE(1024);
+  else SKV_MERGE_WIDE(2048);
 #undef SKV_MERGE
+#undef SKV_MERGE_WIDE
   return check_launch(fn);
 }
 

@@ -6,10 +6,11 @@
 // models its auto-configuration trains use head dims of 24 to 80
 // (simple-llm/src/hyper.py:63-79). These kernels are the ones of
 // decode_kernels.h with the head dim padded to DP, a power of two in
-// [32, 256]: lane i of a 16-lane row owns elements [i*DP/16, (i+1)*DP/16),
-// and the lanes (or parts of a lane) past the real head dim D read an
-// in-row address, meet a zero query and store nothing. Loads are the widest
-// vector that divides D (up to 16 bytes), or single elements.
+// [32, 2048]: lane i of a row of 16 lanes (DP up to 256; 128 with G = 8)
+// or 64 lanes (a wavefront, past that) owns DP/16 or DP/64 consecutive
+// elements, and the lanes (or parts of a lane) past the real head dim D read
+// an in-row address, meet a zero query and store nothing. Loads are the
+// widest vector that divides D (up to 16 bytes), or single elements.
 #include "decode_kernels.h"
 
 int skv::dec::launch_partial_generic(const DecodeArgs& a, int G, bool bf16_cache,

@@ -92,6 +92,11 @@ int launch_partial_generic_paged(const DecodeArgs& a, int G, bool bf16_cache, hi
 bool gqa_mfma_eligible(const DecodeArgs& a, int G, bool bf16_cache, bool paged);
 int launch_partial_gqa(const DecodeArgs& a, int G, bool paged, hipStream_t s);
 
+// Largest head dim the masked kernels take with G query heads per kv head:
+// G * head_dim <= 4096 and head_dim <= 2048 (wavefront rows of up to 32
+// elements a lane).
+inline int max_head_dim(int G) { return G <= 2 ? 2048 : 4096 / G; }
+
 // Kv heads per workgroup: the largest divisor of H_kv that is <= 16.
 inline int heads_per_group(int Hkv) {
   for (int hw = kMaxRows; hw > 1; --hw)
@@ -254,20 +259,37 @@ __device__ void locate(const DecodeArgs& a, long long first, bool write_cum, int
   *off_out = __builtin_amdgcn_readfirstlane(s_off);
 }
 
+// Sum over the LANES lanes of a row: 16 (one DPP row) or 64 (a whole
+// wavefront: the DPP row sums, then across the four rows).
+template <int LANES>
+__device__ __forceinline__ float lanes_sum(float x) {
+  x = row16_sum(x);
+  if constexpr (LANES == 64) {
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+  }
+  return x;
+}
+
 // Tokens [start, end) of sequence b for the workgroup's kv heads -> one
 // partial per query head at `slot`. D is the padded head dim (the real one,
-// a.D, when !MASK); VG the elements per load of the masked form.
-template <typename TC, int D, int G, int TPG, bool PAGED, bool PF, int VG, bool MASK>
+// a.D, when !MASK); VG the elements per load of the masked form. LANES: the
+// lanes of a row, 16 (a DPP row) or 64 (a wavefront, for head dims whose
+// query and accumulators do not fit 16 lanes' registers).
+template <typename TC, int D, int G, int TPG, bool PAGED, bool PF, int VG, bool MASK,
+          int LANES = 16>
 __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b, int start,
                                              int end, int slot) {
   static_assert(!(PF && MASK), "the prefetching loop takes exact head dims");
-  constexpr int EPL = D / 16;
+  static_assert(LANES == 16 || LANES == 64, "a row is a DPP row or a wavefront");
+  constexpr int EPL = D / LANES;
+  constexpr int ROWS = 256 / LANES;  // rows of a full workgroup
   using FragT = typename FragSel<TC, EPL, VG, MASK>::type;
   constexpr int NG = EPL / VG;
   const int RS = MASK ? a.D : D;  // row stride of q, caches and partials
   const int tid = threadIdx.x;
-  const int rid = tid >> 4;  // DPP row
-  const int li = tid & 15;   // lane within the row
+  const int rid = tid / LANES;  // row
+  const int li = tid % LANES;   // lane within the row
   const int e0 = li * EPL;
   const int hl = rid % a.hw;  // kv head within the group
   const int sub = rid / a.hw; // token substream
@@ -380,7 +402,7 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
         float d = 0.f;                                                        \
         _Pragma("unroll") for (int e = 0; e < EPL; ++e) d =                   \
             fmaf(q[h][e], KF[u].get(e), d);                                   \
-        d = row16_sum(d);                                                     \
+        d = lanes_sum<LANES>(d);                                              \
         s[u] = ((T0) + u < mend) ? d : -INFINITY;                              \
       }                                                                       \
       float mx = m[h];                                                        \
@@ -478,7 +500,7 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
       float d = 0.f;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) d = fmaf(q[h][e], kx[e], d);
-      d = row16_sum(d);
+      d = lanes_sum<LANES>(d);
       const float mx = fmaxf(m[h], d);
       const float alpha = fast_exp2(m[h] - mx);  // 0 if the row saw no token yet
       const float p = fast_exp2(d - mx);
@@ -509,8 +531,8 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
 
   // S > 1: merge the S substreams of each head through LDS, one query head
   // at a time. Rows that saw no token drop out through exp2(-inf) = 0.
-  __shared__ float sm_ml[kMaxRows][2];
-  __shared__ float sm_o[kMaxRows][D + 1];
+  __shared__ float sm_ml[ROWS][2];
+  __shared__ float sm_o[ROWS][D + 1];
   const int nthreads = blockDim.x;
 #pragma unroll
   for (int h = 0; h < G; ++h) {
@@ -550,7 +572,8 @@ __device__ __forceinline__ void decode_piece(const DecodeArgs& a, int hg, int b,
 // range is cut at sequence boundaries into pieces; the piece of sequence b
 // in workgroup w gets partial slot w + b (unique: along the stream, each
 // boundary of either kind moves w or b on by at least one).
-template <typename TC, int D, int G, int TPG, bool PAGED, bool PF, int VG, bool MASK>
+template <typename TC, int D, int G, int TPG, bool PAGED, bool PF, int VG, bool MASK,
+          int LANES = 16>
 __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
   const int w = blockIdx.x, hg = blockIdx.y;
   int b, off;
@@ -559,7 +582,7 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
   int budget = a.chunk;
   while (true) {
     const int n = min(clamped_len(a, b) - off, budget);
-    decode_piece<TC, D, G, TPG, PAGED, PF, VG, MASK>(a, hg, b, off, off + n, w + b);
+    decode_piece<TC, D, G, TPG, PAGED, PF, VG, MASK, LANES>(a, hg, b, off, off + n, w + b);
     budget -= n;
     if (budget == 0) break;
     do {
@@ -570,11 +593,12 @@ __global__ __launch_bounds__(256) void k_decode_partial(DecodeArgs a) {
   }
 }
 
-template <typename TC, int D, int G, int TPG, bool PAGED, bool PF, int VG, bool MASK>
+template <typename TC, int D, int G, int TPG, bool PAGED, bool PF, int VG, bool MASK,
+          int LANES = 16>
 void launch_partial_t(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.n_wg, a.Hkv / a.hw);
-  hipLaunchKernelGGL((k_decode_partial<TC, D, G, TPG, PAGED, PF, VG, MASK>), grid,
-                     dim3(16 * a.hw * a.S), 0, s, a);
+  hipLaunchKernelGGL((k_decode_partial<TC, D, G, TPG, PAGED, PF, VG, MASK, LANES>), grid,
+                     dim3(LANES * a.hw * a.S), 0, s, a);
 }
 
 // ---------------------------------------------------------------------------
@@ -588,51 +612,83 @@ void launch_partial_t(const DecodeArgs& a, hipStream_t s) {
 // Tokens in flight per row and iteration, from a register budget: the
 // query and accumulator of G heads take 2*G*EPL registers, each K and V
 // fragment NW words.
-template <typename TC, int DP, int G, int VG>
+template <typename TC, int DP, int G, int VG, int LANES>
 constexpr int tokens_per_group() {
-  constexpr int EPL = DP / 16;
+  constexpr int EPL = DP / LANES;
   constexpr int NW = (sizeof(TC) == 2 && VG >= 2) ? EPL / 2 : EPL;
   constexpr int budget = 160 - 2 * G * EPL;
   constexpr int t = budget / (2 * NW);
   return t >= 8 ? 8 : t >= 4 ? 4 : t >= 2 ? 2 : 1;
 }
 
-template <typename TC, int DP, int G, int VG, bool PAGED>
+// Whether G query heads of a DP-wide head fit a lane's registers with rows
+// of LANES lanes: the queries and accumulators take 2*G*DP/LANES of them.
+template <int DP, int G, int LANES>
+constexpr bool fits() {
+  return 2 * G * (DP / LANES) <= 128;
+}
+
+template <typename TC, int DP, int G, int VG, bool PAGED, int LANES>
 int launch_g(const DecodeArgs& a, hipStream_t s) {
-  if constexpr (2 * G * (DP / 16) > 128) {
+  if constexpr (!fits<DP, G, LANES>()) {
     return set_error(SKV_E_UNSUPPORTED,
-                     "skv_decode_attn: no kernel for head_dim %d with %d query heads per kv head",
+                     "skv_decode_attn: no kernel for head_dim %d with %d query heads per kv head "
+                     "(G * head_dim up to 4096)",
                      a.D, G);
+  } else if constexpr (LANES == 16) {
+    launch_partial_t<TC, DP, G, tokens_per_group<TC, DP, G, VG, 16>(), PAGED, false, VG, true>(
+        a, s);
+    return 0;
   } else {
-    launch_partial_t<TC, DP, G, tokens_per_group<TC, DP, G, VG>(), PAGED, false, VG, true>(a, s);
+    // Rows are wavefronts: a workgroup of 4 serves up to 4 kv heads (the
+    // largest divisor of H_kv that is <= 4), the rest of its rows split the
+    // tokens of each head into substreams.
+    DecodeArgs w = a;
+    w.hw = 1;
+    for (int hw = 4; hw > 1; --hw)
+      if (a.Hkv % hw == 0) {
+        w.hw = hw;
+        break;
+      }
+    w.S = 4 / w.hw;
+    launch_partial_t<TC, DP, G, tokens_per_group<TC, DP, G, VG, 64>(), PAGED, false, VG, true,
+                     64>(w, s);
     return 0;
   }
 }
 
-template <typename TC, int DP, bool PAGED>
+template <typename TC, int DP, bool PAGED, int LANES>
 int launch_dp(const DecodeArgs& a, int G, hipStream_t s) {
-  constexpr int EPL = DP / 16;
+  constexpr int EPL = DP / LANES;
   constexpr int WIDE = sizeof(TC) == 4 ? (EPL < 4 ? EPL : 4) : (EPL < 8 ? EPL : 8);
   const bool wide = a.D % WIDE == 0;
 #define SKV_G(GG)                                                               \
   if (G == GG)                                                                  \
-    return wide ? launch_g<TC, DP, GG, WIDE, PAGED>(a, s)                       \
-                : launch_g<TC, DP, GG, 1, PAGED>(a, s);
+    return wide ? launch_g<TC, DP, GG, WIDE, PAGED, LANES>(a, s)                \
+                : launch_g<TC, DP, GG, 1, PAGED, LANES>(a, s);
   SKV_G(1) SKV_G(2) SKV_G(4) SKV_G(8)
 #undef SKV_G
   return set_error(SKV_E_UNSUPPORTED, "skv_decode_attn: no kernel for G=%d", G);
 }
 
-// The masked pass 1 for this head dim, cache dtype and layout.
+// The masked pass 1 for this head dim, cache dtype and layout: rows of 16
+// lanes up to a padded head dim of 256 (128 with G = 8), wavefront rows past
+// that, up to max_head_dim(G).
 template <typename TC, bool PAGED>
 int launch_generic(const DecodeArgs& a, int G, hipStream_t s) {
-  if (a.D < 1 || a.D > 256)
-    return set_error(SKV_E_UNSUPPORTED, "skv_decode_attn: head_dim %d (supported: 1 to 256)",
-                     a.D);
-  if (a.D <= 32) return launch_dp<TC, 32, PAGED>(a, G, s);
-  if (a.D <= 64) return launch_dp<TC, 64, PAGED>(a, G, s);
-  if (a.D <= 128) return launch_dp<TC, 128, PAGED>(a, G, s);
-  return launch_dp<TC, 256, PAGED>(a, G, s);
+  if (a.D < 1 || a.D > dec::max_head_dim(G))
+    return set_error(SKV_E_UNSUPPORTED,
+                     "skv_decode_attn: head_dim %d with %d query heads per kv head (supported: "
+                     "1 to %d)",
+                     a.D, G, dec::max_head_dim(G));
+  if (a.D <= 32) return launch_dp<TC, 32, PAGED, 16>(a, G, s);
+  if (a.D <= 64) return launch_dp<TC, 64, PAGED, 16>(a, G, s);
+  if (a.D <= 128) return launch_dp<TC, 128, PAGED, 16>(a, G, s);
+  if (a.D <= 256 && G < 8) return launch_dp<TC, 256, PAGED, 16>(a, G, s);
+  if (a.D <= 256) return launch_dp<TC, 256, PAGED, 64>(a, G, s);
+  if (a.D <= 512) return launch_dp<TC, 512, PAGED, 64>(a, G, s);
+  if (a.D <= 1024) return launch_dp<TC, 1024, PAGED, 64>(a, G, s);
+  return launch_dp<TC, 2048, PAGED, 64>(a, G, s);
 }
 
 }  // namespace

@@ -571,12 +571,15 @@ __global__ __launch_bounds__(kThreads) void k_flash_fwd(FfwdArgs a) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// Padded head dim (a multiple of 16, at most 128) and load mode of a head dim.
+// Padded head dim and load mode of a head dim: a multiple of 16 up to 128,
+// then 192 or 256 (the forward only: one wavefront per SIMD holds a 256-wide
+// query row set and its accumulators without spilling; the backward's
+// kernels hold two row operands and an accumulator and stop at 128).
 struct FlashShape {
   int DP, mode;
 };
 FlashShape flash_shape(int D) {
-  const int DP = (D + 15) / 16 * 16;
+  const int DP = D <= 128 ? (D + 15) / 16 * 16 : D <= 192 ? 192 : 256;
   return {DP, D == DP ? 0 : (D % 4 == 0 ? 1 : 2)};
 }
 
@@ -585,6 +588,8 @@ FlashShape flash_shape(int D) {
   X(16, 0) X(16, 1) X(16, 2) X(32, 0) X(32, 1) X(32, 2) X(48, 0) X(48, 1) X(48, 2)    \
   X(64, 0) X(64, 1) X(64, 2) X(80, 0) X(80, 1) X(80, 2) X(96, 0) X(96, 1) X(96, 2)    \
   X(112, 0) X(112, 1) X(112, 2) X(128, 0) X(128, 1) X(128, 2)
+// The forward's shapes past 128.
+#define SKV_FLASH_WIDE_SHAPES(X) X(192, 0) X(192, 1) X(192, 2) X(256, 0) X(256, 1) X(256, 2)
 
 }  // namespace
 }  // namespace skv
@@ -647,7 +652,7 @@ namespace skv {
 int attn_fwd_f32(float* out, float* L, float* M, const float* q, const float* k, const float* v,
                  const int32_t* start, const int32_t* n_new, int B, int C, int Hq, int Hkv, int D,
                  int T_cap, float scale, hipStream_t s, const char* fn) {
-  SKV_REQUIRE(D >= 1 && D <= 128, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 128)",
+  SKV_REQUIRE(D >= 1 && D <= 256, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 256)",
               fn, D);
   SKV_REQUIRE(aligned16(out) && aligned16(q) && aligned16(k) && aligned16(v), SKV_E_INVALID,
               "%s: q, k, v and out must be 16-byte aligned", fn);
@@ -664,6 +669,7 @@ int attn_fwd_f32(float* out, float* L, float* M, const float* q, const float* k,
 #define SKV_FF(DD, MM) \
   if (fs.DP == DD && fs.mode == MM) hipLaunchKernelGGL((k_flash_fwd<DD, MM>), grid, dim3(kThreads), 0, s, a);
   SKV_FLASH_SHAPES(SKV_FF)
+  SKV_FLASH_WIDE_SHAPES(SKV_FF)
 #undef SKV_FF
   return check_launch(fn);
 }

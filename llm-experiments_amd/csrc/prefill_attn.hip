@@ -27,11 +27,13 @@
 //    computed. Grouped-query attention folds the G query heads of a kv
 //    head into the rows (row = query * G + head), so K/V are read once per
 //    group.
-//  * Head dims other than 64 and 128 run the same kernel on the head dim
-//    padded to DP (32, 64 or 128): K/V tiles go through registers into the
-//    same LDS layout, zero-filled past the head dim, and the queries past it
-//    are zeros, so QK^T is unchanged and the padded rows of O^T are never
-//    stored.
+//  * Head dims other than 64, 128 and 256 run the same kernel on the head
+//    dim padded to DP (32, 64, 128 or 256): K/V tiles go through registers
+//    into the same LDS layout, zero-filled past the head dim, and the
+//    queries past it are zeros, so QK^T is unchanged and the padded rows of
+//    O^T are never stored. At 256 a workgroup has 4 wavefronts (one per
+//    SIMD: each holds twice the queries and accumulators) and 128 KB of
+//    double-buffered K/V tiles.
 //  * Long prefixes are split into n_splits token ranges (split-K, so that
 //    about one workgroup runs per CU); partials (m, l, o[D]) are merged by a
 //    second pass. The query tiles of one (sequence, kv head, split) are laid
@@ -48,9 +50,14 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 8;                   // wavefronts per workgroup up to D = 128
 constexpr int kQB = 1;                      // 32-row query blocks per wavefront
 constexpr int kBM = kWaves * kQB * 32;      // query rows per workgroup (256)
+
+// Wavefronts per workgroup at kernel head dim D: 8 (two per SIMD) up to 128;
+// at 256 a wavefront holds twice the queries and accumulators (~310
+// registers), so 4 (one per SIMD, 512 registers each) and 128 query rows.
+constexpr int waves_for(int D) { return D > 128 ? 4 : kWaves; }
 constexpr int kBN = 64;                     // tokens per K/V tile
 constexpr int kXCD = 8;                     // XCDs of an MI355X
 
@@ -92,7 +99,8 @@ struct alignas(16) Smem {
 
 template <int D>
 __device__ __forceinline__ int swz_key(int row) {
-  if constexpr (D == 128) return 4 * (row & 3) + ((row >> 2) & 3);
+  // D = 256 (32 chunks per row, two bank sweeps) takes the D = 128 key
+  if constexpr (D == 128 || D == 256) return 4 * (row & 3) + ((row >> 2) & 3);
   else if constexpr (D == 64) return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
   else return (row >> 2) & 3;  // D = 32: four chunks per row, four rows per bank sweep
 }
@@ -125,9 +133,11 @@ __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0
 // LV = 8 or 1: D is the padded head dim, a.D the real one; tiles move
 // through registers, 16-byte loads (a.D % 8 == 0) or element loads.
 template <int D, int G, int LV>
-__global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) {
+__global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillArgs a) {
   constexpr int KB = D / 16;  // k-blocks of the QK^T product
   constexpr int DB = D / 32;  // 32-row d blocks of O^T
+  constexpr int W = waves_for(D);
+  constexpr int BM = W * kQB * 32;  // query rows of the workgroup
   constexpr bool GEN = LV != 0;
   const int RS = GEN ? a.D : D;  // row stride of q, out and the cache rows
   __shared__ Smem<D> sm;
@@ -147,7 +157,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
   const int P = min(max(a.start[b], 0), a.T_cap);
   const int n = max(0, min(a.n_new ? min(a.n_new[b], a.C) : a.C, a.T_cap - P));
   const int R = n * G;                 // valid rows of this (b, hk)
-  const int row0 = qt * kBM;
+  const int row0 = qt * BM;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lc = lane & 31, g = lane >> 5;
 
@@ -157,7 +167,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
   const int s0 = split * span;
   // the last query of this tile bounds the tokens any of its rows attends;
   // a tile past the valid rows has nothing to do
-  const int last_row = min(row0 + kBM, R) - 1;
+  const int last_row = min(row0 + BM, R) - 1;
   const int s1 = row0 < R ? min(min(s0 + span, kv_end), P + last_row / G + 1) : s0;
   const int first_q = row0 / G;  // smallest query index of the tile
 
@@ -212,17 +222,17 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
   // the last one is fetched too and never read.
   constexpr int RPK = 1024 / (D * 2);          // token rows per 1 KB
   constexpr int KPT = kBN * D * 2 / 1024;      // 1 KB pieces per tile and tensor
-  static_assert(GEN || KPT % kWaves == 0, "tile pieces must split over the wavefronts");
+  static_assert(GEN || KPT % W == 0, "tile pieces must split over the wavefronts");
   // Register-staged tiles (GEN): 16-byte chunk c of a tile is token row
   // c / (D/8), logical chunk c % (D/8), at the same swizzled LDS position as
   // the DMA form; chunks past the head dim are zeros.
   constexpr int NCH = kBN * D / 8;                             // chunks per tile and tensor
-  constexpr int CPT = (NCH + kWaves * 64 - 1) / (kWaves * 64);  // chunks per thread
+  constexpr int CPT = (NCH + W * 64 - 1) / (W * 64);  // chunks per thread
   uint4 rk[GEN ? CPT : 1], rv[GEN ? CPT : 1];
   auto reg_tile_load = [&](int T0) {
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
-      const int c = min(tid + u * kWaves * 64, NCH - 1);  // threads past NCH repeat the last chunk
+      const int c = min(tid + u * W * 64, NCH - 1);  // threads past NCH repeat the last chunk
       const int row = c / (D / 8), lch = c % (D / 8);
       const size_t rofs = (size_t)min(T0 + row, kv_end - 1) * row_stride;
       if constexpr (LV == 8) {
@@ -251,7 +261,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
   auto reg_tile_store = [&](int ST) {
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
-      const int c = tid + u * kWaves * 64;
+      const int c = tid + u * W * 64;
       if (c >= NCH) continue;
       const int row = c / (D / 8), lch = c % (D / 8);
       *reinterpret_cast<uint4*>(&sm.k[ST][swz<D>(row, lch)]) = rk[u];
@@ -260,8 +270,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
   };
 #define SKV_DMA_TILE(T0, ST)                                                                 \
   if constexpr (!GEN) {                                                                      \
-    _Pragma("unroll") for (int c = 0; c < KPT / kWaves; ++c) {                               \
-      const int piece = wave * (KPT / kWaves) + c;                                           \
+    _Pragma("unroll") for (int c = 0; c < KPT / W; ++c) {                                    \
+      const int piece = wave * (KPT / W) + c;                                                \
       const int row = piece * RPK + lane / (D / 8);                                          \
       const int pch = lane % (D / 8);                                                        \
       const int lch = pch ^ swz_key<D>(row);                                                 \
@@ -293,8 +303,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
     const int t0 = s0 + it * kBN;
     // the next tile: DMA into the other stage, or (GEN) loads into registers
     // now and their LDS stores after this tile's products
-    if constexpr (GEN) reg_tile_load(t0 + kBN);
-    else SKV_DMA_TILE(t0 + kBN, st ^ 1);
+    // (At D = 256 the registers of a staged tile are not free during the
+    // products: its loads wait until after them, see the end of the tile.)
+    if constexpr (GEN && D <= 128) reg_tile_load(t0 + kBN);
+    else if constexpr (!GEN) SKV_DMA_TILE(t0 + kBN, st ^ 1);
 
     // S^T for the whole 64-token tile first (two independent accumulator
     // chains per query block), then one online-softmax update, then PV.
@@ -400,6 +412,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void k_prefill_mfma(PrefillArgs a) 
         }
     }
 
+    if constexpr (GEN && D > 128) reg_tile_load(t0 + kBN);
     if constexpr (GEN) reg_tile_store(st ^ 1);
     // the next tile's DMA has landed in LDS before anyone reads it
     wait_all_memory();
@@ -525,13 +538,18 @@ __global__ __launch_bounds__(256) void k_prefill_zero_tail(PrefillArgs a, int D)
   if (i >= n) store_elem(a.out, idx, a.out_dt, 0.f);
 }
 
-int n_query_tiles(int C, int G) { return (C * G + kBM - 1) / kBM; }
+// Query tiles of a (sequence, kv head) at kernel head dim DK (the plan,
+// which does not know the head dim, counts them at DK = 128).
+int n_query_tiles(int C, int G, int DK = 128) {
+  const int bm = waves_for(DK) * kQB * 32;
+  return (C * G + bm - 1) / bm;
+}
 
-// Head dim the bf16 kernel runs at: 64 and 128 as they are, others (up to
-// 128) padded to the next of 32, 64, 128.
+// Head dim the bf16 kernel runs at: 64, 128 and 256 as they are, others
+// padded to the next of 32, 64, 128, 256.
 int kernel_dim(int D) {
-  if (D == 64 || D == 128 || D > 128) return D;
-  return D <= 32 ? 32 : D <= 64 ? 64 : 128;
+  if (D == 64 || D == 128 || D >= 256) return D;
+  return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
 }
 
 bool dt_ok(int dt) { return dt == SKV_F32 || dt == SKV_BF16; }
@@ -586,7 +604,7 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
                         static_cast<const float*>(k_cache), static_cast<const float*>(v_cache),
                         start, n_new, B, C, H_q, H_kv, D, T_cap, scale, (hipStream_t)stream, fn);
   }
-  SKV_REQUIRE(D >= 1 && D <= 128, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 128)",
+  SKV_REQUIRE(D >= 1 && D <= 256, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 256)",
               fn, D);
   SKV_REQUIRE((((uintptr_t)out | (uintptr_t)q | (uintptr_t)ws | (uintptr_t)k_cache |
                 (uintptr_t)v_cache) & 15) == 0,
@@ -611,7 +629,7 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
   a.C = C; a.Hq = H_q; a.Hkv = H_kv; a.T_cap = T_cap;
   a.qscale = scale * LOG2E;
   a.q_dt = q_dt; a.out_dt = out_dt;
-  a.n_qt = n_query_tiles(C, G);
+  a.n_qt = n_query_tiles(C, G, DK);
   a.n_splits = n_splits;
   a.n_groups = B * H_kv * n_splits;
   a.B = B;
@@ -625,11 +643,12 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
   const int LV = DK == D ? 0 : (D % 8 == 0 ? 8 : 1);
 #define SKV_PF(DD, GG, LL)                                                                    \
   if (DK == DD && G == GG && LV == LL)                                                        \
-    hipLaunchKernelGGL((k_prefill_mfma<DD, GG, LL>), dim3((unsigned)blocks), dim3(kWaves * 64), \
-                       0, s, a);
+    hipLaunchKernelGGL((k_prefill_mfma<DD, GG, LL>), dim3((unsigned)blocks),                  \
+                       dim3(waves_for(DD) * 64), 0, s, a);
 #define SKV_PF4(DD, LL) SKV_PF(DD, 1, LL) SKV_PF(DD, 2, LL) SKV_PF(DD, 4, LL) SKV_PF(DD, 8, LL)
-  SKV_PF4(64, 0) SKV_PF4(128, 0)
+  SKV_PF4(64, 0) SKV_PF4(128, 0) SKV_PF4(256, 0)
   SKV_PF4(32, 8) SKV_PF4(32, 1) SKV_PF4(64, 8) SKV_PF4(64, 1) SKV_PF4(128, 8) SKV_PF4(128, 1)
+  SKV_PF4(256, 8) SKV_PF4(256, 1)
 #undef SKV_PF4
 #undef SKV_PF
   int rc = check_launch(fn);
@@ -639,10 +658,12 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
   if (n_splits > 1) {
     const dim3 mgrid((unsigned)(((size_t)C * H_q * (DK / 4) + 255) / 256), (unsigned)B);
     if (LV == 0 && D == 64) hipLaunchKernelGGL((k_prefill_merge<64, false>), mgrid, dim3(256), 0, s, a);
-    else if (LV == 0) hipLaunchKernelGGL((k_prefill_merge<128, false>), mgrid, dim3(256), 0, s, a);
+    else if (LV == 0 && D == 128) hipLaunchKernelGGL((k_prefill_merge<128, false>), mgrid, dim3(256), 0, s, a);
+    else if (LV == 0) hipLaunchKernelGGL((k_prefill_merge<256, false>), mgrid, dim3(256), 0, s, a);
     else if (DK == 32) hipLaunchKernelGGL((k_prefill_merge<32, true>), mgrid, dim3(256), 0, s, a);
     else if (DK == 64) hipLaunchKernelGGL((k_prefill_merge<64, true>), mgrid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_prefill_merge<128, true>), mgrid, dim3(256), 0, s, a);
+    else if (DK == 128) hipLaunchKernelGGL((k_prefill_merge<128, true>), mgrid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_prefill_merge<256, true>), mgrid, dim3(256), 0, s, a);
   } else if (n_new)
     hipLaunchKernelGGL(k_prefill_zero_tail, dim3(mblocks), dim3(256), 0, s, a, D);
   return check_launch(fn);

@@ -125,7 +125,10 @@ def test_entry_points_reject_bad_arguments():
                                  a["T"], a["scale"], a["chunk"], a["n"], fake,
                                  kw.get("ws", ws), 0, 0, 0, None)
 
-    assert dec(D=300) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 256
+    assert dec(D=2056) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 2048 at G <= 2
+    ws8 = L.skv_decode_workspace_bytes(2, 8, 520, 2)
+    assert dec(Hq=8, Hkv=1, D=520, ws=ws8) == _lib.SKV_E_UNSUPPORTED  # G = 8: up to 512
+    assert b"head_dim 520 with 8 query heads" in L.skv_last_error()
     assert dec(D=0) == _lib.SKV_E_INVALID
     assert dec(Hq=6, Hkv=4) == _lib.SKV_E_INVALID
     assert dec(chunk=100) == _lib.SKV_E_INVALID  # not a multiple of 16
@@ -190,8 +193,8 @@ def test_flash_fwd_rejects_bad_arguments():
     def call(D=64, ptr=fake, scale=0.125, n=100):
         return L.skv_flash_fwd(ptr, None, None, fake, fake, fake, 2, n, 3, D, scale, None)
 
-    assert call(D=129) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 128
-    assert call(D=256) == _lib.SKV_E_UNSUPPORTED
+    assert call(D=257) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 256
+    assert b"supported: 1 to 256" in L.skv_last_error()
     assert call(ptr=None) == _lib.SKV_E_INVALID
     assert call(ptr=fake + 4) == _lib.SKV_E_INVALID  # not 16-byte aligned
     assert call(scale=-1.0) == _lib.SKV_E_INVALID
@@ -206,7 +209,7 @@ def test_prefill_rejects_bad_arguments():
         return L.skv_prefill_attn(out, fake, fake, fake, fake, None, 2, 16, Hq, 4, D, 1024, 0.125,
                                   ns, ws, ws_bytes, 1, 1, 1, None)
 
-    assert call(D=136) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 128
+    assert call(D=264) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 256
     assert call(out=fake + 8) == _lib.SKV_E_INVALID  # bf16 path: 16-byte alignment
     assert b"16-byte aligned" in L.skv_last_error()
     assert call(ns=2, ws=fake + 4, ws_bytes=1 << 30) == _lib.SKV_E_INVALID

@@ -15,6 +15,11 @@ and the padded-size edges -- against the CPU oracle:
     rounded K/V, accumulation is fp32 on both sides);
   * the bf16 MFMA prefill: 2e-2 (q and P enter the MFMA as bf16);
   * the fp32 prefill and flash forward/backward: 1e-4.
+
+Past the reference's typical sizes: decode takes head dims up to 2048 (G <=
+2), 1024 (G = 4) and 512 (G = 8), the prefills and the flash forward up to
+256 (the reference's largest flash_attn_max_head_dim, gpu/gpu_device.py:
+468-471), the flash backward up to 128.
 """
 from __future__ import annotations
 
@@ -49,14 +54,17 @@ def _gpu():
 _DECODE_LAYOUTS = [
     (6, 6, torch.float32, False),
     (8, 2, torch.bfloat16, True),    # G = 4 over a paged cache
-    (8, 1, torch.bfloat16, False),   # G = 8 (head dims up to 128: register budget)
+    (8, 1, torch.bfloat16, False),   # G = 8 (past 128: wavefront rows)
     (3, 3, torch.float32, True),
 ]
+# head dims past 256: rows of 64 lanes (a wavefront) instead of 16
+WIDE_DIMS = [264, 320, 384, 512]
 
 
 @pytest.mark.parametrize("D,Hq,Hkv,dtype,paged", [
-    (D, *lay) for lay in _DECODE_LAYOUTS for D in HEAD_DIMS
-    if not (lay[0] // lay[1] == 8 and D > 128)])
+    (D, *lay) for lay in _DECODE_LAYOUTS for D in HEAD_DIMS + WIDE_DIMS] + [
+    (1024, 8, 2, torch.bfloat16, False), (1000, 4, 1, torch.float32, True),
+    (2048, 2, 1, torch.float32, False), (2040, 4, 4, torch.bfloat16, True)])
 def test_decode_any_head_dim(gpu_ctx, D, Hq, Hkv, dtype, paged):
     banner(f"decode D={D} Hq={Hq} Hkv={Hkv} {dtype} paged={paged}")
     gpu = _gpu()
@@ -74,36 +82,15 @@ def test_decode_any_head_dim(gpu_ctx, D, Hq, Hkv, dtype, paged):
         np.repeat(v[1, 0], Hq // Hkv, axis=0), got[1].shape))  # one token: its value row
 
 
-@pytest.mark.parametrize("D", [d for d in HEAD_DIMS if d > 128])
-def test_decode_g8_rejects_head_dims_past_128(gpu_ctx, D):
-    """G = 8 has kernels for head dims up to 128 only: larger ones raise
-    ValueError (SKV_E_UNSUPPORTED) instead of launching."""
+@pytest.mark.parametrize("D,G", [(520, 8), (1032, 4), (2056, 1), (2056, 2)])
+def test_decode_head_dims_past_the_kernels_are_rejected(gpu_ctx, D, G):
+    """Past G * head_dim = 4096 (head_dim 2048 at G <= 2) there is no kernel:
+    ValueError (SKV_E_UNSUPPORTED) before any launch."""
     gpu = _gpu()
-    rng = np.random.default_rng(D)
-    B, T = 2, 64
-    lens = np.array([T, 5])
-    cache, _, _, _ = _filled_cache(gpu, gpu_ctx, rng, B, T, 8, 1, D, torch.bfloat16, lens, False)
-    q = rng.standard_normal((B, 8, D)).astype(np.float32)
-    with pytest.raises(ValueError):
-        _decode(gpu, gpu_ctx, cache, q)
-
-
-def test_decode_g8_above_128_is_rejected(gpu_ctx):
-    gpu = _gpu()
-    rng = np.random.default_rng(0)
-    cache, k, v, _ = _filled_cache(gpu, gpu_ctx, rng, 2, 64, 8, 1, 160, torch.bfloat16,
-                                   np.array([5, 9]))
-    q = rng.standard_normal((2, 8, 160)).astype(np.float32)
-    with pytest.raises(ValueError, match="no kernel for head_dim 160"):
-        _decode(gpu, gpu_ctx, cache, q)
-
-
-def test_decode_head_dim_above_256_is_rejected(gpu_ctx):
-    gpu = _gpu()
-    cache = gpu.kv_cache_create(gpu_ctx, gpu.KVCacheConfig(1, 8, 1, 1, 264))
+    cache = gpu.kv_cache_create(gpu_ctx, gpu.KVCacheConfig(1, 8, 1, G, D, n_kv_heads=1))
     cache.current_len = 1
-    q = torch.zeros((1, 1, 264), device="cuda")
-    with pytest.raises(ValueError, match="supported: 1 to 256"):
+    q = torch.zeros((1, G, D), device="cuda")
+    with pytest.raises(ValueError, match=f"head_dim {D} with {G} query heads"):
         gpu.decode_attention(gpu_ctx, cache, 0, q, torch.empty_like(q))
 
 
@@ -114,6 +101,10 @@ def test_decode_head_dim_above_256_is_rejected(gpu_ctx):
     (80, 16, 16, torch.float32, torch.float32, True),
     (30, 2, 2, torch.bfloat16, torch.bfloat16, False),  # element loads
     (200, 4, 2, torch.bfloat16, torch.float32, False),
+    (192, 8, 1, torch.bfloat16, torch.float32, True),   # G = 8 past 128
+    (320, 4, 2, torch.float32, torch.float32, False),   # wavefront rows
+    (512, 8, 8, torch.bfloat16, torch.bfloat16, True),
+    (1024, 4, 1, torch.bfloat16, torch.float32, False),
 ])
 def test_fused_append_attend_any_head_dim(gpu_ctx, D, Hq, Hkv, cdt, idt, paged):
     """Three fused append + decode steps against skv_append then skv_decode_attn
@@ -236,11 +227,15 @@ def test_append_chunk_any_head_dim(gpu_ctx, D, H, cache_dt, in_dt):
 # prefill (bf16 MFMA kernel; fp32 caches take the fp32 kernel)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("D", [1, 8, 20, 24, 28, 36, 40, 48, 56, 80, 96, 100, 120])
+@pytest.mark.parametrize("D,G", [(D, 2) for D in (1, 8, 20, 24, 28, 36, 40, 48, 56, 80, 96,
+                                                  100, 120, 136, 160, 192, 200, 256)]
+                         + [(160, 1), (256, 1), (192, 8), (256, 4)])
 @pytest.mark.parametrize("n_splits", [1, 3])
-def test_prefill_bf16_any_head_dim(gpu_ctx, D, n_splits):
-    banner(f"prefill bf16 D={D} n_splits={n_splits}")
-    got, want, valid, *_ = run_prefill(gpu_ctx, 2, 900, 8, 4, D, [300, 0], 200,
+def test_prefill_bf16_any_head_dim(gpu_ctx, D, G, n_splits):
+    """Past 128 the kernel runs at 256 (4 wavefronts of 32 query rows a
+    workgroup): exact 256 by LDS DMA, others through registers."""
+    banner(f"prefill bf16 D={D} G={G} n_splits={n_splits}")
+    got, want, valid, *_ = run_prefill(gpu_ctx, 2, 900, 4 * G, 4, D, [300, 0], 200,
                                        n_new=[200, 77], seed=D, n_splits=n_splits)
     # norm-wise per query row over all heads (the reference's [B*T, E] output
     # row): at D = 1 a single head's output is one scalar, often near zero
@@ -251,7 +246,7 @@ def test_prefill_bf16_any_head_dim(gpu_ctx, D, n_splits):
     assert not got[~valid].any()
 
 
-@pytest.mark.parametrize("D", [4, 20, 24, 30, 36, 48, 80, 100, 127])
+@pytest.mark.parametrize("D", [4, 20, 24, 30, 36, 48, 80, 100, 127, 130, 160, 192, 200, 255, 256])
 def test_prefill_fp32_any_head_dim(gpu_ctx, D):
     banner(f"prefill fp32 D={D}")
     gpu = _gpu()
@@ -314,8 +309,36 @@ def test_flash_fwd_bwd_any_head_dim(gpu_ctx, D):
         assert err < FP32_TOL, (name, err)
 
 
-def test_flash_head_dim_above_128_is_rejected(gpu_ctx):
+@pytest.mark.parametrize("D", [130, 160, 192, 200, 255, 256])
+def test_flash_fwd_head_dims_to_256(gpu_ctx, D):
+    """The flash forward (and with it the fp32 prefill) past 128: padded to
+    192 or 256, O, L and M against the oracle."""
+    from test_flash_bwd_gpu import _rel
+    from test_flash_fwd_gpu import _rel_rows, flash_fwd
+    banner(f"flash fwd D={D}")
+    B, N, H = 2, 150, 3
+    rng = np.random.default_rng(D)
+    Q, K, V = (rng.standard_normal((B * N, H * D)).astype(np.float32) for _ in range(3))
+    O_w, L_w, M_w = ko.flash_attention(Q, K, V, B, N, H, D)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    o, Ls, Ms = flash_fwd(dev(Q), dev(K), dev(V), B, N, H, D)
+    err = _rel_rows(o.cpu().numpy().reshape(-1, H, D), O_w.reshape(-1, H, D))
+    print(f"rel_err={err:.3e}")
+    assert err < FP32_TOL
+    assert _rel(Ls.cpu().numpy(), L_w) < FP32_TOL
+    assert _rel(Ms.cpu().numpy(), M_w) < FP32_TOL
+
+
+def test_flash_head_dim_above_256_is_rejected(gpu_ctx):
     from test_flash_fwd_gpu import flash_fwd
-    q = torch.zeros((1 * 4, 2 * 136), device="cuda")
+    q = torch.zeros((1 * 4, 2 * 264), device="cuda")
+    with pytest.raises(ValueError, match="supported: 1 to 256"):
+        flash_fwd(q, q, q, 1, 4, 2, 264)
+
+
+def test_flash_bwd_head_dim_above_128_is_rejected(gpu_ctx):
+    from test_flash_bwd_gpu import flash_bwd
+    x = torch.zeros((1 * 4, 2 * 136), device="cuda")
+    s = torch.zeros(1 * 4 * 2, device="cuda")
     with pytest.raises(ValueError, match="supported: 1 to 128"):
-        flash_fwd(q, q, q, 1, 4, 2, 136)
+        flash_bwd(x, x, x, x, s, s, x, 1, 4, 2, 136)
