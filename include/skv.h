@@ -414,20 +414,32 @@ int skv_next_tokens(int32_t* ids, int32_t* seq, const int32_t* argmax_prev,
 
 /* skv_append_decode_attn for one query head per kv head (MHA), a
  * contiguous cache (16-byte aligned for fp32, 8-byte for bf16; otherwise
- * SKV_E_UNSUPPORTED) and head_dim 64 or 128, WITHOUT the fill advance: one
- * workgroup per (sequence, head) reads the head's whole filled row, folds in
- * the new token (stored at lens[b] when lens[b] in [0, T_cap)) and writes
- * the output; no split, no workspace, no merge pass. lens is left as it
- * was: the caller advances it before the next step (skv_next_embed with
- * advance set does, for every layer). A negative fill is an empty row
- * (output 0, nothing stored). The reference's attention_with_kv_cache
- * (gpu_kv_cache.py:194-289) with its kv_cache_update (:113-186), for the
- * decode step's one token per sequence; sums run in another order than the
- * split kernels', so the bits may differ within fp32 rounding. */
+ * SKV_E_UNSUPPORTED) and head_dim 64 or 128, WITHOUT the fill advance: each
+ * (sequence, head) gets n_split workgroups (1, 2 or 4) that read its filled
+ * row in n_split equal parts, fold in the new token (stored at lens[b] when
+ * lens[b] in [0, T_cap)) and write the output; no merge pass. With n_split >
+ * 1 the last workgroup of a (sequence, head) to finish merges the parts'
+ * partials, in part order (the bits do not depend on which one finishes
+ * last), from ws: skv_decode_direct_workspace_bytes(B, H, D, n_split) bytes,
+ * zero-filled before its first use; every call leaves its arrival counters
+ * at zero again, and calls that share ws must be stream ordered (ws may be
+ * NULL for n_split = 1). lens is left as it was: the caller advances it
+ * before the next step (skv_next_embed with advance set does, for every
+ * layer). A negative fill is an empty row (output 0, nothing stored). The
+ * reference's attention_with_kv_cache (gpu_kv_cache.py:194-289) with its
+ * kv_cache_update (:113-186), for the decode step's one token per sequence;
+ * sums run in another order than the split kernels', so the bits may differ
+ * within fp32 rounding. */
 int skv_append_decode_attn_direct(void* out, const void* q, void* k_cache, void* v_cache,
                                   const void* new_k, const void* new_v, const int32_t* lens,
                                   int B, int H, int D, int T_cap, float scale, int cache_dtype,
-                                  int in_dtype, int q_dtype, int out_dtype, skv_stream_t stream);
+                                  int in_dtype, int q_dtype, int out_dtype, int n_split, void* ws,
+                                  size_t ws_bytes, skv_stream_t stream);
+
+/* Workspace of skv_append_decode_attn_direct with n_split parts: B * H
+ * arrival counters, then B * H * n_split partials (o[D], m, l); 0 for
+ * n_split <= 1. */
+size_t skv_decode_direct_workspace_bytes(int B, int H, int D, int n_split);
 
 /* Bytes of skv_linear_packed's argmax candidates for M rows: [M][256]
  * float values, then [M][256] int32 columns (one per workgroup). */
@@ -506,9 +518,10 @@ size_t skv_flash_bwd_workspace_bytes(int B, int N, int H);
  * q, k, v, o, dout, dq, dk, dv: [B, N, H, D] fp32 (the reference's
  * [B*N, H*D] buffers), 16-byte aligned; L, M: [B, N, H] fp32, the forward's
  * softmax sums and row maxima of the scaled scores (the reference's L and M
- * buffers). The outputs must not overlap the inputs. D from 1 to 128 (past
- * it SKV_E_UNSUPPORTED: the kernels keep two 32-row operands and an
- * accumulator of the head dim in each wavefront's registers).
+ * buffers). The outputs must not overlap the inputs. D from 1 to 256. Past
+ * 128 the head dim is padded to 192 or 256 and the kernels, which keep two
+ * 32-row operands and an accumulator of the head dim per wavefront, spill
+ * part of them to scratch: correct, but far below the narrow shapes' rate.
  * Products run on v_mfma_f32_32x32x2_f32 (fp32); no atomics, so results are
  * bitwise reproducible.
  */

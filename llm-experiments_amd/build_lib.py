@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libskv.so")
 SOURCES = ["skv_api.hip", "append.hip", "decode_attn.hip", "decode_attn_generic.hip",
            "decode_attn_generic_paged.hip", "decode_gqa_mfma.hip",
            "decode_direct.hip", "prefill_attn.hip", "model_ops.hip", "gemm.hip",
-           "sample.hip", "flash_fp32.hip", "bpe_tokenizer.cpp"]
+           "sample.hip", "flash_fp32.hip", "flash_fp32.hip:wide_bwd", "bpe_tokenizer.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -39,7 +39,10 @@ def hipcc() -> str:
 # Extra flags per source. The flash backward keeps its MFMA accumulators in
 # ordinary VGPRs (gfx950 MFMAs take either register file); the default
 # heuristic put them in AGPRs and copied them back and forth every step.
-SOURCE_FLAGS = {"flash_fp32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+SOURCE_FLAGS = {"flash_fp32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+                # the flash backward past a head dim of 128: the same source as its own
+                # translation unit, accumulators free to live in AGPRs
+                "flash_fp32.hip:wide_bwd": ["-DSKV_FLASH_WIDE_BWD=1"]}
 
 _NOISE = "is not a recognized feature for this target"  # hipcc's host pass on -packed-fp32-ops
 
@@ -64,10 +67,11 @@ def build(verbose: bool = False) -> str:
     flags = [f for f in HIPCC_FLAGS if f != "-shared"]
     with tempfile.TemporaryDirectory(prefix="skv_build_") as tmpdir:
         jobs = []
-        for src in SOURCES:
-            obj = os.path.join(tmpdir, src + ".o")
+        for src in SOURCES:  # "file" or "file:variant" (the same file, other flags)
+            obj = os.path.join(tmpdir, src.replace(":", "_") + ".o")
+            path = os.path.join(CSRC, src.split(":")[0])
             jobs.append((obj, [hipcc(), *flags, *SOURCE_FLAGS.get(src, []), "-I", CSRC, "-I",
-                               INCLUDE, "-c", os.path.join(CSRC, src), "-o", obj]))
+                               INCLUDE, "-c", path, "-o", obj]))
         with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 4, 8)) as pool:
             for f in [pool.submit(_run, cmd, verbose) for _, cmd in jobs]:
                 f.result()

@@ -1,25 +1,34 @@
-// Direct single-query decode attention with the step's append: one workgroup
-// per (sequence, head) reads that head's whole filled row and writes the
-// output itself, with no split over the token stream, no partials and no
-// merge pass. The fill is NOT advanced: the caller advances it (the model's
-// step does so at the start of the next step, in skv_next_embed), which is
-// what lets the workgroups of one sequence run without knowing of each
-// other. The same semantics as skv_append_decode_attn otherwise
-// (gpu_kv_cache.py:194-289, gpu_kernels.py:2801-2938): new_k/new_v[b] goes
-// to position lens[b] (if lens[b] in [0, cap)), then
+// Direct single-query decode attention with the step's append: the
+// workgroups of one (sequence, head) read that head's whole filled row and
+// write the output themselves, with no merge pass. The fill is NOT
+// advanced: the caller advances it (the model's step does so at the start of
+// the next step, in skv_next_embed), which is what lets the workgroups of one
+// sequence run without knowing of each other. The same semantics as
+// skv_append_decode_attn otherwise (gpu_kv_cache.py:194-289,
+// gpu_kernels.py:2801-2938): new_k/new_v[b] goes to position lens[b] (if
+// lens[b] in [0, cap)), then
 //   o = softmax(scale * q . K[t], t <= lens[b]) . V
 // over the filled rows and the new one; a negative fill is an empty row.
 //
-// Workgroup of 1024 threads = 64 rows of 16 lanes. Row r takes tokens
-// r, r + 64, r + 128, ... of the head's row; lane i of a row owns elements
-// [i*D/16, (i+1)*D/16) of each K and V row it reads (16 or 32 bytes for
-// fp32, 8 or 16 for bf16). A row issues the loads of TOK tokens before
-// using any (up to 64 * TOK tokens in flight per workgroup: one workgroup
-// per CU streams near a CU's return rate), sums the q.k partials over its
-// 16 lanes with DPP, and keeps an online softmax (m in log2 units, l, o).
-// The new token is folded in by row 0 from registers (rounded to the cache
-// precision, as the stored copy), and stored to the cache by the same row.
-// The 64 rows merge in LDS in row order: results are bitwise reproducible.
+// Split S (1, 2 or 4): a (sequence, head) gets S workgroups of 64 / S rows of
+// 16 lanes (1024 threads in all), workgroup s taking the s-th of S equal
+// parts of the row, so a batch of few (sequence, head) pairs spreads over S
+// times as many CUs (a long row is otherwise read at one CU's return rate).
+// Row r of a workgroup takes tokens r, r + R, r + 2R, ... of its part; lane
+// i of a row owns elements [i*D/16, (i+1)*D/16) of each K and V row it reads
+// (16 or 32 bytes for fp32, 8 or 16 for bf16). A row issues the loads of TOK
+// tokens before using any, sums the q.k partials over its 16 lanes with DPP,
+// and keeps an online softmax (m in log2 units, l, o). The new token is
+// folded in by row 0 of the last part's workgroup from registers (rounded to
+// the cache precision, as the stored copy), and stored to the cache by the
+// same row. The rows of a workgroup merge in LDS in row order. With S > 1
+// each workgroup then writes its (m, l, o) as device-scope atomic stores
+// (they write through to memory: no L2 write-back fence is needed), counts
+// its arrival on the (sequence, head)'s counter, and the last to arrive
+// reads all S partials back (device-scope atomic loads, served from memory),
+// merges them in part order, writes the output and puts the counter back to
+// zero. Results are bitwise reproducible and do not depend on which
+// workgroup arrives last.
 #include "skv_common.h"
 
 namespace skv {
@@ -36,10 +45,11 @@ struct DirectArgs {
   int B, H, T_cap;
   float qscale;  // softmax scale * log2(e)
   int q_dt, in_dt, out_dt;
+  float* part;     // S > 1: [B * H][S][D + 2] partials (o[D], m, l)
+  unsigned* cnt;   // S > 1: [B * H] arrival counters, zero between calls
 };
 
-constexpr int kDirRows = 64;
-constexpr int kDirThreads = kDirRows * 16;
+constexpr int kDirRows = 64;  // rows of 16 lanes per (sequence, head), over its S workgroups
 
 template <typename TC>
 __device__ __forceinline__ float cache_round(float x) {
@@ -67,13 +77,18 @@ __device__ __forceinline__ void load_row(const TC* p, float (&x)[EPL]) {
   }
 }
 
-template <typename TC, int D, int TOK>
-__global__ __launch_bounds__(kDirThreads) void k_decode_direct(DirectArgs a) {
+template <typename TC, int D, int TOK, int S>
+__global__ __launch_bounds__(kDirRows * 16 / S) void k_decode_direct(DirectArgs a) {
   constexpr int EPL = D / 16;
-  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, row = tid >> 4, ln = tid & 15;
+  constexpr int R = kDirRows / S;  // rows of this workgroup
+  const int b = blockIdx.x, h = blockIdx.y, part = blockIdx.z, tid = threadIdx.x,
+            row = tid >> 4, ln = tid & 15;
   const int p = a.lens[b];
-  const int L = min(max(p, 0), a.T_cap);                        // cached rows read
-  const bool app = a.new_k != nullptr && p >= 0 && p < a.T_cap;  // uniform
+  const int Lc = min(max(p, 0), a.T_cap);  // cached rows of the sequence
+  // this workgroup's part [t_lo, t_hi) of the cached rows
+  const int per = (Lc + S - 1) / S;
+  const int t_lo = min(part * per, Lc), t_hi = min(t_lo + per, Lc);
+  const bool app = a.new_k != nullptr && p >= 0 && p < a.T_cap && part == S - 1;  // uniform
   const size_t qo = ((size_t)b * a.H + h) * D + ln * EPL;
   float q[EPL];
 #pragma unroll
@@ -85,11 +100,11 @@ __global__ __launch_bounds__(kDirThreads) void k_decode_direct(DirectArgs a) {
   float m = -INFINITY, l = 0.f, o[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) o[e] = 0.f;
-  for (int t0 = row; t0 < L; t0 += kDirRows * TOK) {
+  for (int t0 = t_lo + row; t0 < t_hi; t0 += R * TOK) {
     float kx[TOK][EPL], vx[TOK][EPL];
 #pragma unroll
-    for (int j = 0; j < TOK; ++j) {  // every load first; rows past L reread row L - 1
-      const size_t off = base + (size_t)min(t0 + j * kDirRows, L - 1) * rs;
+    for (int j = 0; j < TOK; ++j) {  // every load first; rows past the part reread its last
+      const size_t off = base + (size_t)min(t0 + j * R, t_hi - 1) * rs;
       load_row<TC, EPL>(kc + off, kx[j]);
       load_row<TC, EPL>(vc + off, vx[j]);
     }
@@ -100,10 +115,10 @@ __global__ __launch_bounds__(kDirThreads) void k_decode_direct(DirectArgs a) {
 #pragma unroll
       for (int e = 0; e < EPL; ++e) d = fmaf(q[e], kx[j][e], d);
       d = row16_sum(d);
-      s[j] = t0 + j * kDirRows < L ? d : -INFINITY;
+      s[j] = t0 + j * R < t_hi ? d : -INFINITY;
       smax = fmaxf(smax, s[j]);
     }
-    const float mn = fmaxf(m, smax);  // finite: token t0 < L is valid
+    const float mn = fmaxf(m, smax);  // finite: token t0 < t_hi is valid
     const float al = fast_exp2(m - mn);
     l *= al;
 #pragma unroll
@@ -144,9 +159,9 @@ __global__ __launch_bounds__(kDirThreads) void k_decode_direct(DirectArgs a) {
     for (int e = 0; e < EPL; ++e) o[e] = fmaf(w, nv[e], o[e] * al);
     m = mn;
   }
-  // merge the 64 rows in row order
-  __shared__ float s_m[kDirRows], s_l[kDirRows];
-  __shared__ float s_o[kDirRows][D];
+  // merge the workgroup's rows in row order
+  __shared__ float s_m[R], s_l[R];
+  __shared__ float s_o[R][D];
   if (ln == 0) {
     s_m[row] = m;
     s_l[row] = l;
@@ -154,28 +169,75 @@ __global__ __launch_bounds__(kDirThreads) void k_decode_direct(DirectArgs a) {
 #pragma unroll
   for (int e = 0; e < EPL; ++e) s_o[row][ln * EPL + e] = o[e];
   __syncthreads();
+  float M = -INFINITY, LL = 0.f, OO = 0.f;
   if (tid < D) {
-    float M = -INFINITY;
-    for (int r = 0; r < kDirRows; ++r) M = fmaxf(M, s_m[r]);
-    float LL = 0.f, OO = 0.f;
+    for (int r = 0; r < R; ++r) M = fmaxf(M, s_m[r]);
     if (M != -INFINITY) {
-      for (int r = 0; r < kDirRows; ++r) {
+      for (int r = 0; r < R; ++r) {
         const float w = fast_exp2(s_m[r] - M);  // rows with no token: 0
         LL = fmaf(w, s_l[r], LL);
         OO = fmaf(w, s_o[r][tid], OO);
       }
     }
-    // an empty row (no cached token, no append) gives 0, as the split kernels
-    store_elem(a.out, ((size_t)b * a.H + h) * D + tid, a.out_dt, LL > 0.f ? OO / LL : 0.f);
   }
+  const size_t oi = ((size_t)b * a.H + h) * D + tid;
+  if constexpr (S > 1) {
+    // this part's (o, m, l) out to memory, then the last of the S to arrive merges
+    __shared__ unsigned s_last;
+    const size_t bh = (size_t)b * a.H + h;
+    float* pp = a.part + (bh * S + part) * (D + 2);
+    if (tid < D) {
+      __hip_atomic_store(pp + tid, OO, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0) {
+        __hip_atomic_store(pp + D, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + D + 1, LL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the write-through stores are acknowledged
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(a.cnt + bh, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(a.cnt + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid >= D) return;
+    const float* pb = a.part + bh * S * (D + 2);
+    float pm[S], pl[S], po[S];
+#pragma unroll
+    for (int z = 0; z < S; ++z) {  // every part's loads in flight together
+      po[z] = __hip_atomic_load(pb + z * (D + 2) + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pm[z] = __hip_atomic_load(pb + z * (D + 2) + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pl[z] = __hip_atomic_load(pb + z * (D + 2) + D + 1, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+    }
+    M = -INFINITY;
+#pragma unroll
+    for (int z = 0; z < S; ++z) M = fmaxf(M, pm[z]);
+    LL = 0.f;
+    OO = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int z = 0; z < S; ++z) {  // part order: the bits do not depend on the arrival order
+        const float w = fast_exp2(pm[z] - M);  // parts with no token: 0
+        LL = fmaf(w, pl[z], LL);
+        OO = fmaf(w, po[z], OO);
+      }
+    }
+  }
+  // an empty row (no cached token, no append) gives 0, as the split kernels
+  if (tid < D) store_elem(a.out, oi, a.out_dt, LL > 0.f ? OO / LL : 0.f);
 }
 
 template <typename TC, int D>
-void launch_direct(const DirectArgs& a, hipStream_t s) {
+void launch_direct(const DirectArgs& a, int S, hipStream_t s) {
   // tokens in flight per row: 8 at D = 64, 4 at D = 128 (64 registers of K
   // and V a lane; 16 wavefronts a CU leave 128)
   constexpr int TOK = D == 64 ? 8 : 4;
-  hipLaunchKernelGGL((k_decode_direct<TC, D, TOK>), dim3(a.B, a.H), dim3(kDirThreads), 0, s, a);
+  const dim3 grid(a.B, a.H, S);
+  if (S == 1) hipLaunchKernelGGL((k_decode_direct<TC, D, TOK, 1>), grid, dim3(kDirRows * 16), 0, s, a);
+  else if (S == 2) hipLaunchKernelGGL((k_decode_direct<TC, D, TOK, 2>), grid, dim3(kDirRows * 8), 0, s, a);
+  else hipLaunchKernelGGL((k_decode_direct<TC, D, TOK, 4>), grid, dim3(kDirRows * 4), 0, s, a);
 }
 
 }  // namespace
@@ -183,12 +245,20 @@ void launch_direct(const DirectArgs& a, hipStream_t s) {
 
 using namespace skv;
 
+extern "C" size_t skv_decode_direct_workspace_bytes(int B, int H, int D, int n_split) {
+  if (B <= 0 || H <= 0 || D <= 0 || n_split <= 1) return 0;
+  // arrival counters first (256-byte aligned block), then the partials
+  const size_t cnt = ((size_t)B * H * sizeof(unsigned) + 255) / 256 * 256;
+  return cnt + (size_t)B * H * n_split * (D + 2) * sizeof(float);
+}
+
 extern "C" int skv_append_decode_attn_direct(void* out, const void* q, void* k_cache,
                                              void* v_cache, const void* new_k,
                                              const void* new_v, const int32_t* lens, int B,
                                              int H, int D, int T_cap, float scale,
                                              int cache_dtype, int in_dtype, int q_dtype,
-                                             int out_dtype, skv_stream_t stream) {
+                                             int out_dtype, int n_split, void* ws,
+                                             size_t ws_bytes, skv_stream_t stream) {
   const char* fn = "skv_append_decode_attn_direct";
   SKV_REQUIRE(out && q && k_cache && v_cache && new_k && new_v && lens, SKV_E_INVALID,
               "%s: null pointer argument", fn);
@@ -200,20 +270,31 @@ extern "C" int skv_append_decode_attn_direct(void* out, const void* q, void* k_c
                   (q_dtype == SKV_F32 || q_dtype == SKV_BF16) &&
                   (out_dtype == SKV_F32 || out_dtype == SKV_BF16),
               SKV_E_INVALID, "%s: bad dtype", fn);
+  SKV_REQUIRE(n_split == 1 || n_split == 2 || n_split == 4, SKV_E_INVALID,
+              "%s: n_split=%d (supported: 1, 2, 4)", fn, n_split);
   // the cache rows are read as 16-byte (fp32) or 8-byte (bf16) vectors
   const uintptr_t al = cache_dtype == SKV_F32 ? 15 : 7;
   SKV_REQUIRE((((uintptr_t)k_cache | (uintptr_t)v_cache) & al) == 0, SKV_E_UNSUPPORTED,
               "%s: k_cache and v_cache must be %d-byte aligned for this cache dtype", fn,
               (int)al + 1);
+  const size_t need = skv_decode_direct_workspace_bytes(B, H, D, n_split);
+  SKV_REQUIRE(n_split == 1 || (ws && ws_bytes >= need && ((uintptr_t)ws & 3) == 0),
+              SKV_E_WORKSPACE, "%s: workspace %zu bytes < %zu required (4-byte aligned)", fn,
+              ws_bytes, need);
   DirectArgs a{out, q, k_cache, v_cache, new_k, new_v, lens, B, H, T_cap,
-               scale * 1.4426950408889634f, q_dtype, in_dtype, out_dtype};
+               scale * 1.4426950408889634f, q_dtype, in_dtype, out_dtype, nullptr, nullptr};
+  if (n_split > 1) {
+    a.cnt = static_cast<unsigned*>(ws);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(ws) +
+                                      ((size_t)B * H * sizeof(unsigned) + 255) / 256 * 256);
+  }
   hipStream_t s = (hipStream_t)stream;
   if (cache_dtype == SKV_F32) {
-    if (D == 64) launch_direct<float, 64>(a, s);
-    else launch_direct<float, 128>(a, s);
+    if (D == 64) launch_direct<float, 64>(a, n_split, s);
+    else launch_direct<float, 128>(a, n_split, s);
   } else {
-    if (D == 64) launch_direct<uint16_t, 64>(a, s);
-    else launch_direct<uint16_t, 128>(a, s);
+    if (D == 64) launch_direct<uint16_t, 64>(a, n_split, s);
+    else launch_direct<uint16_t, 128>(a, n_split, s);
   }
   return check_launch(fn);
 }

@@ -588,11 +588,66 @@ FlashShape flash_shape(int D) {
   X(16, 0) X(16, 1) X(16, 2) X(32, 0) X(32, 1) X(32, 2) X(48, 0) X(48, 1) X(48, 2)    \
   X(64, 0) X(64, 1) X(64, 2) X(80, 0) X(80, 1) X(80, 2) X(96, 0) X(96, 1) X(96, 2)    \
   X(112, 0) X(112, 1) X(112, 2) X(128, 0) X(128, 1) X(128, 2)
-// The forward's shapes past 128.
+// The shapes past 128 (the forward's here; the backward's in the wide
+// translation unit).
 #define SKV_FLASH_WIDE_SHAPES(X) X(192, 0) X(192, 1) X(192, 2) X(256, 0) X(256, 1) X(256, 2)
 
+FbwdArgs fbwd_args(float* dq, float* dk, float* dv, const float* q, const float* k,
+                   const float* v, const float* o, const float* L, const float* M,
+                   const float* dout, float* delta, int B, int N, int H, int D, float scale) {
+  FbwdArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.L = L; a.M = M;
+  a.dq = dq; a.dk = dk; a.dv = dv;
+  a.delta = delta;
+  a.N = N; a.H = H; a.D = D;
+  a.n_blocks = (N + kRows - 1) / kRows;
+  a.scale = scale;
+  a.sl2 = scale * LOG2E;
+  a.BH = B * H;
+  return a;
+}
+
+// The two backward kernels of shape fs (one of SHAPES) for a.
+#define SKV_FB(DD, MM)                                                             \
+  if (fs.DP == DD && fs.mode == MM) {                                              \
+    hipLaunchKernelGGL((k_fbwd_dq<DD, MM>), grid, dim3(kThreads), 0, s, a);        \
+    int rc = check_launch("skv_flash_bwd");                                        \
+    if (rc) return rc;                                                             \
+    hipLaunchKernelGGL((k_fbwd_dkv<DD, MM>), grid, dim3(kThreads), 0, s, a);       \
+    return check_launch("skv_flash_bwd");                                          \
+  }
+
 }  // namespace
+
+#if SKV_FLASH_WIDE_BWD
+// The backward past a head dim of 128 (padded to 192 or 256). This
+// translation unit is the same source built without -amdgpu-mfma-vgpr-form:
+// each wavefront holds two 32-row operands and an accumulator of the head
+// dim, more than the VGPRs alone (the MFMA accumulators then live in AGPRs;
+// the rest spills to scratch, so these shapes run correctly but far below
+// the narrow ones' rate).
+int fbwd_wide(float* dq, float* dk, float* dv, const float* q, const float* k, const float* v,
+              const float* o, const float* L, const float* M, const float* dout, float* delta,
+              int B, int N, int H, int D, float scale, int DP, int mode, hipStream_t s) {
+  const FbwdArgs a = fbwd_args(dq, dk, dv, q, k, v, o, L, M, dout, delta, B, N, H, D, scale);
+  const FlashShape fs{DP, mode};
+  const dim3 grid((unsigned)(a.n_blocks * a.BH));
+  SKV_FLASH_WIDE_SHAPES(SKV_FB)
+  return set_error(SKV_E_UNSUPPORTED, "skv_flash_bwd: no kernel for head_dim %d", D);
+}
+#else
+namespace {
+int fbwd_launch(const FbwdArgs& a, const FlashShape& fs, hipStream_t s) {
+  const dim3 grid((unsigned)(a.n_blocks * a.BH));
+  SKV_FLASH_SHAPES(SKV_FB)
+  return set_error(SKV_E_UNSUPPORTED, "skv_flash_bwd: no kernel for head_dim %d", a.D);
+}
+}  // namespace
+#endif
+#undef SKV_FB
 }  // namespace skv
+
+#if !SKV_FLASH_WIDE_BWD
 
 using namespace skv;
 
@@ -610,7 +665,7 @@ extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, co
               "%s: null pointer argument", fn);
   SKV_REQUIRE(B > 0 && N > 0 && H > 0 && D > 0, SKV_E_INVALID,
               "%s: dims must be > 0 (B=%d N=%d H=%d D=%d)", fn, B, N, H, D);
-  SKV_REQUIRE(D <= 128, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 128)", fn, D);
+  SKV_REQUIRE(D <= 256, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 256)", fn, D);
   SKV_REQUIRE(scale > 0.f, SKV_E_INVALID, "%s: scale must be > 0", fn);
   SKV_REQUIRE(aligned16(dq) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) &&
                   aligned16(dout),
@@ -619,29 +674,15 @@ extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, co
   const size_t need = skv_flash_bwd_workspace_bytes(B, N, H);
   SKV_REQUIRE(ws && ws_bytes >= need && aligned16(ws), SKV_E_WORKSPACE,
               "%s: workspace %zu bytes < %zu required (16-byte aligned)", fn, ws_bytes, need);
-  FbwdArgs a;
-  a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.L = L; a.M = M;
-  a.dq = dq; a.dk = dk; a.dv = dv;
-  a.delta = static_cast<float*>(ws);
-  a.N = N; a.H = H; a.D = D;
-  a.n_blocks = (N + kRows - 1) / kRows;
-  a.scale = scale;
-  a.sl2 = scale * LOG2E;
+  const FbwdArgs a = fbwd_args(dq, dk, dv, q, k, v, o, L, M, dout, static_cast<float*>(ws), B,
+                               N, H, D, scale);
   hipStream_t s = (hipStream_t)stream;
-  a.BH = B * H;
   SKV_REQUIRE((long)a.n_blocks * a.BH < (1L << 31), SKV_E_UNSUPPORTED, "%s: grid too large", fn);
-  const dim3 grid((unsigned)(a.n_blocks * a.BH));
   const FlashShape fs = flash_shape(D);
-#define SKV_FB(DD, MM)                                                             \
-  if (fs.DP == DD && fs.mode == MM) {                                              \
-    hipLaunchKernelGGL((k_fbwd_dq<DD, MM>), grid, dim3(kThreads), 0, s, a);        \
-    int rc = check_launch(fn);                                                     \
-    if (rc) return rc;                                                             \
-    hipLaunchKernelGGL((k_fbwd_dkv<DD, MM>), grid, dim3(kThreads), 0, s, a);       \
-  }
-  SKV_FLASH_SHAPES(SKV_FB)
-#undef SKV_FB
-  return check_launch(fn);
+  if (fs.DP > 128)  // kernels of the wide translation unit
+    return fbwd_wide(dq, dk, dv, q, k, v, o, L, M, dout, a.delta, B, N, H, D, scale, fs.DP,
+                     fs.mode, s);
+  return fbwd_launch(a, fs, s);
 }
 
 namespace skv {
@@ -688,3 +729,4 @@ extern "C" int skv_flash_fwd(float* out, float* L, float* M, const float* q, con
   return attn_fwd_f32(out, L, M, q, k, v, nullptr, nullptr, B, N, H, H, D, N, scale,
                       (hipStream_t)stream, fn);
 }
+#endif  // !SKV_FLASH_WIDE_BWD

@@ -200,6 +200,13 @@ int attn_fwd_f32(float* out, float* L, float* M, const float* q, const float* k,
                  const int32_t* start, const int32_t* n_new, int B, int C, int Hq, int Hkv, int D,
                  int T_cap, float scale, hipStream_t s, const char* fn);
 
+// The flash backward's kernels past a head dim of 128 (flash_fp32.hip built
+// as its own translation unit with SKV_FLASH_WIDE_BWD; arguments checked by
+// skv_flash_bwd). DP: the padded head dim (192 or 256), mode: its load mode.
+int fbwd_wide(float* dq, float* dk, float* dv, const float* q, const float* k, const float* v,
+              const float* o, const float* L, const float* M, const float* dout, float* delta,
+              int B, int N, int H, int D, float scale, int DP, int mode, hipStream_t s);
+
 // skv_linear over more than 64 rows: the tiled MFMA GEMM (gemm.hip). stats:
 // M * 2 floats of workspace, used when ln_gamma is set.
 int gemm_linear(float* y, const float* x, const float* w_t, const float* bias,

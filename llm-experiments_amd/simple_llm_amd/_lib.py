@@ -53,7 +53,8 @@ _SIGNATURES = {
     "skv_linear_packed": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P]),
     "skv_linear_packed_cand_bytes": (_Z, [_I]),
     "skv_append_decode_attn_direct": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I,
-                                           _I, _I, _I, _P]),
+                                           _I, _I, _I, _I, _P, _Z, _P]),
+    "skv_decode_direct_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "skv_linear_cand": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P, _Z, _P]),
     "skv_linear_cand_bytes": (_Z, [_I, _I, _I]),
     "skv_next_embed": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _I, _I, _I,

@@ -177,8 +177,8 @@ def test_flash_bwd_rejects_bad_arguments():
                                None)
 
     assert call() == _lib.SKV_E_WORKSPACE
-    assert call(D=136, ws_bytes=need) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 128
-    assert call(D=256, ws_bytes=need) == _lib.SKV_E_UNSUPPORTED
+    assert call(D=257, ws_bytes=need) == _lib.SKV_E_UNSUPPORTED  # head dims 1 to 256
+    assert b"supported: 1 to 256" in L.skv_last_error()
     assert call(ptr=None, ws_bytes=need) == _lib.SKV_E_INVALID
     assert call(ptr=fake + 4, ws_bytes=need) == _lib.SKV_E_INVALID  # not 16-byte aligned
     assert call(scale=0.0, ws_bytes=need) == _lib.SKV_E_INVALID
@@ -355,16 +355,28 @@ def test_step_entry_points_reject_bad_arguments():
     assert ne(adv=fake) == _lib.SKV_E_INVALID  # a deferred advance needs every layer's fills
     # the direct decode attention: MHA, head_dim 64 or 128
     assert L.skv_append_decode_attn_direct(fake, fake, fake, fake, fake, fake, fake, 2, 4, 48,
-                                           64, 0.1, 0, 0, 0, 0, None) == _lib.SKV_E_UNSUPPORTED
+                                           64, 0.1, 0, 0, 0, 0, 1, None, 0,
+                                           None) == _lib.SKV_E_UNSUPPORTED
     assert L.skv_append_decode_attn_direct(fake, fake, fake, fake, None, fake, fake, 2, 4, 64,
-                                           64, 0.1, 0, 0, 0, 0, None) == _lib.SKV_E_INVALID
+                                           64, 0.1, 0, 0, 0, 0, 1, None, 0,
+                                           None) == _lib.SKV_E_INVALID
+    # split over the row: 1, 2 or 4 parts, the partials in a workspace
+    need = L.skv_decode_direct_workspace_bytes(2, 4, 64, 2)
+    assert need == 256 + 2 * 4 * 2 * 66 * 4
+    assert L.skv_decode_direct_workspace_bytes(2, 4, 64, 1) == 0
+    for ns, ws, wsb, rc_want in ((3, fake, need, _lib.SKV_E_INVALID),
+                                 (2, None, need, _lib.SKV_E_WORKSPACE),
+                                 (2, fake, need - 4, _lib.SKV_E_WORKSPACE)):
+        rc = L.skv_append_decode_attn_direct(fake, fake, fake, fake, fake, fake, fake, 2, 4, 64,
+                                             64, 0.1, 0, 0, 0, 0, ns, ws, wsb, None)
+        assert rc == rc_want, ns
     # the cache rows are read as vectors: 16-byte (fp32) or 8-byte (bf16)
     # aligned caches only (rejected before any launch)
     for cdt, off in ((0, 8), (0, 4), (1, 4), (1, 2)):
         rc = L.skv_append_decode_attn_direct(fake, fake, fake + off, fake, fake, fake, fake, 2, 4,
-                                             64, 64, 0.1, cdt, 0, 0, 0, None)
+                                             64, 64, 0.1, cdt, 0, 0, 0, 1, None, 0, None)
         assert rc == _lib.SKV_E_UNSUPPORTED, (cdt, off)
         assert b"aligned" in L.skv_last_error()
         rc = L.skv_append_decode_attn_direct(fake, fake, fake, fake + off, fake, fake, fake, 2, 4,
-                                             128, 64, 0.1, cdt, 0, 0, 0, None)
+                                             128, 64, 0.1, cdt, 0, 0, 0, 1, None, 0, None)
         assert rc == _lib.SKV_E_UNSUPPORTED, (cdt, off)

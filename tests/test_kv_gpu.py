@@ -631,15 +631,19 @@ def test_c2_full_run_every_step_matches_c_oracle(gpu_ctx, variant):
 # ---------------------------------------------------------------------------
 
 
+@pytest.mark.parametrize("n_split", [1, 2, 4])
 @pytest.mark.parametrize("B,H,D,T,dt", [(1, 4, 64, 256, "f32"), (1, 4, 64, 256, "bf16"),
-                                         (16, 12, 64, 1024, "f32"), (16, 12, 64, 1024, "bf16")])
-def test_direct_attention_matches_oracle(gpu_ctx, B, H, D, T, dt):
+                                         (16, 12, 64, 1024, "f32"), (16, 12, 64, 1024, "bf16"),
+                                         (3, 5, 128, 700, "bf16")])
+def test_direct_attention_matches_oracle(gpu_ctx, B, H, D, T, dt, n_split):
     """skv_append_decode_attn_direct, the attention of the C1 (B=1, 4 x 64,
     context 256) and C3 (B=16, 12 x 64, context 1024) greedy steps, against
     the float64 oracle over a host mirror of the cache: empty, ragged, last
     free position, full (no append) and retired (negative fill: zero output)
-    rows; the appended rows bit-exact and the fills left in place."""
-    banner(f"direct attention vs oracle B={B} H={H} D={D} T={T} {dt}")
+    rows; the appended rows bit-exact and the fills left in place. With the
+    row split over 2 or 4 workgroups (the last to finish merges), every call
+    leaves the arrival counters at zero, so calls in a row stay right."""
+    banner(f"direct attention vs oracle B={B} H={H} D={D} T={T} {dt} n_split={n_split}")
     from simple_llm_amd import _lib
     L = _lib.lib()
     s = _lib.stream_handle()
@@ -650,10 +654,16 @@ def test_direct_attention_matches_oracle(gpu_ctx, B, H, D, T, dt):
     vc = torch.from_numpy(r.standard_normal((B, T, H, D)).astype(np.float32)).cuda().to(tdt)
     kw = kc.float().cpu().numpy()
     vw = vc.float().cpu().numpy()
-    # B = 1: one call per kind of row; B = 16: every kind in one call
+    # B = 1: one call per kind of row; B >= 5: every kind in one call, twice
     special = [0, int(r.integers(1, T - 1)), T - 1, T, -1]
-    calls = ([np.array([f]) for f in special] if B == 1 else
-             [np.concatenate([special, r.integers(0, T, B - len(special))])])
+    if B == 1:
+        calls = [np.array([f]) for f in special]
+    elif B < len(special):
+        calls = [np.array(special[:B]), np.array(special[-B:])]
+    else:
+        calls = [np.concatenate([special, r.integers(0, T, B - len(special))])] * 2
+    wsb = L.skv_decode_direct_workspace_bytes(B, H, D, n_split)
+    ws = torch.zeros(max(wsb, 4), dtype=torch.uint8, device="cuda")
     for fills in calls:
         q, kn, vn = (r.standard_normal((B, H, D)).astype(np.float32) for _ in range(3))
         lens = to_dev(fills.astype(np.int32), torch.int32)
@@ -662,7 +672,7 @@ def test_direct_attention_matches_oracle(gpu_ctx, B, H, D, T, dt):
         _lib.check(L.skv_append_decode_attn_direct(
             out.data_ptr(), qd.data_ptr(), kc.data_ptr(), vc.data_ptr(), knd.data_ptr(),
             vnd.data_ptr(), lens.data_ptr(), B, H, D, T, D ** -0.5, cdt, _lib.F32, _lib.F32,
-            _lib.F32, s), "skv_append_decode_attn_direct")
+            _lib.F32, n_split, ws.data_ptr(), wsb, s), "skv_append_decode_attn_direct")
         torch.cuda.synchronize()
         att = np.zeros(B, np.int64)
         for b, f in enumerate(fills):
@@ -682,6 +692,8 @@ def test_direct_attention_matches_oracle(gpu_ctx, B, H, D, T, dt):
         print(f"fills={fills.tolist()[:6]} rel_err={err:.3e}")
         assert err < FP32_TOL  # the same (rounded) cache values on both sides
         assert not got[~live].any()  # retired rows give 0
+        if n_split > 1:  # every arrival counter is back at zero
+            assert not ws[:B * H * 4].any()
 
 
 def _c4_bench_cache(gpu, ctx):

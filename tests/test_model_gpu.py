@@ -749,10 +749,11 @@ def test_fused_step_tail_generates_the_same_tokens(gpu_ctx, vocab, d, heads):
     assert all(len(o) == 70 and o[:len(p)] == p for o, p in zip(a, prompts))
 
 
+@pytest.mark.parametrize("n_split", [1, 2, 4])
 @pytest.mark.parametrize("B,H,D,T,dt", [(1, 4, 64, 256, "f32"), (16, 12, 64, 1024, "f32"),
                                          (16, 12, 64, 1024, "bf16"), (3, 8, 128, 512, "bf16"),
                                          (5, 4, 128, 300, "f32")])
-def test_direct_attention_matches_split(gpu_ctx, B, H, D, T, dt):
+def test_direct_attention_matches_split(gpu_ctx, B, H, D, T, dt, n_split):
     """skv_append_decode_attn_direct against skv_append_decode_attn on the same
     inputs (ragged fills, an empty row, a full row, a retired row): outputs
     within 1e-5, the same bits stored for the new token, and the fills left
@@ -784,10 +785,13 @@ def test_direct_attention_matches_split(gpu_ctx, B, H, D, T, dt):
                                         lens2.data_ptr(), B, H, H, D, T, sc, chunk, n,
                                         ws.data_ptr(), ws.numel(), cdt, _lib.F32, _lib.F32,
                                         _lib.F32, s), "split")
+    wsb = L.skv_decode_direct_workspace_bytes(B, H, D, n_split)
+    dws = torch.zeros(max(wsb, 4), dtype=torch.uint8, device="cuda")
     _lib.check(L.skv_append_decode_attn_direct(got.data_ptr(), q.data_ptr(), kc.data_ptr(),
                                                vc.data_ptr(), nk.data_ptr(), nv.data_ptr(),
                                                lens.data_ptr(), B, H, D, T, sc, cdt, _lib.F32,
-                                               _lib.F32, _lib.F32, s), "direct")
+                                               _lib.F32, _lib.F32, n_split, dws.data_ptr(), wsb,
+                                               s), "direct")
     g, w = got.cpu().numpy(), want.cpu().numpy()
     np.testing.assert_allclose(g, w, rtol=1e-5, atol=1e-5 * np.abs(w).max())
     assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
@@ -796,14 +800,17 @@ def test_direct_attention_matches_split(gpu_ctx, B, H, D, T, dt):
         assert not g.reshape(B, -1)[2].any()  # a retired row gives 0
 
 
+@pytest.mark.parametrize("splits", [1, 2, 4])
 @pytest.mark.parametrize("fused", [True, False])
-def test_direct_attention_generates_the_same_tokens(gpu_ctx, fused):
+def test_direct_attention_generates_the_same_tokens(gpu_ctx, fused, splits):
     """Greedy generation with the direct attention (the fills advanced by the
-    next step's next-token kernel) gives the tokens of the split attention,
-    graph-replayed and eager, and the fills end where the split run's do."""
-    banner(f"direct attention generate, fused={fused}")
+    next step's next-token kernel; each row read by 1, 2 or 4 workgroups)
+    gives the tokens of the split attention, graph-replayed and eager, and
+    the fills end where the split run's do."""
+    banner(f"direct attention generate, fused={fused} splits={splits}")
     from simple_llm_amd import model as M
     m, params = make_model(gpu_ctx, 300, 256, 4, 2, 96, seed=13, std=0.1)
+    m.direct_splits = splits
     r = np.random.default_rng(31)
     prompts = [r.integers(0, 300, n).tolist() for n in (9, 30, 2)]
     tot = [96, 70, 50]
