@@ -140,7 +140,23 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
   constexpr int BM = W * kQB * 32;  // query rows of the workgroup
   constexpr bool GEN = LV != 0;
   const int RS = GEN ? a.D : D;  // row stride of q, out and the cache rows
-  __shared__ Smem<D> sm;
+  // LDS stages: register-staged tiles (GEN) share one struct; DMA-staged
+  // tiles get one variable per stage, so the compiler sees that a stage's
+  // reads cannot alias the DMA landing in the other one and does not make
+  // them wait for it.
+  __shared__ Smem<GEN ? D : 16> sm;
+  __shared__ __attribute__((aligned(16))) uint16_t lds0[GEN ? 8 : 2 * kBN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t lds1[GEN ? 8 : 2 * kBN * D];
+  auto sk = [&](auto stage) -> uint16_t* {
+    constexpr int s_ = decltype(stage)::value;
+    if constexpr (GEN) return sm.k[s_];
+    else return s_ == 0 ? lds0 : lds1;
+  };
+  auto sv = [&](auto stage) -> uint16_t* {
+    constexpr int s_ = decltype(stage)::value;
+    if constexpr (GEN) return sm.v[s_];
+    else return (s_ == 0 ? lds0 : lds1) + kBN * D;
+  };
 
   // ---- which (sequence, kv head, split, query tile) this workgroup is ----
   const int w = blockIdx.x;
@@ -276,8 +292,8 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
       const int pch = lane % (D / 8);                                                        \
       const int lch = pch ^ swz_key<D>(row);                                                 \
       const size_t gofs = (size_t)min((T0) + row, kv_end - 1) * row_stride + lch * 8;        \
-      dma16(kbase + gofs, &sm.k[(ST)][piece * 512]);                                         \
-      dma16(vbase + gofs, &sm.v[(ST)][piece * 512]);                                         \
+      dma16(kbase + gofs, sk(std::integral_constant<int, (ST)>{}) + piece * 512);            \
+      dma16(vbase + gofs, sv(std::integral_constant<int, (ST)>{}) + piece * 512);            \
     }                                                                                        \
   }
 
@@ -321,7 +337,7 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb) {
         const bf16x8 ka =
-            *reinterpret_cast<const bf16x8*>(&sm.k[st][swz<D>(tb * 32 + lc, kb * 2 + g)]);
+            *reinterpret_cast<const bf16x8*>(sk(stage) + swz<D>(tb * 32 + lc, kb * 2 + g));
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb)
           sc[tb][qb] =
@@ -398,8 +414,8 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
           for (int kk = 0; kk < 2; ++kk) {
             const int r0 = tb * 32 + kk * 16 + 4 * g + (L >> 2);
             const int r1 = r0 + 8;
-            const uint16_t* p0 = &sm.v[st][swz<D>(r0, d >> 3) + (d & 7)];
-            const uint16_t* p1 = &sm.v[st][swz<D>(r1, d >> 3) + (d & 7)];
+            const uint16_t* p0 = sv(stage) + swz<D>(r0, d >> 3) + (d & 7);
+            const uint16_t* p1 = sv(stage) + swz<D>(r1, d >> 3) + (d & 7);
             const i16x4 lo = lds_read_tr16(p0);
             const i16x4 hi = lds_read_tr16(p1);
             const bf16x8 va = __builtin_bit_cast(
