@@ -38,7 +38,13 @@
 //    about one workgroup runs per CU); partials (m, l, o[D]) are merged by a
 //    second pass. The query tiles of one (sequence, kv head, split) are laid
 //    out 8 blocks apart so they land on the same XCD together and the second
-//    tile's K/V reads hit that XCD's L2.
+//    tile's K/V reads hit that XCD's L2. (A merge by the last split of each
+//    tile to finish, with the partials written through to memory by
+//    device-scope stores, gave the same bits but took the C4 chunk from 568
+//    to 621 us on MI355X: 133 KB of write-through stores per workgroup cost
+//    more than the 12 us merge pass.)
+//  * Rows i >= n_new[b] of the output are written as zeros by the workgroup
+//    that owns them (one split) or by the merge pass.
 #include <type_traits>
 
 #include "skv_common.h"
@@ -128,6 +134,17 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const uint16_t* p) {
 // Waits until every memory operation this wavefront issued (including LDS
 // DMA writes) has completed.
 __device__ __forceinline__ void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Four consecutive outputs (16-byte aligned for fp32, 8-byte for bf16).
+__device__ __forceinline__ void store4(void* out, size_t i, int dt, const float (&o)[4]) {
+  if (dt == SKV_BF16) {
+    const uint32_t w0 = (uint32_t)f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
+    const uint32_t w1 = (uint32_t)f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + i) = make_uint2(w0, w1);
+  } else {
+    *reinterpret_cast<float4*>(static_cast<float*>(out) + i) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
 
 // LV = 0: D is the real head dim (64 or 128) and tiles move by LDS DMA.
 // LV = 8 or 1: D is the padded head dim, a.D the real one; tiles move
@@ -442,54 +459,65 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
 
   // ---- epilogue: this lane holds query column lc of each row block; the
   // accumulator slot r of d block db is d = db*32 + (r/4)*8 + 4g + r%4 ----
+  const int CG = a.C * G;  // output rows of this (b, hk): query i, head h -> i * G + h % G
+  float lt[kQB];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) lt[qb] = l[qb] + __shfl_xor(l[qb], 32);
+  // Row r's output from its normalised values v(db, r4, e), or zeros for a
+  // row past the sequence's new tokens; rows past the chunk are not stored.
+  auto store_row = [&](int r, auto&& v) {
+    if (r >= CG) return;
+    const int i = r / G, h = hk * G + r % G;
+    const size_t orow = ((size_t)b * a.C + i) * a.Hq + h;
+    const bool valid = r < R;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d0 = db * 32 + r4 * 8 + g * 4;
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = valid ? v(db, r4, e) : 0.f;
+        if constexpr (GEN) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (d0 + e < RS) store_elem(a.out, orow * RS + d0 + e, a.out_dt, x[e]);
+        } else {
+          store4(a.out, orow * D + d0, a.out_dt, x);
+        }
+      }
+  };
+  if (a.n_splits == 1) {
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+      const float inv = 1.f / lt[qb];
+      store_row(qrow[qb], [&](int db, int r4, int e) { return o[qb][db][r4 * 4 + e] * inv; });
+    }
+    return;
+  }
+  // n_splits > 1: this split's partial of every valid row, for the merge pass
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
-    const float lt = l[qb] + __shfl_xor(l[qb], 32);
     const int r = qrow[qb];
     if (r >= R) continue;
     const int i = r / G, h = hk * G + r % G;
-    const size_t orow = ((size_t)b * a.C + i) * a.Hq + h;
-    if (a.n_splits == 1) {
-      const float inv = 1.f / lt;
+    const size_t prow = (size_t)split * a.B * a.C * a.Hq + ((size_t)b * a.C + i) * a.Hq + h;
+    float* dst = a.ws_o + prow * D;
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int d = db * 32 + r4 * 8 + g * 4 + e;
-            if (!GEN || d < RS) store_elem(a.out, orow * RS + d, a.out_dt, o[qb][db][r4 * 4 + e] * inv);
-          }
-    } else {
-      const size_t prow = (size_t)split * a.B * a.C * a.Hq + orow;
-      float* dst = a.ws_o + prow * D;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          float4 x;
-          x.x = o[qb][db][r4 * 4 + 0];
-          x.y = o[qb][db][r4 * 4 + 1];
-          x.z = o[qb][db][r4 * 4 + 2];
-          x.w = o[qb][db][r4 * 4 + 3];
-          *reinterpret_cast<float4*>(dst + db * 32 + r4 * 8 + g * 4) = x;
-        }
-      if (g == 0) {
-        a.ws_ml[prow * 2 + 0] = m[qb];
-        a.ws_ml[prow * 2 + 1] = lt;
+      for (int r4 = 0; r4 < 4; ++r4) {
+        float4 x;
+        x.x = o[qb][db][r4 * 4 + 0];
+        x.y = o[qb][db][r4 * 4 + 1];
+        x.z = o[qb][db][r4 * 4 + 2];
+        x.w = o[qb][db][r4 * 4 + 3];
+        *reinterpret_cast<float4*>(dst + db * 32 + r4 * 8 + g * 4) = x;
       }
+    if (g == 0) {
+      a.ws_ml[prow * 2 + 0] = m[qb];
+      a.ws_ml[prow * 2 + 1] = lt[qb];
     }
-  }
-}
-
-// Four consecutive outputs (16-byte aligned for fp32, 8-byte for bf16).
-__device__ __forceinline__ void store4(void* out, size_t i, int dt, const float (&o)[4]) {
-  if (dt == SKV_BF16) {
-    const uint32_t w0 = (uint32_t)f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
-    const uint32_t w1 = (uint32_t)f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + i) = make_uint2(w0, w1);
-  } else {
-    *reinterpret_cast<float4*>(static_cast<float*>(out) + i) = make_float4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -539,19 +567,6 @@ __global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a) {
   } else {
     store4(a.out, row * D + d, a.out_dt, o);
   }
-}
-
-// Zero-fill of rows i >= n_new[b] when there is no merge pass.
-__global__ __launch_bounds__(256) void k_prefill_zero_tail(PrefillArgs a, int D) {
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const size_t rows = (size_t)a.B * a.C * a.Hq;
-  if (idx >= rows * D) return;
-  const size_t row = idx / D;
-  const int b = (int)(row / ((size_t)a.C * a.Hq));
-  const int i = (int)((row / a.Hq) % a.C);
-  const int P = min(max(a.start[b], 0), a.T_cap);
-  const int n = max(0, min(a.n_new ? min(a.n_new[b], a.C) : a.C, a.T_cap - P));
-  if (i >= n) store_elem(a.out, idx, a.out_dt, 0.f);
 }
 
 // Query tiles of a (sequence, kv head) at kernel head dim DK (the plan,
@@ -669,8 +684,6 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
 #undef SKV_PF
   int rc = check_launch(fn);
   if (rc) return rc;
-  const size_t elems = (size_t)B * C * H_q * D;
-  const unsigned mblocks = (unsigned)((elems + 255) / 256);
   if (n_splits > 1) {
     const dim3 mgrid((unsigned)(((size_t)C * H_q * (DK / 4) + 255) / 256), (unsigned)B);
     if (LV == 0 && D == 64) hipLaunchKernelGGL((k_prefill_merge<64, false>), mgrid, dim3(256), 0, s, a);
@@ -680,7 +693,6 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
     else if (DK == 64) hipLaunchKernelGGL((k_prefill_merge<64, true>), mgrid, dim3(256), 0, s, a);
     else if (DK == 128) hipLaunchKernelGGL((k_prefill_merge<128, true>), mgrid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((k_prefill_merge<256, true>), mgrid, dim3(256), 0, s, a);
-  } else if (n_new)
-    hipLaunchKernelGGL(k_prefill_zero_tail, dim3(mblocks), dim3(256), 0, s, a, D);
+  }
   return check_launch(fn);
 }

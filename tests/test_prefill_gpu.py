@@ -70,7 +70,8 @@ def run_prefill(ctx, B, T, Hq, Hkv, D, prefix, C, n_new=None, seed=0, n_splits=0
     q = rng.standard_normal((B, C, Hq, D)).astype(np.float32)
     if q_dtype == torch.bfloat16:
         q = ko.bf16_round(q)
-    out = torch.empty((B, C, Hq, D), dtype=out_dtype, device="cuda")
+    # NaN-filled: every element, the zeros of rows past n_new included, must be written
+    out = torch.full((B, C, Hq, D), float("nan"), dtype=out_dtype, device="cuda")
     fills = gpu.kv_cache_prefill(ctx, cache, 0, to_dev(kn), to_dev(vn), to_dev(q, q_dtype), out,
                                  n_new=n_new, n_splits=n_splits)
     nn = np.full(B, C) if n_new is None else np.asarray(n_new)
@@ -99,13 +100,31 @@ def test_prefill_matches_oracle(gpu_ctx, B, T, Hq, Hkv, D, prefix, C):
     assert err < BF16_TOL
 
 
-@pytest.mark.parametrize("n_splits", [1, 2, 7])
+@pytest.mark.parametrize("n_splits", [1, 2, 3, 4, 5, 7])
 def test_prefill_split_counts_agree(gpu_ctx, n_splits):
-    """Forced split counts (no merge pass, and merges of 2 and 7 partials)."""
+    """Forced split counts (no merge pass, and merges of 2 to 7 partials)."""
     banner(f"prefill n_splits={n_splits}")
     got, want, valid, *_ = run_prefill(gpu_ctx, 2, 4096, 8, 8, 128, [2900, 1500], 256,
                                        seed=5, n_splits=n_splits)
     assert rel_err(got, want, valid) < BF16_TOL
+
+
+def test_prefill_split_merge_repeats_bit_exact(gpu_ctx):
+    """Calls of other shapes and split counts between two runs of the same call
+    share its workspace and leave nothing behind: the repeat gives the same bits."""
+    banner("prefill split merge: repeat after other shapes")
+    first = {}
+    for rnd in range(2):
+        for ns in (2, 4, 3):
+            got, want, valid, *_ = run_prefill(gpu_ctx, 2, 3000, 8, 4, 128, [2500, 900], 200,
+                                               n_new=[200, 131], seed=11, n_splits=ns)
+            assert rel_err(got, want, valid) < BF16_TOL
+            if rnd == 0:
+                first[ns] = got
+            else:
+                np.testing.assert_array_equal(got, first[ns])
+            # another shape between the repeats, through the same workspace
+            run_prefill(gpu_ctx, 3, 1500, 16, 16, 64, [700, 0, 1200], 96, seed=ns, n_splits=ns)
 
 
 def test_prefill_ragged_chunk_zero_rows(gpu_ctx):
