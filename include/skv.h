@@ -436,9 +436,10 @@ int skv_append_decode_attn_direct(void* out, const void* q, void* k_cache, void*
                                   int in_dtype, int q_dtype, int out_dtype, int n_split, void* ws,
                                   size_t ws_bytes, skv_stream_t stream);
 
-/* Workspace of skv_append_decode_attn_direct with n_split parts: B * H
- * arrival counters, then B * H * n_split partials (o[D], m, l); 0 for
- * n_split <= 1. */
+/* Workspace of skv_append_decode_attn_direct with n_split parts: a fixed
+ * 256 KiB block of arrival counters (B * H <= 65536), then B * H * n_split
+ * partials (o[D], m, l); 0 for n_split <= 1. The fixed block lets calls of
+ * any shape share one zero-filled workspace. */
 size_t skv_decode_direct_workspace_bytes(int B, int H, int D, int n_split);
 
 /* Bytes of skv_linear_packed's argmax candidates for M rows: [M][256]

@@ -50,6 +50,12 @@ struct DirectArgs {
 };
 
 constexpr int kDirRows = 64;  // rows of 16 lanes per (sequence, head), over its S workgroups
+// The workspace starts with a fixed block of arrival counters, one per
+// (sequence, head), and the partials follow at a fixed offset: calls of any
+// shape can share one workspace without a call's partials landing on
+// another's counters.
+constexpr int kDirCounters = 65536;
+constexpr size_t kDirCounterBytes = kDirCounters * sizeof(unsigned);
 
 template <typename TC>
 __device__ __forceinline__ float cache_round(float x) {
@@ -247,9 +253,8 @@ using namespace skv;
 
 extern "C" size_t skv_decode_direct_workspace_bytes(int B, int H, int D, int n_split) {
   if (B <= 0 || H <= 0 || D <= 0 || n_split <= 1) return 0;
-  // arrival counters first (256-byte aligned block), then the partials
-  const size_t cnt = ((size_t)B * H * sizeof(unsigned) + 255) / 256 * 256;
-  return cnt + (size_t)B * H * n_split * (D + 2) * sizeof(float);
+  // the arrival counters' fixed block, then the partials
+  return kDirCounterBytes + (size_t)B * H * n_split * (D + 2) * sizeof(float);
 }
 
 extern "C" int skv_append_decode_attn_direct(void* out, const void* q, void* k_cache,
@@ -277,6 +282,9 @@ extern "C" int skv_append_decode_attn_direct(void* out, const void* q, void* k_c
   SKV_REQUIRE((((uintptr_t)k_cache | (uintptr_t)v_cache) & al) == 0, SKV_E_UNSUPPORTED,
               "%s: k_cache and v_cache must be %d-byte aligned for this cache dtype", fn,
               (int)al + 1);
+  SKV_REQUIRE(n_split == 1 || (long)B * H <= kDirCounters, SKV_E_UNSUPPORTED,
+              "%s: B * H = %ld above the %d (sequence, head) rows a split call takes", fn,
+              (long)B * H, kDirCounters);
   const size_t need = skv_decode_direct_workspace_bytes(B, H, D, n_split);
   SKV_REQUIRE(n_split == 1 || (ws && ws_bytes >= need && ((uintptr_t)ws & 3) == 0),
               SKV_E_WORKSPACE, "%s: workspace %zu bytes < %zu required (4-byte aligned)", fn,
@@ -285,8 +293,7 @@ extern "C" int skv_append_decode_attn_direct(void* out, const void* q, void* k_c
                scale * 1.4426950408889634f, q_dtype, in_dtype, out_dtype, nullptr, nullptr};
   if (n_split > 1) {
     a.cnt = static_cast<unsigned*>(ws);
-    a.part = reinterpret_cast<float*>(static_cast<char*>(ws) +
-                                      ((size_t)B * H * sizeof(unsigned) + 255) / 256 * 256);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kDirCounterBytes);
   }
   hipStream_t s = (hipStream_t)stream;
   if (cache_dtype == SKV_F32) {

@@ -92,16 +92,23 @@ def _as_dict(params, n_layers: int) -> dict:
 
 
 def _leaves(params):
-    """Identities of the arrays params holds (the cache key's fingerprint);
-    None when a field is missing (_as_dict then says which)."""
+    """The layer objects and arrays params holds (the cache entry's
+    fingerprint, compared by identity; the entry keeps them alive, so an
+    array replaced since cannot come back under a reused id); None when a
+    field is missing (_as_dict then says which)."""
     try:
-        ids = [id(_field(params, "embedding")), id(_field(params, "pos_encoding"))]
+        objs = [_field(params, "embedding"), _field(params, "pos_encoding")]
         for lp in _field(params, "layers"):
-            ids.append(id(lp))
-            ids.extend(id(_field(lp, f)) for f in LAYER_FIELDS)
+            objs.append(lp)
+            objs.extend(_field(lp, f) for f in LAYER_FIELDS)
     except (KeyError, AttributeError, TypeError):
         return None
-    return tuple(ids)
+    return tuple(objs)
+
+
+def _same(a, b) -> bool:
+    return a is not None and b is not None and len(a) == len(b) and \
+        all(x is y for x, y in zip(a, b))
 
 
 _MAX_MODELS = 4
@@ -129,7 +136,7 @@ def device_model(params, n_layers: int, n_heads: int, head_dim: int,
     key = (id(params), int(n_layers), int(n_heads), int(head_dim))
     hit = _models.get(key)
     fp = _leaves(params)
-    if hit is not None and hit[0] is params and hit[1] == fp:
+    if hit is not None and hit[0] is params and _same(hit[1], fp):
         _models.move_to_end(key)
         return hit[2]
     p = _as_dict(params, n_layers)

@@ -362,7 +362,7 @@ def test_step_entry_points_reject_bad_arguments():
                                            None) == _lib.SKV_E_INVALID
     # split over the row: 1, 2 or 4 parts, the partials in a workspace
     need = L.skv_decode_direct_workspace_bytes(2, 4, 64, 2)
-    assert need == 256 + 2 * 4 * 2 * 66 * 4
+    assert need == 65536 * 4 + 2 * 4 * 2 * 66 * 4  # the fixed counter block, then partials
     assert L.skv_decode_direct_workspace_bytes(2, 4, 64, 1) == 0
     for ns, ws, wsb, rc_want in ((3, fake, need, _lib.SKV_E_INVALID),
                                  (2, None, need, _lib.SKV_E_WORKSPACE),

@@ -68,3 +68,22 @@ def test_backend_seed_of_keys():
     assert a == _seed_of([0, 42]) and 0 <= a < (1 << 64)
     assert a != _seed_of(np.array([0, 43], np.uint32))
     assert a != _seed_of(np.array([1, 42], np.uint32))
+
+
+def test_backend_weight_cache_fingerprint_is_by_identity():
+    """The device weights of forward() are reused only while params holds the
+    very same layer objects and arrays: a replaced array (even an equal one)
+    is a different fingerprint; the entry keeps the old objects alive, so a
+    new array cannot come back under a reused id."""
+    from simple_llm_amd import backend
+    from oracle import model_oracle as mo
+
+    params = mo.init_params(50, 64, 2, 16, seed=0)
+    fp = backend._leaves(params)
+    assert backend._same(fp, backend._leaves(params))
+    params["layers"][1]["ff_b2"] = params["layers"][1]["ff_b2"].copy()  # equal values, new array
+    assert not backend._same(fp, backend._leaves(params))
+    params["layers"].pop()
+    assert not backend._same(fp, backend._leaves(params))
+    assert backend._leaves({"embedding": params["embedding"]}) is None
+    assert not backend._same(None, None)
