@@ -21,9 +21,12 @@
 //   k_fbwd_dkv  one workgroup per (128 keys, b, h). Per 32-query piece:
 //               S = Q K^T and dP = dO V^T, then dV += P^T dO, dK += dS^T Q.
 // Each of the 4 waves owns 32 rows. Its row operands (Q and dO, or K and V)
-// stay in registers for the whole call; the other side is staged through LDS
-// 64 rows at a time, the next rows' global loads issued before the current
-// ones are used. Work past the causal diagonal is skipped per wave.
+// stay in registers for the whole call (up to a head dim of 64, k_fbwd_dkv
+// keeps V in LDS instead); the other side is staged through LDS 64 rows at a
+// time, the next rows' global loads issued a step ahead, into registers, or,
+// where the kernel runs more wavefronts per SIMD (D <= 64: two for
+// k_fbwd_dkv, three for k_fbwd_dq and the forward), at the top of each step.
+// Work past the causal diagonal is skipped per wave.
 //
 // v_mfma_f32_32x32x2_f32 lane layout (lane l, c = l % 32, hf = l / 32):
 //   A (32 x 2): A[c][hf]   B (2 x 32): B[hf][c]
@@ -162,7 +165,7 @@ struct Stage {
 
 // dQ and the row deltas; rank 0 = the last query block (the most keys).
 template <int D, int MODE>
-__global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
+__global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_fbwd_dq(FbwdArgs a) {
   constexpr int G = D / 8;             // 16-byte pairs of a row fragment
   constexpr int DT = (D + 31) / 32;    // 32-row tiles of dQ^T
   constexpr int SP = Stage<D, MODE>::SP;
@@ -212,12 +215,14 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   const float* kh = a.k + row_off(b, 0, N, H, h, RS);
   const float* vh = a.v + row_off(b, 0, N, H, h, RS);
   Stage<D, MODE> st;
-  st.load(kh, vh, 0, N, rs, RS);
+  constexpr bool PF = D > 64;  // the next rows a step ahead, in registers
+  if (PF) st.load(kh, vh, 0, N, rs, RS);
   for (int j = 0; j < steps; ++j) {
+    if (!PF) st.load(kh, vh, j * kCols, N, rs, RS);
     __syncthreads();
     st.store(sK, sV);
     __syncthreads();
-    if (j + 1 < steps) st.load(kh, vh, (j + 1) * kCols, N, rs, RS);
+    if (PF && j + 1 < steps) st.load(kh, vh, (j + 1) * kCols, N, rs, RS);
 #pragma unroll
     for (int sub = 0; sub < kCols / 32; ++sub) {
       const int key0 = j * kCols + sub * 32;
@@ -279,15 +284,21 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq(FbwdArgs a) {
   }
 }
 
-// dK and dV; rank 0 = key block 0 (the most queries).
+// dK and dV; rank 0 = key block 0 (the most queries). Up to a head dim of
+// 64 the workgroup's V rows wait in LDS rather than registers, so that two
+// workgroups fit a CU (two wavefronts per SIMD).
+template <int D>
+constexpr bool fbwd_v_in_lds() { return D <= 64; }
 template <int D, int MODE>
-__global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
+__global__ __launch_bounds__(kThreads, fbwd_v_in_lds<D>() ? 2 : 1) void k_fbwd_dkv(FbwdArgs a) {
   constexpr int G = D / 8;
   constexpr int DT = (D + 31) / 32;
   constexpr int SP = Stage<D, MODE>::SP;
+  constexpr bool VL = fbwd_v_in_lds<D>();
   const int RS = MODE == 0 ? D : a.D;  // the real head dim
   __shared__ __attribute__((aligned(16))) float sQ[kCols * SP];
   __shared__ __attribute__((aligned(16))) float sD[kCols * SP];  // dO
+  __shared__ __attribute__((aligned(16))) float sV[VL ? kRows * SP : 4];  // the block's V rows
   __shared__ __attribute__((aligned(16))) float sM2[kCols];
   __shared__ __attribute__((aligned(16))) float sIL[kCols];
   __shared__ __attribute__((aligned(16))) float sDL[kCols];
@@ -302,12 +313,14 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
   const int krow = wk0 + c;  // a key past N is masked for every query (query < N <= krow)
   const size_t koff = row_off(b, min(krow, N - 1), N, H, h, RS);
 
-  f32x4 kf[G], vf[G];
+  f32x4 kf[G], vf[VL ? 1 : G];
+  float* vrow = sV + (VL ? (wave * 32 + c) * SP + 4 * hf : 0);  // V fragment g: vrow[8 g ..]
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int d0 = 8 * g + 4 * hf;
     kf[g] = load4m<MODE>(a.k + koff, d0, RS);
-    vf[g] = load4m<MODE>(a.v + koff, d0, RS);
+    if constexpr (VL) *reinterpret_cast<f32x4*>(vrow + 8 * g) = load4m<MODE>(a.v + koff, d0, RS);
+    else vf[g] = load4m<MODE>(a.v + koff, d0, RS);
   }
   f32x16 dva[DT], dka[DT];
 #pragma unroll
@@ -332,11 +345,18 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
   const size_t rs = (size_t)H * RS;
   const float* qh = a.q + row_off(b, 0, N, H, h, RS);
   const float* dh = a.dout + row_off(b, 0, N, H, h, RS);
-  if (j0 < steps) {
+  // With V in LDS (two workgroups a CU) the next rows are loaded at the top
+  // of each step, the other workgroup's products covering the wait; with one
+  // workgroup a CU they are loaded a step ahead, into registers.
+  if (!VL && j0 < steps) {
     st.load(qh, dh, j0 * kCols, N, rs, RS);
     SKV_FB_STATS(j0)
   }
   for (int j = j0; j < steps; ++j) {
+    if (VL) {
+      st.load(qh, dh, j * kCols, N, rs, RS);
+      SKV_FB_STATS(j)
+    }
     __syncthreads();
     st.store(sQ, sD);
     if (threadIdx.x < kCols) {
@@ -345,7 +365,7 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
       sDL[threadIdx.x] = dl;
     }
     __syncthreads();
-    if (j + 1 < steps) {
+    if (!VL && j + 1 < steps) {
       st.load(qh, dh, (j + 1) * kCols, N, rs, RS);
       SKV_FB_STATS(j + 1)
     }
@@ -361,14 +381,17 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dkv(FbwdArgs a) {
       for (int g = 0; g < G; ++g) {
         const f32x4 qa = *reinterpret_cast<const f32x4*>(qr + 8 * g);
         const f32x4 da = *reinterpret_cast<const f32x4*>(dr + 8 * g);
+        f32x4 vg;
+        if constexpr (VL) vg = *reinterpret_cast<const f32x4*>(vrow + 8 * g);
+        else vg = vf[g];
         s = mfma(qa.x, kf[g].x, s);
-        dp = mfma(da.x, vf[g].x, dp);
+        dp = mfma(da.x, vg.x, dp);
         s = mfma(qa.y, kf[g].y, s);
-        dp = mfma(da.y, vf[g].y, dp);
+        dp = mfma(da.y, vg.y, dp);
         s = mfma(qa.z, kf[g].z, s);
-        dp = mfma(da.z, vf[g].z, dp);
+        dp = mfma(da.z, vg.z, dp);
         s = mfma(qa.w, kf[g].w, s);
-        dp = mfma(da.w, vf[g].w, dp);
+        dp = mfma(da.w, vg.w, dp);
       }
       // s[r], dp[r]: query q0 + 8(r/4) + 4hf + r%4, key krow
       f32x16 p, ds;
@@ -448,7 +471,7 @@ struct FfwdArgs {
 // units), so O and l are rescaled on few pieces; the true maximum is kept
 // beside it for M and the final L.
 template <int D, int MODE>
-__global__ __launch_bounds__(kThreads) void k_flash_fwd(FfwdArgs a) {
+__global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_flash_fwd(FfwdArgs a) {
   constexpr int G8 = D / 8;
   constexpr int DT = (D + 31) / 32;
   constexpr int SP = Stage<D, MODE>::SP;
