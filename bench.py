@@ -1074,9 +1074,9 @@ def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py: this build runs on one GPU only (the decode path shards over "
-              "sequences/kv heads with no exchange; see the sharding note in DESIGN.md); "
-              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        print("bench.py: this build runs on one GPU only (the decode path would shard over "
+              "sequences, kv heads or token ranges, each GPU running the same kernels on its "
+              f"share); --gpus {args.gpus} is not supported", file=sys.stderr)
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
