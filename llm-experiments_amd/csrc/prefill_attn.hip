@@ -521,6 +521,8 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
   }
 }
 
+constexpr int kMergeBatch = 4;  // splits whose partials the merge loads in one round trip
+
 // Merge of the split partials, grid (tiles of C * Hq * D/4 threads, B): one
 // thread per 4 consecutive d of a row, 16-byte partial loads, 32-bit index
 // arithmetic. (One thread per element with 64-bit divisions took 31 us on
@@ -541,21 +543,41 @@ __global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a) {
   const int P = min(max(a.start[b], 0), a.T_cap);
   const int n = max(0, min(a.n_new ? min(a.n_new[b], a.C) : a.C, a.T_cap - P));
   float o[4] = {0.f, 0.f, 0.f, 0.f};
+  // One split's weighted partial into (L, o), in split order.
+  auto add = [&](float2 ml, float4 x, float M, float& L) {
+    if (ml.x == -INFINITY) return;
+    const float wgt = fast_exp2(ml.x - M);
+    L = fmaf(wgt, ml.y, L);
+    o[0] = fmaf(wgt, x.x, o[0]);
+    o[1] = fmaf(wgt, x.y, o[1]);
+    o[2] = fmaf(wgt, x.z, o[2]);
+    o[3] = fmaf(wgt, x.w, o[3]);
+  };
   if (i < n) {
-    float M = -INFINITY;
-    for (int s = 0; s < a.n_splits; ++s) M = fmaxf(M, a.ws_ml[(s * rows + row) * 2]);
-    float L = 0.f;
-    for (int s = 0; s < a.n_splits; ++s) {
-      const size_t pr = s * rows + row;
-      const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + pr * 2);
-      if (ml.x == -INFINITY) continue;
-      const float wgt = fast_exp2(ml.x - M);
-      const float4 x = *reinterpret_cast<const float4*>(a.ws_o + pr * D + d);
-      L = fmaf(wgt, ml.y, L);
-      o[0] = fmaf(wgt, x.x, o[0]);
-      o[1] = fmaf(wgt, x.y, o[1]);
-      o[2] = fmaf(wgt, x.z, o[2]);
-      o[3] = fmaf(wgt, x.w, o[3]);
+    float M = -INFINITY, L = 0.f;
+    if (a.n_splits <= kMergeBatch) {
+      // every split's (m, l) and o loaded together: one memory round trip
+      float2 ml[kMergeBatch];
+      float4 x[kMergeBatch];
+#pragma unroll
+      for (int s = 0; s < kMergeBatch; ++s) {
+        const size_t pr = (size_t)min(s, a.n_splits - 1) * rows + row;
+        ml[s] = *reinterpret_cast<const float2*>(a.ws_ml + pr * 2);
+        x[s] = *reinterpret_cast<const float4*>(a.ws_o + pr * D + d);
+      }
+#pragma unroll
+      for (int s = 0; s < kMergeBatch; ++s)
+        if (s < a.n_splits) M = fmaxf(M, ml[s].x);
+#pragma unroll
+      for (int s = 0; s < kMergeBatch; ++s)
+        if (s < a.n_splits) add(ml[s], x[s], M, L);
+    } else {
+      for (int s = 0; s < a.n_splits; ++s) M = fmaxf(M, a.ws_ml[(s * rows + row) * 2]);
+      for (int s = 0; s < a.n_splits; ++s) {
+        const size_t pr = s * rows + row;
+        add(*reinterpret_cast<const float2*>(a.ws_ml + pr * 2),
+            *reinterpret_cast<const float4*>(a.ws_o + pr * D + d), M, L);
+      }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = o[e] / L;
