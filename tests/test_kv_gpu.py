@@ -696,6 +696,44 @@ def test_direct_attention_matches_oracle(gpu_ctx, B, H, D, T, dt, n_split):
             assert not ws[:65536 * 4].any()
 
 
+def test_direct_attention_split_shapes_share_a_workspace(gpu_ctx):
+    """Split calls of different shapes (B x H, head dim, dtype) through one
+    zero-filled workspace, interleaved: the arrival counters sit in a fixed
+    block before every shape's partials, so no call's partials land on
+    another's counters; each output matches the float64 oracle and the
+    counters read zero after every call."""
+    banner("direct attention: shapes sharing one workspace")
+    from simple_llm_amd import _lib
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    shapes = [(16, 12, 64, 300, torch.float32), (2, 3, 128, 200, torch.bfloat16),
+              (40, 8, 64, 100, torch.float32)]
+    need = max(L.skv_decode_direct_workspace_bytes(B, H, D, 4) for B, H, D, _, _ in shapes)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    r = np.random.default_rng(5)
+    for rnd in range(2):
+        for B, H, D, T, tdt in shapes:
+            kc = torch.from_numpy(r.standard_normal((B, T, H, D)).astype(np.float32)).cuda().to(tdt)
+            vc = torch.from_numpy(r.standard_normal((B, T, H, D)).astype(np.float32)).cuda().to(tdt)
+            fills = r.integers(0, T, B).astype(np.int32)
+            q, kn, vn = (r.standard_normal((B, H, D)).astype(np.float32) for _ in range(3))
+            qd, knd, vnd = to_dev(q), to_dev(kn), to_dev(vn)
+            lens = to_dev(fills, torch.int32)
+            out = torch.full((B, H, D), float("nan"), device="cuda")
+            cdt = _lib.BF16 if tdt == torch.bfloat16 else _lib.F32
+            _lib.check(L.skv_append_decode_attn_direct(
+                out.data_ptr(), qd.data_ptr(), kc.data_ptr(), vc.data_ptr(), knd.data_ptr(),
+                vnd.data_ptr(), lens.data_ptr(), B, H, D, T, D ** -0.5, cdt, _lib.F32, _lib.F32,
+                _lib.F32, 4, ws.data_ptr(), need, s), "skv_append_decode_attn_direct")
+            torch.cuda.synchronize()
+            kw, vw = kc.float().cpu().numpy(), vc.float().cpu().numpy()  # the appended rows in place
+            want = ko.decode_attention(q, kw, vw, fills.astype(np.int64) + 1)
+            err = rel_err(out.cpu().numpy(), want)
+            print(f"round {rnd} B={B} H={H} D={D} {tdt}: rel_err={err:.3e}")
+            assert err < FP32_TOL
+            assert not ws[:65536 * 4].any()
+
+
 def _c4_bench_cache(gpu, ctx):
     """The C4 cache as bench.py builds it: [4, 32768, 16, 128] bf16, each
     sequence filled to 32000 with N(0, 1) from torch generator seed 0."""
