@@ -899,7 +899,9 @@ def run_fb(args, ctx):
                "frac": fwd_flops / fwd_s / 1e12 / MFMA_FP32_PEAK_TFLOPS, "flops": fwd_flops,
                "kernel": "skv_flash_fwd (k_flash_fwd), O, L, M in fp32"}
     dq, dk, dv = (torch.empty_like(q) for _ in range(3))
-    ws = torch.empty(L.skv_flash_bwd_workspace_bytes(B_, N, H_), dtype=torch.uint8, device=dev)
+    # the workspace of the five-product form (the row deltas and dS)
+    ws = torch.empty(L.skv_flash_bwd_fast_workspace_bytes(B_, N, H_, Dh), dtype=torch.uint8,
+                     device=dev)
 
     def call():
         rc = L.skv_flash_bwd(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), q.data_ptr(),
@@ -926,7 +928,7 @@ def run_fb(args, ctx):
     flops = 10.0 * Dh * (N * (N + 1) / 2) * B_ * H_
     roof = {"bound": "mfma", "achieved": flops / call_s / 1e12, "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": flops / call_s / 1e12 / MFMA_FP32_PEAK_TFLOPS,
-            "traffic": None, "kernel": "skv_flash_bwd (k_fbwd_dq + k_fbwd_dkv), HIP events",
+            "traffic": None, "kernel": "skv_flash_bwd, five-product form (k_fbwd_delta + k_fbwd_dkv + k_fbwd_dq_ds), HIP events",
             "mean_call_us": call_s * 1e6, "algorithmic_flops": flops}
     # same-run accuracy: the gradients of two (sequence, head) pairs against
     # float64 autograd on the CPU over the same q, k, v, dO (norm-wise per tensor)

@@ -508,6 +508,16 @@ int skv_flash_fwd(float* out, float* L, float* M, const float* q, const float* k
 /* Bytes of workspace skv_flash_bwd needs: the row deltas, B*N*H floats. */
 size_t skv_flash_bwd_workspace_bytes(int B, int N, int H);
 
+/* Bytes of workspace that let skv_flash_bwd run its five-product form: for
+ * D <= 64, the row deltas (a 256-byte aligned block) and then dS in 32 x 32
+ * tiles, B*H*ceil(N/32)^2*1024 floats; otherwise
+ * skv_flash_bwd_workspace_bytes. No reference
+ * counterpart: the reference's own grad_K_workspace, num_q_blocks full copies
+ * of dK (gpu_pass_backward.py:522-530), is usually this size or more (head_dim
+ * at least its block rows and N a multiple of 32); skv_flash_bwd takes the
+ * five-product form whenever ws_bytes is this size. */
+size_t skv_flash_bwd_fast_workspace_bytes(int B, int N, int H, int D);
+
 /*
  * Gradients of causal attention, replacing flash_attention_backward and its
  * reduce pass (simple-llm/src/gpu/gpu_pass_backward.py:445-580, kernels
@@ -524,7 +534,11 @@ size_t skv_flash_bwd_workspace_bytes(int B, int N, int H);
  * 32-row operands and an accumulator of the head dim per wavefront, spill
  * part of them to scratch: correct, but far below the narrow shapes' rate.
  * Products run on v_mfma_f32_32x32x2_f32 (fp32); no atomics, so results are
- * bitwise reproducible.
+ * bitwise reproducible. Two forms, by the workspace: with
+ * skv_flash_bwd_workspace_bytes, dQ recomputes S and dP (seven products);
+ * with skv_flash_bwd_fast_workspace_bytes (D <= 64), the dK/dV
+ * kernel writes dS and dQ is formed from it (five products, dS written and
+ * read once). Both give the same bits.
  */
 int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, const float* k, const float* v,
                   const float* o, const float* L, const float* M, const float* dout, int B, int N,

@@ -60,7 +60,8 @@ struct FbwdArgs {
   float* dq;
   float* dk;
   float* dv;
-  float* delta;  // [B, N, H] row deltas Dl, written by k_fbwd_dq
+  float* delta;  // [B, N, H] row deltas Dl, written by k_fbwd_dq (or k_fbwd_delta)
+  float* ds;     // dS in 32 x 32 tiles (see ds_tile), written by k_fbwd_dkv<.., true> for k_fbwd_dq_ds
   int N, H, BH, n_blocks;
   int D;  // head dim (the padded size is the kernel's template D)
   float scale, sl2;  // scale and scale * log2(e)
@@ -284,12 +285,26 @@ __global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_fbwd_dq(FbwdArgs 
   }
 }
 
+// dS of the five-product backward in 32 x 32 tiles: tile (query block qb, key
+// block kb) of (b, h) holds 32 rows of 32 floats, row = query qb*32 + i, and
+// within a row key kb*32 + 8 qq + 4 hf + t at position 16 hf + 4 qq + t: the
+// order in which lane (query i, half hf) of k_fbwd_dq_ds takes the keys as
+// k-steps, so that lane reads 64 contiguous bytes and a wavefront a whole
+// 4 KB tile.
+__device__ __forceinline__ float* ds_tile(const FbwdArgs& a, int bh, int qb, int kb) {
+  const int nt = (a.N + 31) >> 5;
+  return a.ds + (((size_t)bh * nt + qb) * nt + kb) * 1024;
+}
+__device__ __forceinline__ int ds_key_pos(int c) {  // key c of a block: 8 qq + 4 hf + t
+  return 16 * ((c >> 2) & 1) + 4 * (c >> 3) + (c & 3);
+}
+
 // dK and dV; rank 0 = key block 0 (the most queries). Up to a head dim of
 // 64 the workgroup's V rows wait in LDS rather than registers, so that two
 // workgroups fit a CU (two wavefronts per SIMD).
 template <int D>
 constexpr bool fbwd_v_in_lds() { return D <= 64; }
-template <int D, int MODE>
+template <int D, int MODE, bool DSO = false>  // DSO: also write dS (a.ds) for k_fbwd_dq_ds
 __global__ __launch_bounds__(kThreads, fbwd_v_in_lds<D>() ? 2 : 1) void k_fbwd_dkv(FbwdArgs a) {
   constexpr int G = D / 8;
   constexpr int DT = (D + 31) / 32;
@@ -328,6 +343,11 @@ __global__ __launch_bounds__(kThreads, fbwd_v_in_lds<D>() ? 2 : 1) void k_fbwd_d
     dva[dt] = f32x16{};
     dka[dt] = f32x16{};
   }
+  // DSO: this lane's place in the dS tiles of its key block (query block 0;
+  // the query block adds a whole row of tiles): key c, rows 4 hf + ...
+  float* dsw = nullptr;
+  if constexpr (DSO)
+    dsw = ds_tile(a, bh, 0, wk0 >> 5) + ds_key_pos(c) + 128 * hf;
 
   const int j0 = (blk * kRows) / kCols;  // first step holding a query >= the block's first key
   const int steps = (N + kCols - 1) / kCols;
@@ -408,6 +428,20 @@ __global__ __launch_bounds__(kThreads, fbwd_v_in_lds<D>() ? 2 : 1) void k_fbwd_d
           const float pr = (krow <= query && query < N) ? e : 0.f;
           p[r] = pr;
           ds[r] = pr * (dp[r] - d4[t]);
+        }
+      }
+      if constexpr (DSO) {
+        // dS of the piece (query block q0 / 32, key block wk0 / 32) for
+        // k_fbwd_dq_ds, in the order its lanes read: for each slot the 32
+        // lanes of a half write one query's 128-byte tile row
+        if (krow < N) {
+          float* tp = dsw + (size_t)(q0 >> 5) * ((N + 31) >> 5) * 1024;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int qi = 8 * (r / 4) + 4 * hf + (r % 4);  // query q0 + qi
+            if (q0 + qi < N)  // row qi of the tile; streamed past the caches (read once, later)
+              __builtin_nontemporal_store(ds[r], tp + (8 * (r / 4) + (r % 4)) * 32);
+          }
         }
       }
       // dV[key][d] += sum_query P^T[key][query] dO[query][d]; dK likewise with dS and Q
@@ -592,6 +626,144 @@ __global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_flash_fwd(FfwdArg
   }
 }
 
+// ---------------------------------------------------------------------------
+// The five-product backward (head dims up to 64, a workspace that holds dS):
+// k_fbwd_delta writes the row deltas, k_fbwd_dkv also writes dS = P * (dP -
+// Dl) of every (query, key <= query) piece it forms, and k_fbwd_dq_ds forms
+// dQ = scale * dS K from it, so dQ no longer recomputes S and dP (7 products
+// -> 5, at the cost of writing and reading dS once: B * H * N^2 / 2 floats).
+// ---------------------------------------------------------------------------
+
+// Dl = rowsum(dO * O): 16 lanes per (b, n, h) row, lane i = 2 g + hf holding
+// elements 8 g + 4 hf .. + 3 (coalesced: a row's lanes read its 256 bytes);
+// the sums are taken as k_fbwd_dq takes them (each half's fragments in order
+// of g, then the two halves), so Dl has the same bits.
+template <int D, int MODE>
+__global__ __launch_bounds__(256) void k_fbwd_delta(FbwdArgs a, long rows) {
+  const long row = ((long)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const int i = threadIdx.x & 15;  // lane in the row
+  const long rr = row < rows ? row : rows - 1;
+  const int RS = MODE == 0 ? D : a.D;
+  float t = 0.f;
+  if (i < D / 4) {  // D / 8 groups of two halves: D / 4 lanes
+    const int d0 = 8 * (i >> 1) + 4 * (i & 1);
+    const f32x4 x = load4m<MODE>(a.dout + (size_t)rr * RS, d0, RS);
+    const f32x4 y = load4m<MODE>(a.o + (size_t)rr * RS, d0, RS);
+    t = x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+  }
+  float half[2] = {0.f, 0.f};
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int g = 0; g < D / 8; ++g) half[hf] += __shfl(t, (threadIdx.x & 48) + 2 * g + hf, 64);
+  if (i == 0 && row < rows) a.delta[row] = half[0] + half[1];
+}
+
+// dQ from the stored dS: one workgroup per (128 queries, b, h), rank 0 = the
+// last query block; each wave owns 32 queries. Per 32-key piece the lane of
+// query c loads its dS row's keys 8 qq + 4 hf .. + 3 (the k-steps of the
+// product, as k_fbwd_dq orders them) one piece ahead, and K goes through LDS
+// 64 rows at a time. dS of a key past the query (or past N) is masked by a
+// select: k_fbwd_dkv wrote zeros there only for the pieces it formed.
+template <int D, int MODE>
+__global__ __launch_bounds__(kThreads) void k_fbwd_dq_ds(FbwdArgs a) {
+  constexpr int DT = (D + 31) / 32;
+  constexpr int SP = D + 4;
+  constexpr int C4 = D / 4;
+  constexpr int NV = kCols * C4 / kThreads;  // float4 of K per thread per step
+  const int RS = MODE == 0 ? D : a.D;
+  __shared__ __attribute__((aligned(16))) float sK[kCols * SP];
+
+  const int H = a.H, N = a.N;
+  const int bh = (int)(blockIdx.x % (unsigned)a.BH), rank = (int)(blockIdx.x / (unsigned)a.BH);
+  const int b = bh / H, h = bh % H;
+  const int blk = a.n_blocks - 1 - rank;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 31, hf = lane >> 5;
+  const int qrow = blk * kRows + wave * 32 + c;
+  const bool qok = qrow < N;
+  const int qr = qok ? qrow : N - 1;
+  const int qlim = qok ? qrow : -1;  // keys <= qlim are unmasked
+  const int qb = blk * 4 + wave;  // the wave's query block
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+  const int q_last = min(blk * kRows + kRows, N) - 1;
+  const int wq_last = blk * kRows + wave * 32 < N ? min(blk * kRows + wave * 32 + 31, N - 1) : -1;
+  const int steps = q_last / kCols + 1;
+  const size_t rs = (size_t)H * RS;
+  const float* kh = a.k + row_off(b, 0, N, H, h, RS);
+
+  // dS of the piece at key0 for this lane: keys key0 + 8 qq + 4 hf + t, 64
+  // contiguous bytes of the tile (entries past N were never written: masked
+  // by a select, as every key past the query)
+  auto load_ds = [&](int key0, f32x4 (&x)[4]) {
+    const float* tp = ds_tile(a, bh, qb, key0 >> 5) + c * 32 + 16 * hf;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      x[qq] = *reinterpret_cast<const f32x4*>(tp + 4 * qq);
+      const int k0 = key0 + 8 * qq + 4 * hf;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) x[qq][t] = k0 + t <= qlim ? x[qq][t] : 0.f;
+    }
+  };
+  f32x4 cur[4], nxt[4] = {};
+  if (wq_last >= 0) load_ds(0, cur);
+  for (int j = 0; j < steps; ++j) {
+    f32x4 kr[NV];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int e = threadIdx.x + kThreads * u;
+      const int n = min(j * kCols + e / C4, N - 1);
+      kr[u] = load4m<MODE>(kh + (size_t)n * rs, 4 * (e % C4), RS);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int e = threadIdx.x + kThreads * u;
+      *reinterpret_cast<f32x4*>(sK + (e / C4) * SP + 4 * (e % C4)) = kr[u];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sub = 0; sub < kCols / 32; ++sub) {
+      const int key0 = j * kCols + sub * 32;
+      if (key0 > wq_last) break;  // wave-uniform: every later key is masked for this wave
+      if (key0 + 32 <= wq_last) load_ds(key0 + 32, nxt);
+      // dQ^T[d][query] += sum_key K[key][d] dS^T[key][query]
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int dcol = dt * 32 + c;
+        const bool dok = (MODE == 0 && D % 32 == 0) || dcol < RS;
+        const float* kc = sK + (sub * 32 + 4 * hf) * SP + (dok ? dcol : RS - 1);
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float kv = kc[(8 * qq + t) * SP];
+            acc[dt] = mfma(dok ? kv : 0.f, cur[qq][t], acc[dt]);
+          }
+        }
+      }
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) cur[qq] = nxt[qq];
+    }
+  }
+  if (qok) {
+    const size_t qoff = row_off(b, qr, N, H, h, RS);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = dt * 32 + 8 * qq + 4 * hf;
+        const f32x4 y = {acc[dt][4 * qq] * a.scale, acc[dt][4 * qq + 1] * a.scale,
+                         acc[dt][4 * qq + 2] * a.scale, acc[dt][4 * qq + 3] * a.scale};
+        store4m<MODE>(a.dq + qoff, d0, RS, y);
+      }
+    }
+  }
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Padded head dim and load mode of a head dim: a multiple of 16 up to 128,
@@ -622,6 +794,7 @@ FbwdArgs fbwd_args(float* dq, float* dk, float* dv, const float* q, const float*
   a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.L = L; a.M = M;
   a.dq = dq; a.dk = dk; a.dv = dv;
   a.delta = delta;
+  a.ds = nullptr;
   a.N = N; a.H = H; a.D = D;
   a.n_blocks = (N + kRows - 1) / kRows;
   a.scale = scale;
@@ -665,6 +838,38 @@ int fbwd_launch(const FbwdArgs& a, const FlashShape& fs, hipStream_t s) {
   SKV_FLASH_SHAPES(SKV_FB)
   return set_error(SKV_E_UNSUPPORTED, "skv_flash_bwd: no kernel for head_dim %d", a.D);
 }
+
+// The five-product backward (a.ds set): row deltas, dK/dV with dS written,
+// then dQ from dS.
+#define SKV_FB_DS(DD, MM)                                                            \
+  if (fs.DP == DD && fs.mode == MM) {                                                \
+    hipLaunchKernelGGL((k_fbwd_delta<DD, MM>), dim3((unsigned)((rows + 15) / 16)),    \
+                       dim3(256), 0, s, a, rows);                                    \
+    int rc = check_launch("skv_flash_bwd");                                          \
+    if (rc) return rc;                                                               \
+    hipLaunchKernelGGL((k_fbwd_dkv<DD, MM, true>), grid, dim3(kThreads), 0, s, a);   \
+    rc = check_launch("skv_flash_bwd");                                              \
+    if (rc) return rc;                                                               \
+    hipLaunchKernelGGL((k_fbwd_dq_ds<DD, MM>), grid, dim3(kThreads), 0, s, a);       \
+    return check_launch("skv_flash_bwd");                                            \
+  }
+int fbwd_launch_ds(const FbwdArgs& a, const FlashShape& fs, long rows, hipStream_t s) {
+  const dim3 grid((unsigned)(a.n_blocks * a.BH));
+  SKV_FB_DS(16, 0) SKV_FB_DS(16, 1) SKV_FB_DS(16, 2) SKV_FB_DS(32, 0) SKV_FB_DS(32, 1)
+  SKV_FB_DS(32, 2) SKV_FB_DS(48, 0) SKV_FB_DS(48, 1) SKV_FB_DS(48, 2) SKV_FB_DS(64, 0)
+  SKV_FB_DS(64, 1) SKV_FB_DS(64, 2)
+  return set_error(SKV_E_UNSUPPORTED, "skv_flash_bwd: no kernel for head_dim %d", a.D);
+}
+#undef SKV_FB_DS
+
+// Workspace of the five-product backward: the row deltas (256-byte
+// aligned block), then dS; 0 where that path does not apply.
+size_t fbwd_ds_bytes(int B, int N, int H, int D) {
+  if (B <= 0 || N <= 0 || H <= 0 || D <= 0 || D > 64) return 0;
+  const size_t dl = ((size_t)B * N * H * sizeof(float) + 255) / 256 * 256;
+  const size_t n32 = ((size_t)N + 31) / 32 * 32;  // N in whole 32 x 32 tiles
+  return dl + (size_t)B * H * n32 * n32 * sizeof(float);
+}
 }  // namespace
 #endif
 #undef SKV_FB
@@ -677,6 +882,11 @@ using namespace skv;
 extern "C" size_t skv_flash_bwd_workspace_bytes(int B, int N, int H) {
   if (B <= 0 || N <= 0 || H <= 0) return 0;
   return (size_t)B * N * H * sizeof(float);
+}
+
+extern "C" size_t skv_flash_bwd_fast_workspace_bytes(int B, int N, int H, int D) {
+  const size_t fast = fbwd_ds_bytes(B, N, H, D);
+  return fast ? fast : skv_flash_bwd_workspace_bytes(B, N, H);
 }
 
 extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, const float* k,
@@ -705,6 +915,13 @@ extern "C" int skv_flash_bwd(float* dq, float* dk, float* dv, const float* q, co
   if (fs.DP > 128)  // kernels of the wide translation unit
     return fbwd_wide(dq, dk, dv, q, k, v, o, L, M, dout, a.delta, B, N, H, D, scale, fs.DP,
                      fs.mode, s);
+  const size_t fast = fbwd_ds_bytes(B, N, H, D);
+  if (fast && ws_bytes >= fast) {  // room for dS: the five-product path
+    FbwdArgs ad = a;
+    ad.ds = reinterpret_cast<float*>(static_cast<char*>(ws) +
+                                     ((size_t)B * N * H * sizeof(float) + 255) / 256 * 256);
+    return fbwd_launch_ds(ad, fs, (long)B * N * H, s);
+  }
   return fbwd_launch(a, fs, s);
 }
 

@@ -66,6 +66,7 @@ _SIGNATURES = {
     "skv_sample_workspace_bytes": (_Z, [_I, _I]),
     "skv_flash_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
     "skv_flash_bwd_workspace_bytes": (_Z, [_I, _I, _I]),
+    "skv_flash_bwd_fast_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "skv_flash_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _Z,
                            _P]),
     "skv_bpe_train": (_I, [_P, _Z, _I, _P, _I, ctypes.POINTER(_I)]),

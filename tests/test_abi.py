@@ -170,6 +170,10 @@ def test_flash_bwd_rejects_bad_arguments():
     B, N, H = 2, 100, 3
     need = L.skv_flash_bwd_workspace_bytes(B, N, H)
     assert need == B * N * H * 4 and L.skv_flash_bwd_workspace_bytes(0, N, H) == 0
+    # the five-product form: the row deltas (256-byte aligned block), then dS [B*H][N][N]
+    # in 32 x 32 tiles (N = 100 -> 4 x 4 tiles)
+    assert L.skv_flash_bwd_fast_workspace_bytes(B, N, H, 64) == 2560 + B * H * 128 * 128 * 4
+    assert L.skv_flash_bwd_fast_workspace_bytes(B, N, H, 65) == need  # D > 64: seven products
 
     def call(D=64, ws_bytes=None, ptr=fake, scale=0.125, n=N):
         return L.skv_flash_bwd(ptr, fake, fake, fake, fake, fake, fake, fake, fake, fake, B, n,

@@ -40,13 +40,15 @@ def _lib():
     return _lib
 
 
-def flash_bwd(q, k, v, o, L, M, do, B, N, H, D):
-    """dq, dk, dv of device fp32 tensors through the C ABI."""
+def flash_bwd(q, k, v, o, L, M, do, B, N, H, D, fast=False):
+    """dq, dk, dv of device fp32 tensors through the C ABI; fast: with the
+    workspace of the five-product form (dS stored, where it applies)."""
     lib = _lib()
     L_ = lib.lib()
     dq, dk, dv = (torch.empty_like(q) for _ in range(3))
-    ws = torch.empty(max(L_.skv_flash_bwd_workspace_bytes(B, N, H), 16), dtype=torch.uint8,
-                     device=q.device)
+    nb = (L_.skv_flash_bwd_fast_workspace_bytes(B, N, H, D) if fast
+          else L_.skv_flash_bwd_workspace_bytes(B, N, H))
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=q.device)
     rc = L_.skv_flash_bwd(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), q.data_ptr(), k.data_ptr(),
                           v.data_ptr(), o.data_ptr(), L.data_ptr(), M.data_ptr(), do.data_ptr(),
                           B, N, H, D, float(1 / np.sqrt(D)), ws.data_ptr(), ws.numel(),
@@ -106,16 +108,18 @@ SHAPES = [(1, 1, 1, 16), (2, 5, 3, 16), (1, 63, 2, 32), (2, 64, 1, 32), (1, 65, 
           (1, 129, 3, 64), (2, 200, 2, 128), (1, 300, 1, 64), (1, 513, 2, 128), (3, 40, 2, 64)]
 
 
+@pytest.mark.parametrize("fast", [False, True])
 @pytest.mark.parametrize("B,N,H,D", SHAPES)
-def test_ragged_shapes_match_oracle(gpu_ctx, B, N, H, D):
-    banner(f"flash bwd vs oracle B={B} N={N} H={H} D={D}")
+def test_ragged_shapes_match_oracle(gpu_ctx, B, N, H, D, fast):
+    banner(f"flash bwd vs oracle B={B} N={N} H={H} D={D} fast={fast}")
     rng = np.random.default_rng(B * 1000 + N * 10 + D)
     Q, K, V, dO = (rng.standard_normal((B * N, H * D)).astype(np.float32) for _ in range(4))
     O, L, M = ko.flash_attention(Q, K, V, B, N, H, D)
     O, L, M = O.astype(np.float32), L.astype(np.float32), M.astype(np.float32)
     want = ko.flash_attention_backward(Q, K, V, O, L, M, dO, B, N, H, D)
     dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
-    got = flash_bwd(dev(Q), dev(K), dev(V), dev(O), dev(L), dev(M), dev(dO), B, N, H, D)
+    got = flash_bwd(dev(Q), dev(K), dev(V), dev(O), dev(L), dev(M), dev(dO), B, N, H, D,
+                    fast=fast)
     for name, g, w in zip(("dq", "dk", "dv"), got, want):
         g = g.cpu().numpy()
         if N == 1 and name != "dv":
@@ -125,6 +129,29 @@ def test_ragged_shapes_match_oracle(gpu_ctx, B, N, H, D):
         err = _rel(g, w)
         print(f"{name} rel_err={err:.2e}")
         assert err < TOL, (name, err)
+
+
+@pytest.mark.parametrize("B,N,H,D", [(2, 300, 3, 64), (1, 517, 2, 48), (3, 128, 2, 40),
+                                     (2, 261, 2, 20), (1, 64, 4, 16), (2, 1024, 4, 32),
+                                     (1, 1, 2, 64), (2, 33, 3, 36)])
+def test_five_product_form_gives_the_same_bits(gpu_ctx, B, N, H, D):
+    """With the larger workspace (D <= 64) the dK/dV kernel writes
+    dS and dQ is formed from it instead of from S and dP recomputed: the same
+    products in the same order, so dq, dk and dv are bit-identical to the
+    seven-product form's (head dims with every load mode)."""
+    banner(f"flash bwd five-product form B={B} N={N} H={H} D={D}")
+    L_ = _lib().lib()
+    assert L_.skv_flash_bwd_fast_workspace_bytes(B, N, H, D) > L_.skv_flash_bwd_workspace_bytes(
+        B, N, H)
+    rng = np.random.default_rng(N + D)
+    Q, K, V, dO = (rng.standard_normal((B * N, H * D)).astype(np.float32) for _ in range(4))
+    O, L, M = ko.flash_attention(Q, K, V, B, N, H, D)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    args = (dev(Q), dev(K), dev(V), dev(O), dev(L), dev(M), dev(dO), B, N, H, D)
+    slow = flash_bwd(*args)
+    fast = flash_bwd(*args, fast=True)
+    for name, a, b in zip(("dq", "dk", "dv"), slow, fast):
+        assert torch.equal(a, b), name
 
 
 def _torch_reference(q, k, v, do, B, N, H, D):
@@ -152,7 +179,8 @@ def test_bench_shape_against_torch_fp32_and_identities(gpu_ctx, B, N, H, D):
     g = torch.Generator(device="cuda").manual_seed(11)
     q, k, v, do = (torch.randn(B * N, H * D, device="cuda", generator=g) for _ in range(4))
     o, L, M, rq, rk, rv = _torch_reference(q, k, v, do, B, N, H, D)
-    dq, dk, dv = flash_bwd(q, k, v, o, L, M, do, B, N, H, D)
+    # the form the bench times: five products where D <= 64 (the workspace holds dS)
+    dq, dk, dv = flash_bwd(q, k, v, o, L, M, do, B, N, H, D, fast=True)
     for name, x, r in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
         err = float((x - r).double().norm() / r.double().norm())
         print(f"{name} rel_err vs torch fp32 = {err:.2e}")
@@ -163,6 +191,9 @@ def test_bench_shape_against_torch_fp32_and_identities(gpu_ctx, B, N, H, D):
     assert float((sdv - sdo).norm() / sdo.norm()) < TOL
     sdk = dk.double().view(B, N, H, D).sum(1)
     assert float(sdk.abs().max() / dk.double().view(B, N, H, D).abs().sum(1).max()) < TOL
-    again = flash_bwd(q, k, v, o, L, M, do, B, N, H, D)
+    again = flash_bwd(q, k, v, o, L, M, do, B, N, H, D, fast=True)
     for x, y in zip((dq, dk, dv), again):
         assert torch.equal(x, y)  # bitwise reproducible
+    seven = flash_bwd(q, k, v, o, L, M, do, B, N, H, D)
+    for x, y in zip((dq, dk, dv), seven):
+        assert torch.equal(x, y)  # the seven-product form gives the same bits
