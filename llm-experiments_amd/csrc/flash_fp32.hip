@@ -696,17 +696,12 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq_ds(FbwdArgs a) {
   const float* kh = a.k + row_off(b, 0, N, H, h, RS);
 
   // dS of the piece at key0 for this lane: keys key0 + 8 qq + 4 hf + t, 64
-  // contiguous bytes of the tile (entries past N were never written: masked
-  // by a select, as every key past the query)
+  // contiguous bytes of the tile, loaded a piece ahead; masked only where it
+  // is used (a select there, not here, so the load is not waited for at once)
   auto load_ds = [&](int key0, f32x4 (&x)[4]) {
     const float* tp = ds_tile(a, bh, qb, key0 >> 5) + c * 32 + 16 * hf;
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      x[qq] = *reinterpret_cast<const f32x4*>(tp + 4 * qq);
-      const int k0 = key0 + 8 * qq + 4 * hf;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) x[qq][t] = k0 + t <= qlim ? x[qq][t] : 0.f;
-    }
+    for (int qq = 0; qq < 4; ++qq) x[qq] = *reinterpret_cast<const f32x4*>(tp + 4 * qq);
   };
   f32x4 cur[4], nxt[4] = {};
   if (wq_last >= 0) load_ds(0, cur);
@@ -730,6 +725,12 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq_ds(FbwdArgs a) {
       const int key0 = j * kCols + sub * 32;
       if (key0 > wq_last) break;  // wave-uniform: every later key is masked for this wave
       if (key0 + 32 <= wq_last) load_ds(key0 + 32, nxt);
+      // keys past the query (or past N: entries never written) weigh 0, by a select
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          cur[qq][t] = key0 + 8 * qq + 4 * hf + t <= qlim ? cur[qq][t] : 0.f;
       // dQ^T[d][query] += sum_key K[key][d] dS^T[key][query]
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
