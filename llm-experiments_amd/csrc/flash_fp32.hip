@@ -705,14 +705,17 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq_ds(FbwdArgs a) {
   };
   f32x4 cur[4], nxt[4] = {};
   if (wq_last >= 0) load_ds(0, cur);
-  for (int j = 0; j < steps; ++j) {
-    f32x4 kr[NV];
+  f32x4 kr[NV];  // the next step's K rows, loaded a step ahead
+  auto load_k = [&](int j) {
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
       const int e = threadIdx.x + kThreads * u;
       const int n = min(j * kCols + e / C4, N - 1);
       kr[u] = load4m<MODE>(kh + (size_t)n * rs, 4 * (e % C4), RS);
     }
+  };
+  load_k(0);
+  for (int j = 0; j < steps; ++j) {
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
@@ -720,6 +723,7 @@ __global__ __launch_bounds__(kThreads) void k_fbwd_dq_ds(FbwdArgs a) {
       *reinterpret_cast<f32x4*>(sK + (e / C4) * SP + 4 * (e % C4)) = kr[u];
     }
     __syncthreads();
+    if (j + 1 < steps) load_k(j + 1);
 #pragma unroll
     for (int sub = 0; sub < kCols / 32; ++sub) {
       const int key0 = j * kCols + sub * 32;
