@@ -422,13 +422,15 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
     {
       const int gr = lane >> 4, L = lane & 15;
       const int dq = (gr & 1) * 16 + 4 * (L & 3);  // d offset within the 32-row block
+      // kk outside db: consecutive MFMAs accumulate into different O blocks
+      // (each block still takes its four k-blocks in the same order)
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const int d = db * 32 + dq;
+        for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
+          for (int db = 0; db < DB; ++db) {
+            const int d = db * 32 + dq;
             const int r0 = tb * 32 + kk * 16 + 4 * g + (L >> 2);
             const int r1 = r0 + 8;
             const uint16_t* p0 = sv(stage) + swz<D>(r0, d >> 3) + (d & 7);
@@ -442,7 +444,6 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
               o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf[qb][tb * 2 + kk],
                                                                    o[qb][db], 0, 0, 0);
           }
-        }
     }
 
     if constexpr (GEN && D > 128) reg_tile_load(t0 + kBN);
