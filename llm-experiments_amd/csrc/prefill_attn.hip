@@ -17,9 +17,10 @@
 //    O^T += V^T P^T needs (accumulator slot r of rows 8kk..8kk+7 is slot j of
 //    k-block kk). Only V needs a transpose, done once per tile while staging
 //    it into LDS.
-//  * Workgroup = 8 wavefronts of 32 query rows (256 rows). A wavefront needs
-//    ~206 registers at D = 128, so two run on each SIMD and the softmax of
-//    one overlaps the MFMAs of the other. (With 4 wavefronts of 64 rows, each
+//  * Workgroup = 8 wavefronts of 32 query rows (256 rows). A wavefront fits
+//    the 256 registers of two wavefronts per SIMD at D = 128 (148 at D = 64),
+//    so two run on each SIMD and the softmax of one overlaps the MFMAs of
+//    the other. (With 4 wavefronts of 64 rows, each
 //    K/V operand fed two MFMAs, but ~460 registers were live and the
 //    compiler shuttled values between AGPRs and VGPRs on every tile: 11%
 //    slower, measured on MI355X.) K/V tiles of 64 tokens are double
