@@ -197,7 +197,7 @@ __global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_fbwd_dq(FbwdArgs 
     const f32x4 od = load4m<MODE>(a.o + qoff, d0, RS);
     dl += df[g].x * od.x + df[g].y * od.y + df[g].z * od.z + df[g].w * od.w;
   }
-  dl += __shfl_xor(dl, 32);
+  dl = xor32_sum(dl);
   const size_t srow = (size_t)(b * N + qr) * H + h;
   if (qok && hf == 0) a.delta[srow] = dl;
   const float m2 = a.M[srow] * LOG2E;
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_flash_fwd(FfwdArg
         s[r] = key <= qlim ? s[r] * a.sl2 : -INFINITY;
         tmax = fmaxf(tmax, s[r]);
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));  // both halves hold the same query
+      tmax = xor32_max(tmax);  // both halves hold the same query
       m_true = fmaxf(m_true, tmax);
       const bool upd = tmax > m_run + 8.f;  // also true on the first piece with a key
       if (__ballot(upd) != 0ull) {          // wave-uniform branch
@@ -606,7 +606,7 @@ __global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_flash_fwd(FfwdArg
       }
     }
   }
-  const float lt = l + __shfl_xor(l, 32);
+  const float lt = xor32_sum(l);
   if (qi >= C) return;
   const size_t orow = ((size_t)b * C + qi) * Hq + h;
   const float inv = qok ? 1.f / lt : 0.f;  // a valid row saw its own key: lt >= 1

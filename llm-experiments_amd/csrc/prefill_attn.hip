@@ -384,7 +384,7 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
       for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[tb][qb][r]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      tmax = xor32_max(tmax);  // lanes l and l ^ 32 hold the same query
       // Lazy rescaling: the running max m only moves when the tile's max
       // exceeds it by more than 8 (log2 units), so probabilities stay
       // <= 2^8 (exact in fp32, in range for bf16) and O, l are rescaled
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
   const int CG = a.C * G;  // output rows of this (b, hk): query i, head h -> i * G + h % G
   float lt[kQB];
 #pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) lt[qb] = l[qb] + __shfl_xor(l[qb], 32);
+  for (int qb = 0; qb < kQB; ++qb) lt[qb] = xor32_sum(l[qb]);
   // Row r's output from its normalised values v(db, r4, e), or zeros for a
   // row past the sequence's new tokens; rows past the chunk are not stored.
   auto store_row = [&](int r, auto&& v) {

@@ -179,6 +179,22 @@ __device__ __forceinline__ float row16_max(float x) {
   return x;
 }
 
+// x of this lane and x of lane ^ 32, without the LDS round trip of a
+// ds_bpermute shuffle: v_permlane32_swap exchanges the two 32-lane halves of a
+// register, so the pair (first, second) holds (x of lanes 0-31, x of lanes
+// 32-63) in every lane. Max and sum over the pair are exact / commutative, so
+// they equal x op shfl_xor(x, 32) bit for bit.
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // 2^x on the hardware exp unit (v_exp_f32). exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
