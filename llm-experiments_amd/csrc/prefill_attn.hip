@@ -126,6 +126,18 @@ __device__ __forceinline__ void dma16(const uint16_t* src, const uint16_t* lds_b
                                    (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
 }
 
+// The same through a buffer descriptor (buffer_load_dwordx4 ... lds): lane i
+// writes lds_base + 16 * i with the 16 bytes at byte offset voff of the
+// buffer, or zeros where voff + 16 passes the descriptor's size. (The
+// compiler keeps counting the wavefront's LDS reads in order past these, where
+// a pending global_load_lds makes it wait for all of them.)
+constexpr int kRsrcW3 = 0x00020000;  // descriptor word 3: raw 32-bit data
+__device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff,
+                                          const uint16_t* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(lds_base),
+                                           16, voff, 0, 0, 0);
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives as its slot j
 // the element i%4 of the four 16-bit values addressed by lane 4j + i/4.
 __device__ __forceinline__ i16x4 lds_read_tr16(const uint16_t* p) {
@@ -248,12 +260,16 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
   const uint16_t* kbase = a.k + ((size_t)b * a.T_cap * a.Hkv + hk) * RS;
   const uint16_t* vbase = a.v + ((size_t)b * a.T_cap * a.Hkv + hk) * RS;
 
-  // Tiles go from HBM straight into LDS (global_load_lds_dwordx4: each lane
-  // moves 16 bytes, a wavefront fills 1 KB of LDS in lane order), so no
+  // Tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds: each
+  // lane moves 16 bytes, a wavefront fills 1 KB of LDS in lane order), so no
   // registers are spent on staging. A lane picks the global chunk that the
-  // swizzled layout stores at its LDS position. Token rows past kv_end are
-  // clamped to the last filled row (in bounds, masked later); the tile after
-  // the last one is fetched too and never read.
+  // swizzled layout stores at its LDS position. Each tile's descriptor starts
+  // at its first row and covers only the rows below kv_end, so rows past it
+  // read zeros (masked later) and nothing outside the cache is addressed; the
+  // tile after the last one is fetched too and never read. (With the DMA as
+  // global_load_lds the compiler waited for every pending LDS read before
+  // each MFMA operand, as a pending global access that writes LDS made it
+  // stop counting them in order: 552.2 -> 531.9 us per C4 chunk, same bits.)
   constexpr int RPK = 1024 / (D * 2);          // token rows per 1 KB
   constexpr int KPT = kBN * D * 2 / 1024;      // 1 KB pieces per tile and tensor
   static_assert(GEN || KPT % W == 0, "tile pieces must split over the wavefronts");
@@ -302,16 +318,32 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
       *reinterpret_cast<uint4*>(&sm.v[ST][swz<D>(row, lch)]) = rv[u];
     }
   };
+  // Per lane, the byte offset of its 16-byte chunk within a tile (the same
+  // for every tile): token row piece * RPK + lane / (D / 8), swizzled chunk.
+  uint32_t dma_off[GEN ? 1 : KPT / W];
+  if constexpr (!GEN) {
+#pragma unroll
+    for (int c = 0; c < KPT / W; ++c) {
+      const int piece = wave * (KPT / W) + c;
+      const int row = piece * RPK + lane / (D / 8);
+      const int lch = (lane % (D / 8)) ^ swz_key<D>(row);
+      dma_off[c] = (uint32_t)(row * row_stride + lch * 8) * 2u;
+    }
+  }
 #define SKV_DMA_TILE(T0, ST)                                                                 \
   if constexpr (!GEN) {                                                                      \
+    /* a buffer over the tile's rows that exist: rows past kv_end read zeros */             \
+    const int rows_ = max(0, min(kv_end - (T0), kBN));                                       \
+    const int nrec_ = rows_ > 0 ? (int)(((rows_ - 1) * row_stride + D) * 2) : 0;           \
+    const size_t base_ = (size_t)max(min((T0), kv_end - 1), 0) * row_stride;               \
+    const __amdgpu_buffer_rsrc_t rk_ =                                                       \
+        __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + base_), (short)0, nrec_, kRsrcW3);  \
+    const __amdgpu_buffer_rsrc_t rv_ =                                                       \
+        __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + base_), (short)0, nrec_, kRsrcW3);  \
     _Pragma("unroll") for (int c = 0; c < KPT / W; ++c) {                                    \
       const int piece = wave * (KPT / W) + c;                                                \
-      const int row = piece * RPK + lane / (D / 8);                                          \
-      const int pch = lane % (D / 8);                                                        \
-      const int lch = pch ^ swz_key<D>(row);                                                 \
-      const size_t gofs = (size_t)min((T0) + row, kv_end - 1) * row_stride + lch * 8;        \
-      dma16(kbase + gofs, sk(std::integral_constant<int, (ST)>{}) + piece * 512);            \
-      dma16(vbase + gofs, sv(std::integral_constant<int, (ST)>{}) + piece * 512);            \
+      buf_dma16(rk_, dma_off[c], sk(std::integral_constant<int, (ST)>{}) + piece * 512);     \
+      buf_dma16(rv_, dma_off[c], sv(std::integral_constant<int, (ST)>{}) + piece * 512);     \
     }                                                                                        \
   }
 
