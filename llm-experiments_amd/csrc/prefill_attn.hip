@@ -118,17 +118,10 @@ __device__ __forceinline__ int swz(int row, int chunk) {  // element offset of a
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-// 16 bytes from global memory straight into LDS (global_load_lds_dwordx4):
-// lane i of the wavefront writes lds_base + 16 * i. lds_base must be the
-// same for every lane of the wavefront.
-__device__ __forceinline__ void dma16(const uint16_t* src, const uint16_t* lds_base) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src),
-                                   (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
-}
-
-// The same through a buffer descriptor (buffer_load_dwordx4 ... lds): lane i
-// writes lds_base + 16 * i with the 16 bytes at byte offset voff of the
-// buffer, or zeros where voff + 16 passes the descriptor's size. (The
+// 16 bytes from global memory straight into LDS through a buffer descriptor
+// (buffer_load_dwordx4 ... lds): lane i writes lds_base + 16 * i with the 16
+// bytes at byte offset voff of the buffer, or zeros where voff + 16 passes
+// the descriptor's size. lds_base must be the same for every lane. (The
 // compiler keeps counting the wavefront's LDS reads in order past these, where
 // a pending global_load_lds makes it wait for all of them.)
 constexpr int kRsrcW3 = 0x00020000;  // descriptor word 3: raw 32-bit data
