@@ -171,8 +171,14 @@ __global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_fbwd_dq(FbwdArgs 
   constexpr int DT = (D + 31) / 32;    // 32-row tiles of dQ^T
   constexpr int SP = Stage<D, MODE>::SP;
   const int RS = MODE == 0 ? D : a.D;  // the real head dim: row stride, last valid column + 1
-  __shared__ __attribute__((aligned(16))) float sK[kCols * SP];
-  __shared__ __attribute__((aligned(16))) float sV[kCols * SP];
+  // K and V tiles in one LDS object (one base register plus immediates)
+  struct alignas(16) KV {
+    float k[kCols * SP];
+    float v[kCols * SP];
+  };
+  __shared__ KV skv;
+  float* const sK = skv.k;
+  float* const sV = skv.v;
 
   const int H = a.H, N = a.N;
   const int bh = (int)(blockIdx.x % (unsigned)a.BH), rank = (int)(blockIdx.x / (unsigned)a.BH);
@@ -311,12 +317,22 @@ __global__ __launch_bounds__(kThreads, fbwd_v_in_lds<D>() ? 2 : 1) void k_fbwd_d
   constexpr int SP = Stage<D, MODE>::SP;
   constexpr bool VL = fbwd_v_in_lds<D>();
   const int RS = MODE == 0 ? D : a.D;  // the real head dim
-  __shared__ __attribute__((aligned(16))) float sQ[kCols * SP];
-  __shared__ __attribute__((aligned(16))) float sD[kCols * SP];  // dO
-  __shared__ __attribute__((aligned(16))) float sV[VL ? kRows * SP : 4];  // the block's V rows
-  __shared__ __attribute__((aligned(16))) float sM2[kCols];
-  __shared__ __attribute__((aligned(16))) float sIL[kCols];
-  __shared__ __attribute__((aligned(16))) float sDL[kCols];
+  // One LDS object: the arrays sit at fixed offsets from each other, so a
+  // lane's addresses into all of them are one register plus immediates (as
+  // separate objects the compiler kept a register per array and spilled some)
+  struct alignas(16) Smem {
+    float q[kCols * SP];
+    float d[kCols * SP];  // dO
+    float m2[kCols], il[kCols], dl[kCols];
+    float v[VL ? kRows * SP : 4];  // the block's V rows
+  };
+  __shared__ Smem sm;
+  float* const sQ = sm.q;
+  float* const sD = sm.d;
+  float* const sV = sm.v;
+  float* const sM2 = sm.m2;
+  float* const sIL = sm.il;
+  float* const sDL = sm.dl;
 
   const int H = a.H, N = a.N;
   const int bh = (int)(blockIdx.x % (unsigned)a.BH), rank = (int)(blockIdx.x / (unsigned)a.BH);
@@ -510,8 +526,14 @@ __global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_flash_fwd(FfwdArg
   constexpr int DT = (D + 31) / 32;
   constexpr int SP = Stage<D, MODE>::SP;
   const int RS = MODE == 0 ? D : a.D;  // the real head dim
-  __shared__ __attribute__((aligned(16))) float sK[kCols * SP];
-  __shared__ __attribute__((aligned(16))) float sV[kCols * SP];
+  // K and V tiles in one LDS object (one base register plus immediates)
+  struct alignas(16) KV {
+    float k[kCols * SP];
+    float v[kCols * SP];
+  };
+  __shared__ KV skv;
+  float* const sK = skv.k;
+  float* const sV = skv.v;
 
   const int Hq = a.Hq, C = a.C;
   const int bh = (int)(blockIdx.x % (unsigned)a.BH), rank = (int)(blockIdx.x / (unsigned)a.BH);
