@@ -431,19 +431,39 @@ __global__ __launch_bounds__(kThreads, fbwd_v_in_lds<D>() ? 2 : 1) void k_fbwd_d
       }
       // s[r], dp[r]: query q0 + 8(r/4) + 4hf + r%4, key krow
       f32x16 p, ds;
+      // wave-uniform: every key of the wave precedes every query of the
+      // piece and every query exists, so no slot is masked or skipped
+      const bool interior = q0 >= wk0 + 31 && q0 + 32 <= N;
+      if (interior) {
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int ql = sub * 32 + 8 * qq + 4 * hf;
-        const f32x4 m4 = *reinterpret_cast<const f32x4*>(sM2 + ql);
-        const f32x4 i4 = *reinterpret_cast<const f32x4*>(sIL + ql);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(sDL + ql);
+        for (int qq = 0; qq < 4; ++qq) {
+          const int ql = sub * 32 + 8 * qq + 4 * hf;
+          const f32x4 m4 = *reinterpret_cast<const f32x4*>(sM2 + ql);
+          const f32x4 i4 = *reinterpret_cast<const f32x4*>(sIL + ql);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(sDL + ql);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int r = 4 * qq + t, query = j * kCols + ql + t;
-          const float e = fast_exp2(s[r] * a.sl2 - m4[t]) * i4[t];
-          const float pr = (krow <= query && query < N) ? e : 0.f;
-          p[r] = pr;
-          ds[r] = pr * (dp[r] - d4[t]);
+          for (int t = 0; t < 4; ++t) {
+            const int r = 4 * qq + t;
+            const float e = fast_exp2(s[r] * a.sl2 - m4[t]) * i4[t];
+            p[r] = e;
+            ds[r] = e * (dp[r] - d4[t]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int ql = sub * 32 + 8 * qq + 4 * hf;
+          const f32x4 m4 = *reinterpret_cast<const f32x4*>(sM2 + ql);
+          const f32x4 i4 = *reinterpret_cast<const f32x4*>(sIL + ql);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(sDL + ql);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int r = 4 * qq + t, query = j * kCols + ql + t;
+            const float e = fast_exp2(s[r] * a.sl2 - m4[t]) * i4[t];
+            const float pr = (krow <= query && query < N) ? e : 0.f;
+            p[r] = pr;
+            ds[r] = pr * (dp[r] - d4[t]);
+          }
         }
       }
       if constexpr (DSO) {
@@ -452,11 +472,17 @@ __global__ __launch_bounds__(kThreads, fbwd_v_in_lds<D>() ? 2 : 1) void k_fbwd_d
         // lanes of a half write one query's 128-byte tile row
         if (krow < N) {
           float* tp = dsw + (size_t)(q0 >> 5) * ((N + 31) >> 5) * 1024;
+          if (q0 + 32 <= N) {  // wave-uniform: every row of the tile exists
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int qi = 8 * (r / 4) + 4 * hf + (r % 4);  // query q0 + qi
-            if (q0 + qi < N)  // row qi of the tile; streamed past the caches (read once, later)
+            for (int r = 0; r < 16; ++r)
               __builtin_nontemporal_store(ds[r], tp + (8 * (r / 4) + (r % 4)) * 32);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int qi = 8 * (r / 4) + 4 * hf + (r % 4);  // query q0 + qi
+              if (q0 + qi < N)  // row qi of the tile; streamed past the caches (read once, later)
+                __builtin_nontemporal_store(ds[r], tp + (8 * (r / 4) + (r % 4)) * 32);
+            }
           }
         }
       }
