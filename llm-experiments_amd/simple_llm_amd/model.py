@@ -625,8 +625,9 @@ class Generator:
     (torch.cuda.CUDAGraph over the library's launches) and replayed.
     With retire_rows (the default) a sequence is retired once its last token
     is recorded: every layer's fill of its row becomes -1, so the remaining
-    steps read none of its cache (the fills in self.cache read -1 after
-    run(); run() starts from reset() each time).
+    steps read none of its cache. When run() returns, every row's fill is
+    back at the positions its cache holds, so forward_step or prefill can
+    continue on self.cache; run() starts from reset() each time.
     """
 
     def __init__(self, model: TransformerModel, prompts: Sequence[Sequence[int]],
