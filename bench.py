@@ -884,7 +884,8 @@ def run_fb(args, ctx):
                    "skv_flash_fwd")
 
     # the forward (O, L, M for the backward), timed on its own with HIP events
-    fwd()
+    # after the same clock settle as the prefill record (back-to-back calls)
+    fwd_settle_s = settle(lambda: [fwd() for _ in range(4)], lambda: None)
     fevs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in range(10)]
     for e0, e1 in fevs:
@@ -897,6 +898,7 @@ def run_fb(args, ctx):
     forward = {"mean_us": fwd_s * 1e6, "tflops": fwd_flops / fwd_s / 1e12,
                "peak_tflops": MFMA_FP32_PEAK_TFLOPS,
                "frac": fwd_flops / fwd_s / 1e12 / MFMA_FP32_PEAK_TFLOPS, "flops": fwd_flops,
+               "settle_s": round(fwd_settle_s, 3),
                "kernel": "skv_flash_fwd (k_flash_fwd), O, L, M in fp32"}
     dq, dk, dv = (torch.empty_like(q) for _ in range(3))
     # the workspace of the five-product form (the row deltas and dS)

@@ -586,8 +586,9 @@ __global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_flash_fwd(FfwdArg
   // keys this workgroup and this wave need
   const int blk_q = min(blk * kRows + kRows, n);  // valid queries of the block end here
   const int steps = blk * kRows < n ? (P + blk_q + kCols - 1) / kCols : 0;
-  const int wq_last = blk * kRows + wave * 32 < n ? P + min(blk * kRows + wave * 32 + 31, n - 1)
-                                                  : -1;
+  const int wq0 = blk * kRows + wave * 32;  // the wave's first query
+  const bool wfull = wq0 + 31 < n;           // all 32 of its queries valid
+  const int wq_last = wq0 < n ? P + min(wq0 + 31, n - 1) : -1;
   const size_t rs = (size_t)a.Hkv * RS;
   const float* kh = a.k + ((size_t)b * a.T_cap * a.Hkv + hk) * RS;
   const float* vh = a.v + ((size_t)b * a.T_cap * a.Hkv + hk) * RS;
@@ -612,13 +613,23 @@ __global__ __launch_bounds__(kThreads, D <= 64 ? 3 : 1) void k_flash_fwd(FfwdArg
         s = mfma(ka.z, qf[g].z, s);
         s = mfma(ka.w, qf[g].w, s);
       }
-      // s[r]: key key0 + 8(r/4) + 4hf + r%4 of this lane's query, in log2 units
+      // s[r]: key key0 + 8(r/4) + 4hf + r%4 of this lane's query, in log2 units.
+      // A piece wholly at or below the diagonal of a wave whose 32 queries
+      // are all valid masks nothing (wave-uniform test).
       float tmax = -INFINITY;
+      if (wfull && key0 + 31 <= P + wq0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = key0 + 8 * (r / 4) + 4 * hf + (r % 4);
-        s[r] = key <= qlim ? s[r] * a.sl2 : -INFINITY;
-        tmax = fmaxf(tmax, s[r]);
+        for (int r = 0; r < 16; ++r) {
+          s[r] *= a.sl2;
+          tmax = fmaxf(tmax, s[r]);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = key0 + 8 * (r / 4) + 4 * hf + (r % 4);
+          s[r] = key <= qlim ? s[r] * a.sl2 : -INFINITY;
+          tmax = fmaxf(tmax, s[r]);
+        }
       }
       tmax = xor32_max(tmax);  // both halves hold the same query
       m_true = fmaxf(m_true, tmax);
