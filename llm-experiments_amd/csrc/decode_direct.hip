@@ -87,8 +87,18 @@ template <typename TC, int D, int TOK, int S>
 __global__ __launch_bounds__(kDirRows * 16 / S) void k_decode_direct(DirectArgs a) {
   constexpr int EPL = D / 16;
   constexpr int R = kDirRows / S;  // rows of this workgroup
-  const int b = blockIdx.x, h = blockIdx.y, part = blockIdx.z, tid = threadIdx.x,
-            row = tid >> 4, ln = tid & 15;
+  // (sequence, head, part) from the flat workgroup index, the sequence
+  // slowest. The dispatcher deals workgroups in index order over the XCDs and
+  // their CUs, so indices 256 apart share a CU; with the sequence fastest
+  // (B = 16) those were parts of one sequence, and the CUs that drew a long
+  // row got all of its bytes. Sequence slowest, a CU's workgroups come from
+  // different sequences (C3, 16 ragged rows, fp32 cache, S = 4: 543.4 ->
+  // 528.7 us per decode step on MI355X, same output bits). B * H * S <= 2^31
+  // (checked on the host).
+  const unsigned wid = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int part = (int)(wid % S), h = (int)((wid / S) % (unsigned)a.H),
+            b = (int)(wid / (S * (unsigned)a.H));
+  const int tid = threadIdx.x, row = tid >> 4, ln = tid & 15;
   const int p = a.lens[b];
   const int Lc = min(max(p, 0), a.T_cap);  // cached rows of the sequence
   // this workgroup's part [t_lo, t_hi) of the cached rows
@@ -268,7 +278,8 @@ extern "C" int skv_append_decode_attn_direct(void* out, const void* q, void* k_c
   SKV_REQUIRE(out && q && k_cache && v_cache && new_k && new_v && lens, SKV_E_INVALID,
               "%s: null pointer argument", fn);
   SKV_REQUIRE(B > 0 && H > 0 && T_cap > 0, SKV_E_INVALID, "%s: dims must be > 0", fn);
-  SKV_REQUIRE(B <= 65535 && H <= 65535, SKV_E_UNSUPPORTED, "%s: grid too large", fn);
+  SKV_REQUIRE(B <= 65535 && H <= 65535 && (long)B * H * 4 <= 2147483647L, SKV_E_UNSUPPORTED,
+              "%s: grid too large", fn);
   SKV_REQUIRE(D == 64 || D == 128, SKV_E_UNSUPPORTED, "%s: D=%d (supported: 64, 128)", fn, D);
   SKV_REQUIRE((cache_dtype == SKV_F32 || cache_dtype == SKV_BF16) &&
                   (in_dtype == SKV_F32 || in_dtype == SKV_BF16) &&

@@ -235,8 +235,9 @@ class TransformerModel:
         4; direct_splits overrides it): 4 where a batch has few (sequence,
         head) pairs, or fp32 rows and fewer pairs than CUs, else 1. Measured
         on MI355X, whole generate runs: C1 (4 pairs) 11,330 tokens/s at 4
-        against 11,040 at 1; C3 (192 pairs) fp32 22,010 at 4 against 21,760
-        at 1 and 21,130 at 2, bf16 24,380 at 1 against 23,950 at 4."""
+        against 11,040 at 1; C3 (192 pairs) fp32 22,556 at 4 against 21,744
+        at 1 and 21,569 at 2, bf16 24,340 at 1 against 23,795 at 2 and 24,189
+        at 4."""
         if self.direct_splits:
             return int(self.direct_splits)
         pairs = B * self.tm_params.n_heads
