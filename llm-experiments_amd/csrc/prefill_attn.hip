@@ -691,6 +691,10 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
               SKV_E_INVALID, "%s: out, q, the caches and ws must be 16-byte aligned", fn);
   const int DK = kernel_dim(D);  // the kernel's (padded) head dim
   SKV_REQUIRE((size_t)C * H_q * D < (1u << 31), SKV_E_UNSUPPORTED, "%s: chunk too large", fn);
+  // a K/V tile's buffer descriptor spans kBN cache rows of H_kv * D elements
+  // (32-bit byte counts)
+  SKV_REQUIRE((long)H_kv * D * kBN * 2 < (1L << 31), SKV_E_UNSUPPORTED,
+              "%s: cache rows too wide (H_kv * head_dim = %ld)", fn, (long)H_kv * D);
   const int G = H_q / H_kv;
   SKV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, SKV_E_UNSUPPORTED,
               "%s: no kernel for G=%d", fn, G);

@@ -222,6 +222,10 @@ def test_prefill_rejects_bad_arguments():
     need = L.skv_prefill_workspace_bytes(2, 16, 4, 128, 2)
     assert need == 2 * 2 * 16 * 4 * (128 + 2) * 4
     assert call(ns=2, ws=fake, ws_bytes=need - 1) == _lib.SKV_E_WORKSPACE
+    # 65536 kv heads of 256: a 64-row K/V tile spans more than 2 GB of cache rows
+    assert L.skv_prefill_attn(fake, fake, fake, fake, fake, None, 2, 16, 65536, 65536, 256, 1024,
+                              0.125, 1, None, 0, 1, 1, 1, None) == _lib.SKV_E_UNSUPPORTED
+    assert b"too wide" in L.skv_last_error()
 
 
 def test_argmax_workspace_and_rejects():
