@@ -248,15 +248,15 @@ __global__ __launch_bounds__(kDirRows * 16 / S) void k_decode_direct(DirectArgs 
 template <typename TC, int D>
 void launch_direct(const DirectArgs& a, int S, hipStream_t s) {
   // tokens in flight per row: 4 at D = 128 (64 registers of K and V a lane;
-  // 16 wavefronts a CU leave 128); at D = 64, 8 for a bf16 cache and 4 for
-  // fp32 (C3, fp32 cache, S = 4, whole generate runs on MI355X: 22,652
-  // tokens/s at 4 against 22,540 at 8, 22,614 at 2, 22,504 at 6, 21,385 at
-  // 12)
-  constexpr int TOK = D == 64 ? (sizeof(TC) == 4 ? 4 : 8) : 4;
+  // 16 wavefronts a CU leave 128); at D = 64, 8 on one workgroup per row and
+  // 4 on split rows (C3, S = 4, whole generate runs on MI355X: fp32 cache
+  // 22,652 tokens/s at 4 against 22,540 at 8, 22,614 at 2, 22,504 at 6,
+  // 21,385 at 12; bf16 cache 24,493-24,503 at 4 against 24,165-24,172 at 8)
+  constexpr int TOK1 = D == 64 ? 8 : 4, TOKS = 4;
   const dim3 grid(a.B, a.H, S);
-  if (S == 1) hipLaunchKernelGGL((k_decode_direct<TC, D, TOK, 1>), grid, dim3(kDirRows * 16), 0, s, a);
-  else if (S == 2) hipLaunchKernelGGL((k_decode_direct<TC, D, TOK, 2>), grid, dim3(kDirRows * 8), 0, s, a);
-  else hipLaunchKernelGGL((k_decode_direct<TC, D, TOK, 4>), grid, dim3(kDirRows * 4), 0, s, a);
+  if (S == 1) hipLaunchKernelGGL((k_decode_direct<TC, D, TOK1, 1>), grid, dim3(kDirRows * 16), 0, s, a);
+  else if (S == 2) hipLaunchKernelGGL((k_decode_direct<TC, D, TOKS, 2>), grid, dim3(kDirRows * 8), 0, s, a);
+  else hipLaunchKernelGGL((k_decode_direct<TC, D, TOKS, 4>), grid, dim3(kDirRows * 4), 0, s, a);
 }
 
 }  // namespace

@@ -232,16 +232,16 @@ class TransformerModel:
 
     def direct_split(self, B: int, dtype: torch.dtype) -> int:
         """Workgroups per (sequence, head) of the direct attention (1, 2 or
-        4; direct_splits overrides it): 4 where a batch has few (sequence,
-        head) pairs, or fp32 rows and fewer pairs than CUs, else 1. Measured
-        on MI355X, whole generate runs: C1 (4 pairs) 11,330 tokens/s at 4
-        against 11,040 at 1; C3 (192 pairs) fp32 22,556 at 4 against 21,744
-        at 1 and 21,569 at 2, bf16 24,340 at 1 against 23,795 at 2 and 24,189
-        at 4."""
+        4; direct_splits overrides it): 4 where a batch has fewer (sequence,
+        head) pairs than CUs, else 1. Measured on MI355X, whole generate
+        runs: C1 (4 pairs) 11,330 tokens/s at 4 against 11,040 at 1; C3 (192
+        pairs) fp32 22,556 at 4 against 21,744 at 1 and 21,569 at 2, bf16
+        24,493-24,503 at 4 against 24,135-24,165 at 1 and 23,865-23,888 at 2.
+        dtype is kept for callers; both cache dtypes take the same rule."""
         if self.direct_splits:
             return int(self.direct_splits)
         pairs = B * self.tm_params.n_heads
-        return 4 if pairs < 64 or (dtype == torch.float32 and pairs < 256) else 1
+        return 4 if pairs < 256 else 1
 
     def prefill_buffers(self, B: int, C: int) -> _PrefillBuffers:
         key = ("prefill", B, C)
