@@ -634,7 +634,8 @@ def test_c2_full_run_every_step_matches_c_oracle(gpu_ctx, variant):
 @pytest.mark.parametrize("n_split", [1, 2, 4])
 @pytest.mark.parametrize("B,H,D,T,dt", [(1, 4, 64, 256, "f32"), (1, 4, 64, 256, "bf16"),
                                          (16, 12, 64, 1024, "f32"), (16, 12, 64, 1024, "bf16"),
-                                         (3, 5, 128, 700, "bf16")])
+                                         (3, 5, 128, 700, "bf16"), (5, 7, 64, 300, "f32"),
+                                         (5, 7, 128, 300, "f32")])
 def test_direct_attention_matches_oracle(gpu_ctx, B, H, D, T, dt, n_split):
     """skv_append_decode_attn_direct, the attention of the C1 (B=1, 4 x 64,
     context 256) and C3 (B=16, 12 x 64, context 1024) greedy steps, against
