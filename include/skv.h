@@ -207,7 +207,9 @@ int skv_append_decode_attn_paged(void* out, const void* q, void* k_pool, void* v
  */
 int skv_prefill_plan(int B, int C, int H_q, int H_kv, int max_kv_end, int* n_splits /* host */);
 
-/* Bytes of workspace skv_prefill_attn needs (0 when n_splits == 1). */
+/* Bytes of workspace skv_prefill_attn and skv_append_prefill_attn need (0
+ * when n_splits == 1): the split partials, then B int32 (16-byte padded) that
+ * skv_append_prefill_attn keeps the fills in. */
 size_t skv_prefill_workspace_bytes(int B, int C, int H_q, int D, int n_splits);
 
 /*
@@ -236,6 +238,26 @@ int skv_prefill_attn(void* out, const void* q, const void* k_cache, const void* 
                      const int32_t* start, const int32_t* n_new, int B, int C, int H_q,
                      int H_kv, int D, int T_cap, float scale, int n_splits, void* ws,
                      size_t ws_bytes, int cache_dt, int q_dt, int out_dt, skv_stream_t stream);
+
+/*
+ * One chunked-prefill call of a layer: skv_append_chunk (the chunk's K/V
+ * rows k_new, v_new [B, C, H_kv, D] of in_dt into the cache at lens[b]),
+ * then skv_prefill_attn over the cache with start = lens, then the fills
+ * advanced as skv_advance(lens, n_new, C, ...) does: the same outputs, cache
+ * rows and fills as those three calls in a row. On the split bf16 path
+ * (n_splits > 1) the attention keeps the fills in the workspace's tail and
+ * its merge pass advances them, so there is no separate advance launch. All
+ * of skv_prefill_attn's checks run before anything is launched, so a
+ * rejected call changes nothing. The reference's kv_cache_update
+ * (simple-llm/src/gpu/gpu_kv_cache.py:113-186) for a chunk of tokens
+ * followed by its flash_attention (gpu_pass_forward.py:497-588) with the
+ * cache prefix.
+ */
+int skv_append_prefill_attn(void* out, const void* q, void* k_cache, void* v_cache,
+                            const void* k_new, const void* v_new, int32_t* lens,
+                            const int32_t* n_new, int B, int C, int H_q, int H_kv, int D,
+                            int T_cap, float scale, int n_splits, void* ws, size_t ws_bytes,
+                            int cache_dt, int in_dt, int q_dt, int out_dt, skv_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Decode-step ops of the model around the cache (fp32). They replace the

@@ -85,6 +85,11 @@ struct PrefillArgs {
   float* ws_ml;  // [n_splits][B][C][Hq][2]
   int B;
   int D;         // head dim: the row stride of q, out and the caches
+  // skv_append_prefill_attn with a split: workgroup 0 of the attention keeps
+  // the fills as the call found them in snap, and the merge pass, which reads
+  // them from there, advances the fills in adv (no separate advance launch)
+  int32_t* snap;
+  int32_t* adv;
 };
 
 // K and V tiles live in LDS row-major, [kBN tokens][D] bf16, two stages
@@ -180,6 +185,9 @@ __global__ __launch_bounds__(waves_for(D) * 64, 1) void k_prefill_mfma(PrefillAr
     if constexpr (GEN) return sm.v[s_];
     else return (s_ == 0 ? lds0 : lds1) + kBN * D;
   };
+
+  if (a.snap != nullptr && blockIdx.x == 0)
+    for (int i = threadIdx.x; i < a.B; i += blockDim.x) a.snap[i] = a.start[i];
 
   // ---- which (sequence, kv head, split, query tile) this workgroup is ----
   const int w = blockIdx.x;
@@ -567,7 +575,12 @@ __global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a) {
   const int i = rb / a.Hq;
   const size_t rows = (size_t)a.B * a.C * a.Hq;
   const size_t row = (size_t)b * a.C * a.Hq + rb;
-  const int P = min(max(a.start[b], 0), a.T_cap);
+  // the fill as the call found it (from the snapshot when this pass also
+  // advances it: nothing here reads the fills themselves then)
+  const int P0 = a.snap != nullptr ? a.snap[b] : a.start[b];
+  if (a.adv != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    a.adv[b] = min(P0 + (a.n_new ? a.n_new[b] : a.C), a.T_cap);  // skv_advance's rule
+  const int P = min(max(P0, 0), a.T_cap);
   const int n = max(0, min(a.n_new ? min(a.n_new[b], a.C) : a.C, a.T_cap - P));
   float o[4] = {0.f, 0.f, 0.f, 0.f};
   // One split's weighted partial into (L, o), in split order.
@@ -639,6 +652,12 @@ bool dt_ok(int dt) { return dt == SKV_F32 || dt == SKV_BF16; }
 
 using namespace skv;
 
+namespace {
+size_t prefill_part_bytes(int B, int C, int H_q, int D, int n_splits) {
+  return (size_t)n_splits * B * C * H_q * (size_t)(kernel_dim(D) + 2) * sizeof(float);
+}
+}  // namespace
+
 extern "C" int skv_prefill_plan(int B, int C, int H_q, int H_kv, int max_kv_end, int* n_splits) {
   SKV_REQUIRE(n_splits, SKV_E_INVALID, "skv_prefill_plan: null output");
   SKV_REQUIRE(B > 0 && C > 0 && H_q > 0 && H_kv > 0 && max_kv_end > 0 && H_q % H_kv == 0,
@@ -658,16 +677,21 @@ extern "C" int skv_prefill_plan(int B, int C, int H_q, int H_kv, int max_kv_end,
 
 extern "C" size_t skv_prefill_workspace_bytes(int B, int C, int H_q, int D, int n_splits) {
   if (B <= 0 || C <= 0 || H_q <= 0 || D <= 0 || n_splits <= 1) return 0;
-  // partials at the kernel's (padded) head dim
-  return (size_t)n_splits * B * C * H_q * (size_t)(kernel_dim(D) + 2) * sizeof(float);
+  // partials at the kernel's (padded) head dim, then the fills' snapshot of
+  // skv_append_prefill_attn (B int32, 16-byte padded)
+  return prefill_part_bytes(B, C, H_q, D, n_splits) + ((size_t)B * sizeof(int32_t) + 15) / 16 * 16;
 }
 
-extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
-                                const void* v_cache, const int32_t* start, const int32_t* n_new,
-                                int B, int C, int H_q, int H_kv, int D, int T_cap, float scale,
-                                int n_splits, void* ws, size_t ws_bytes, int cache_dt, int q_dt,
-                                int out_dt, skv_stream_t stream) {
-  const char* fn = "skv_prefill_attn";
+namespace {
+
+// skv_prefill_attn's checks and launches. adv (split bf16 path only): the
+// merge pass advances these fills (skv_advance's rule) from the snapshot at
+// the end of ws. launch = false: the checks alone, nothing launched.
+int prefill_attn_impl(void* out, const void* q, const void* k_cache, const void* v_cache,
+                      const int32_t* start, const int32_t* n_new, int B, int C, int H_q,
+                      int H_kv, int D, int T_cap, float scale, int n_splits, void* ws,
+                      size_t ws_bytes, int cache_dt, int q_dt, int out_dt, skv_stream_t stream,
+                      const char* fn, int32_t* adv, bool launch) {
   SKV_REQUIRE(out && q && k_cache && v_cache && start, SKV_E_INVALID, "%s: null pointer argument",
               fn);
   SKV_REQUIRE(B > 0 && C > 0 && H_q > 0 && H_kv > 0 && T_cap > 0, SKV_E_INVALID,
@@ -680,6 +704,16 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
   if (cache_dt == SKV_F32) {  // fp32 cache: the fp32 MFMA path, no split
     SKV_REQUIRE(q_dt == SKV_F32 && out_dt == SKV_F32, SKV_E_UNSUPPORTED,
                 "%s: an fp32 cache takes fp32 q and out", fn);
+    if (!launch) {  // attn_fwd_f32's own checks (128 queries a workgroup there)
+      SKV_REQUIRE(D >= 1 && D <= 256, SKV_E_UNSUPPORTED, "%s: head_dim %d (supported: 1 to 256)",
+                  fn, D);
+      SKV_REQUIRE((((uintptr_t)out | (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) &
+                   15) == 0,
+                  SKV_E_INVALID, "%s: q, k, v and out must be 16-byte aligned", fn);
+      SKV_REQUIRE((long)((C + 127) / 128) * B * H_q < (1L << 31), SKV_E_UNSUPPORTED,
+                  "%s: grid too large", fn);
+      return SKV_OK;
+    }
     return attn_fwd_f32(static_cast<float*>(out), nullptr, nullptr, static_cast<const float*>(q),
                         static_cast<const float*>(k_cache), static_cast<const float*>(v_cache),
                         start, n_new, B, C, H_q, H_kv, D, T_cap, scale, (hipStream_t)stream, fn);
@@ -706,6 +740,13 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
                 fn, ws_bytes, need);
   }
   PrefillArgs a;
+  a.snap = nullptr;
+  a.adv = nullptr;
+  if (adv != nullptr && n_splits > 1) {
+    a.adv = adv;
+    a.snap = reinterpret_cast<int32_t*>(static_cast<char*>(ws) +
+                                        prefill_part_bytes(B, C, H_q, D, n_splits));
+  }
   a.q = q; a.out = out;
   a.k = static_cast<const uint16_t*>(k_cache);
   a.v = static_cast<const uint16_t*>(v_cache);
@@ -722,6 +763,7 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
   a.ws_ml = n_splits > 1 ? a.ws_o + (size_t)n_splits * B * C * H_q * DK : nullptr;
   const long blocks = (long)((a.n_groups + kXCD - 1) / kXCD) * kXCD * a.n_qt;
   SKV_REQUIRE(blocks < (1L << 31), SKV_E_UNSUPPORTED, "%s: grid too large", fn);
+  if (!launch) return SKV_OK;
   hipStream_t s = (hipStream_t)stream;
   // LV: 0 = LDS DMA at the exact head dim; 8 = 16-byte register loads; 1 = element loads
   const int LV = DK == D ? 0 : (D % 8 == 0 ? 8 : 1);
@@ -748,4 +790,39 @@ extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
     else hipLaunchKernelGGL((k_prefill_merge<256, true>), mgrid, dim3(256), 0, s, a);
   }
   return check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" int skv_prefill_attn(void* out, const void* q, const void* k_cache,
+                                const void* v_cache, const int32_t* start, const int32_t* n_new,
+                                int B, int C, int H_q, int H_kv, int D, int T_cap, float scale,
+                                int n_splits, void* ws, size_t ws_bytes, int cache_dt, int q_dt,
+                                int out_dt, skv_stream_t stream) {
+  return prefill_attn_impl(out, q, k_cache, v_cache, start, n_new, B, C, H_q, H_kv, D, T_cap,
+                           scale, n_splits, ws, ws_bytes, cache_dt, q_dt, out_dt, stream,
+                           "skv_prefill_attn", nullptr, true);
+}
+
+extern "C" int skv_append_prefill_attn(void* out, const void* q, void* k_cache, void* v_cache,
+                                       const void* k_new, const void* v_new, int32_t* lens,
+                                       const int32_t* n_new, int B, int C, int H_q, int H_kv,
+                                       int D, int T_cap, float scale, int n_splits, void* ws,
+                                       size_t ws_bytes, int cache_dt, int in_dt, int q_dt,
+                                       int out_dt, skv_stream_t stream) {
+  const char* fn = "skv_append_prefill_attn";
+  // every check of the attention first, so that a rejected call changes nothing
+  int rc = prefill_attn_impl(out, q, k_cache, v_cache, lens, n_new, B, C, H_q, H_kv, D, T_cap,
+                             scale, n_splits, ws, ws_bytes, cache_dt, q_dt, out_dt, stream, fn,
+                             lens, false);
+  if (rc) return rc;
+  rc = skv_append_chunk(k_cache, v_cache, k_new, v_new, lens, n_new, B, C, H_kv, D, T_cap,
+                        cache_dt, in_dt, stream);
+  if (rc) return rc;
+  rc = prefill_attn_impl(out, q, k_cache, v_cache, lens, n_new, B, C, H_q, H_kv, D, T_cap, scale,
+                         n_splits, ws, ws_bytes, cache_dt, q_dt, out_dt, stream, fn, lens, true);
+  if (rc) return rc;
+  // the split bf16 path's merge pass has advanced the fills; the others advance here
+  if (cache_dt == SKV_BF16 && n_splits > 1) return SKV_OK;
+  return skv_advance(lens, n_new, C, B, T_cap, stream);
 }

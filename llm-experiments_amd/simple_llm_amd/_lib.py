@@ -42,6 +42,8 @@ _SIGNATURES = {
     "skv_prefill_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
     "skv_prefill_attn": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _Z,
                               _I, _I, _I, _P]),
+    "skv_append_prefill_attn": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                     _F, _I, _P, _Z, _I, _I, _I, _I, _P]),
     "skv_embed": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "skv_layernorm": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "skv_linear": (_I, [_P, _P, _P, _P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _Z, _P]),

@@ -7,7 +7,7 @@ free functions of its JAX backend, and this module gives them a drop-in:
       simple-llm/src/jax_backend.py:143-148: logits of every position of
       [B, T] token ids. Here one prefill of all T tokens through the device
       model (skv_embed, the tiled MFMA projections of skv_linear,
-      skv_append_chunk, skv_prefill_attn), on a cache kept per batch size.
+      skv_append_prefill_attn), on a cache kept per batch size.
   sample_token(key, logits, temperature, top_k, top_p, min_p,
                repetition_penalty, recent_tokens)
       simple-llm/src/jax_backend.py:413-515: one next token from a logits

@@ -558,9 +558,6 @@ def kv_cache_prefill(ctx: GPUContext, cache: KVCache, layer_idx: int, new_k: tor
              torch.from_numpy(n_host.astype(np.int32)).to(dev, non_blocking=False))
     n_ptr = n_dev.data_ptr() if n_dev is not None else None
     kc, vc = layer.k_cache.buffer, layer.v_cache.buffer
-    rc = L.skv_append_chunk(kc.data_ptr(), vc.data_ptr(), new_k.data_ptr(), new_v.data_ptr(),
-                            layer.lens.data_ptr(), n_ptr, B, C, Hkv, D, T, cdt, idt, stream)
-    _lib.check(rc, "skv_append_chunk")
     if want_attn:
         ns = ctypes.c_int()
         if n_splits > 0:
@@ -571,13 +568,21 @@ def kv_cache_prefill(ctx: GPUContext, cache: KVCache, layer_idx: int, new_k: tor
         need = L.skv_prefill_workspace_bytes(B, C, Hq, D, ns.value)
         ws = _prefill_workspace(ctx, need)
         sc = float(scale) if scale is not None else 1.0 / float(np.sqrt(D))
-        rc = L.skv_prefill_attn(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                layer.lens.data_ptr(), n_ptr, B, C, Hq, Hkv, D, T, sc, ns.value,
-                                ws.data_ptr() if ws is not None else None,
-                                ws.numel() if ws is not None else 0, cdt,
-                                _lib.dtype_code(q.dtype), _lib.dtype_code(out.dtype), stream)
-        _lib.check(rc, "skv_prefill_attn")
-    rc = L.skv_advance(layer.lens.data_ptr(), n_ptr, C, B, T, stream)
-    _lib.check(rc, "skv_advance")
+        # chunk append + attention + fill advance in one call
+        rc = L.skv_append_prefill_attn(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                       new_k.data_ptr(), new_v.data_ptr(), layer.lens.data_ptr(),
+                                       n_ptr, B, C, Hq, Hkv, D, T, sc, ns.value,
+                                       ws.data_ptr() if ws is not None else None,
+                                       ws.numel() if ws is not None else 0, cdt, idt,
+                                       _lib.dtype_code(q.dtype), _lib.dtype_code(out.dtype),
+                                       stream)
+        _lib.check(rc, "skv_append_prefill_attn")
+    else:
+        rc = L.skv_append_chunk(kc.data_ptr(), vc.data_ptr(), new_k.data_ptr(),
+                                new_v.data_ptr(), layer.lens.data_ptr(), n_ptr, B, C, Hkv, D, T,
+                                cdt, idt, stream)
+        _lib.check(rc, "skv_append_chunk")
+        rc = L.skv_advance(layer.lens.data_ptr(), n_ptr, C, B, T, stream)
+        _lib.check(rc, "skv_advance")
     layer.host_lens = np.minimum(start + n_host, T)
     return layer.host_lens.copy()

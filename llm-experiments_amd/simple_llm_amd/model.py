@@ -14,9 +14,10 @@ libskv.so:
   * prefill: every prompt (a ragged batch) goes through all layers at once:
     embedding + position of every prompt row, the fused q/k/v projection as
     a tiled MFMA GEMM (LayerNorm applied as the rows are staged), the chunk
-    append into the cache (skv_append_chunk) and causal attention over it
-    (skv_prefill_attn: the fp32 MFMA kernel for an fp32 cache, the bf16 one
-    for a bf16 cache), output projection and MLP as GEMMs; then the logits of
+    append into the cache, causal attention over it and the fill advance in
+    one call (skv_append_prefill_attn: the fp32 MFMA kernel for an fp32
+    cache, the bf16 one for a bf16 cache), output projection and MLP as
+    GEMMs; then the logits of
     each sequence's last prompt row only;
   * decode: one token per sequence and step: embedding + position, fused
     q/k/v projection (LayerNorm folded into its reads), the cache append and
@@ -545,12 +546,11 @@ class TransformerModel:
                     "skv_gather_rows")
             # the chunk's k, v at each sequence's fill, then causal attention of
             # its queries over prefix + chunk; then the fill moves past the chunk
-            chk(L.skv_append_chunk(kc, vc, k_ptr, v_ptr, lens, n_ptr, B, C, H, D, T, cdt,
-                                   _lib.F32, s), "skv_append_chunk")
-            chk(L.skv_prefill_attn(attn, q_ptr, kc, vc, lens, n_ptr, B, C, H, H, D, T, scale,
-                                   ns.value, pws_ptr, pws_n, cdt, _lib.F32, _lib.F32, s),
-                "skv_prefill_attn")
-            chk(L.skv_advance(lens, n_ptr, C, B, T, s), "skv_advance")
+            # (one call)
+            chk(L.skv_append_prefill_attn(attn, q_ptr, kc, vc, k_ptr, v_ptr, lens, n_ptr, B, C,
+                                          H, H, D, T, scale, ns.value, pws_ptr, pws_n, cdt,
+                                          _lib.F32, _lib.F32, _lib.F32, s),
+                "skv_append_prefill_attn")
             a_rows = attn
             if packed:  # the valid rows of the attention output, packed, into qkv's space
                 chk(L.skv_gather_rows(qkv, attn, pb.gather_pk.data_ptr(), Mp, d, M, s),

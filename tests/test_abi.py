@@ -220,7 +220,7 @@ def test_prefill_rejects_bad_arguments():
     assert call(Hq=12) == _lib.SKV_E_UNSUPPORTED  # G = 3
     assert call(ns=33) == _lib.SKV_E_INVALID
     need = L.skv_prefill_workspace_bytes(2, 16, 4, 128, 2)
-    assert need == 2 * 2 * 16 * 4 * (128 + 2) * 4
+    assert need == 2 * 2 * 16 * 4 * (128 + 2) * 4 + 16  # partials, then the fills' snapshot
     assert call(ns=2, ws=fake, ws_bytes=need - 1) == _lib.SKV_E_WORKSPACE
     # 65536 kv heads of 256: a 64-row K/V tile spans more than 2 GB of cache rows
     assert L.skv_prefill_attn(fake, fake, fake, fake, fake, None, 2, 16, 65536, 65536, 256, 1024,

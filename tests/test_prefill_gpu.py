@@ -239,3 +239,58 @@ def test_prefill_c4_full_size_sampled(gpu_ctx):
         vh = vv[b, :P + i + 1, h].float().cpu().numpy()[None, :, None, :]
         want = ko.decode_attention(qh[b:b + 1, i, h:h + 1], kh, vh, [P + i + 1])
         assert rel_err(got[b:b + 1, i, h:h + 1], want) < BF16_TOL
+
+
+@pytest.mark.parametrize("cache_dt,n_splits,ragged", [("bf16", 1, False), ("bf16", 2, True),
+                                                      ("bf16", 3, False), ("f32", 1, True)])
+def test_fused_prefill_call_equals_the_three_calls(gpu_ctx, cache_dt, n_splits, ragged):
+    """skv_append_prefill_attn against skv_append_chunk + skv_prefill_attn +
+    skv_advance on the same inputs: the same output bits, cache bytes and
+    fills (on the split bf16 path the merge pass advances the fills from the
+    snapshot in the workspace's tail)."""
+    banner(f"fused prefill call vs three calls: {cache_dt} n_splits={n_splits} ragged={ragged}")
+    from simple_llm_amd import _lib
+    L = _lib.lib()
+    s = _lib.stream_handle()
+    B, T, Hq, Hkv, D, C = 3, 1500, 8, 4, 128, 160
+    tdt = torch.bfloat16 if cache_dt == "bf16" else torch.float32
+    cdt = _lib.BF16 if cache_dt == "bf16" else _lib.F32
+    rng = np.random.default_rng(n_splits * 10 + ragged)
+    prefix = np.array([1200, 0, 777], np.int32)
+    n_new = np.array([160, 1, 93], np.int32) if ragged else None
+    base_k = torch.from_numpy(rng.standard_normal((B * T, Hkv * D)).astype(np.float32)).cuda().to(tdt)
+    base_v = torch.from_numpy(rng.standard_normal((B * T, Hkv * D)).astype(np.float32)).cuda().to(tdt)
+    kn = to_dev(rng.standard_normal((B, C, Hkv, D)).astype(np.float32))
+    vn = to_dev(rng.standard_normal((B, C, Hkv, D)).astype(np.float32))
+    q = to_dev(rng.standard_normal((B, C, Hq, D)).astype(np.float32))
+    nd = to_dev(n_new, torch.int32) if ragged else None
+    n_ptr = nd.data_ptr() if nd is not None else None
+    need = L.skv_prefill_workspace_bytes(B, C, Hq, D, n_splits)
+    results = []
+    for fused in (False, True):
+        kc, vc = base_k.clone(), base_v.clone()
+        lens = to_dev(prefix, torch.int32)
+        out = torch.full((B, C, Hq, D), float("nan"), device="cuda")
+        ws = torch.full((max(need, 16),), 0xAB, dtype=torch.uint8, device="cuda")
+        args = (B, C, Hq, Hkv, D, T, D ** -0.5, n_splits, ws.data_ptr(), ws.numel())
+        if fused:
+            _lib.check(L.skv_append_prefill_attn(out.data_ptr(), q.data_ptr(), kc.data_ptr(),
+                                                 vc.data_ptr(), kn.data_ptr(), vn.data_ptr(),
+                                                 lens.data_ptr(), n_ptr, *args, cdt, _lib.F32,
+                                                 _lib.F32, _lib.F32, s), "skv_append_prefill_attn")
+        else:
+            _lib.check(L.skv_append_chunk(kc.data_ptr(), vc.data_ptr(), kn.data_ptr(),
+                                          vn.data_ptr(), lens.data_ptr(), n_ptr, B, C, Hkv, D, T,
+                                          cdt, _lib.F32, s), "skv_append_chunk")
+            _lib.check(L.skv_prefill_attn(out.data_ptr(), q.data_ptr(), kc.data_ptr(),
+                                          vc.data_ptr(), lens.data_ptr(), n_ptr, *args, cdt,
+                                          _lib.F32, _lib.F32, s), "skv_prefill_attn")
+            _lib.check(L.skv_advance(lens.data_ptr(), n_ptr, C, B, T, s), "skv_advance")
+        torch.cuda.synchronize()
+        results.append((out.cpu(), kc.cpu(), vc.cpu(), lens.cpu()))
+    (o0, k0, v0, l0), (o1, k1, v1, l1) = results
+    nn = n_new if ragged else np.full(B, C)
+    np.testing.assert_array_equal(l1.numpy(), np.minimum(prefix + nn, T))
+    np.testing.assert_array_equal(l1.numpy(), l0.numpy())
+    assert torch.equal(k1, k0) and torch.equal(v1, v0)
+    assert torch.equal(o1, o0)  # NaN-filled before: every element written, the same bits
