@@ -1,6 +1,6 @@
-"""Parity of the MFMA chunked prefill (skv_append_chunk + skv_prefill_attn +
-skv_advance, driven through kv_cache_prefill) with the CPU oracle. Needs the
-MI355X.
+"""Parity of the MFMA chunked prefill (skv_append_prefill_attn: skv_append_chunk
++ skv_prefill_attn + the fill advance, driven through kv_cache_prefill) with
+the CPU oracle. Needs the MI355X.
 
 On bf16 caches the prefill feeds Q, K, V and the softmax probabilities to
 v_mfma_f32_32x32x16_bf16 in bf16, with fp32 accumulation and softmax (fp32
