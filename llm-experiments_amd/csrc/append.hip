@@ -131,16 +131,19 @@ __device__ __forceinline__ void copy_vec(TC* __restrict__ dst, const TI* __restr
 // fp32 -> bf16, took 16 us for C4's 50 MB chunk, 3.1 TB/s, on MI355X.)
 // Rows i < n_new[b] of sequence b go to position lens[b] + i. lens is read
 // only.
-template <typename TC, typename TI>
+// NV = 2 (fp32 input into a bf16 cache): two 16-byte input vectors per
+// thread, so the 8 bf16 results go out as one 16-byte store.
+template <typename TC, typename TI, int NV = 1>
 __global__ __launch_bounds__(256) void k_append_chunk(TC* __restrict__ kc, TC* __restrict__ vc,
                                                       const TI* __restrict__ kn,
                                                       const TI* __restrict__ vn,
                                                       const int32_t* __restrict__ lens,
                                                       const int32_t* __restrict__ n_new, int C,
                                                       int E, int T_cap) {
-  constexpr int V = In16<TI>::N;  // elements per 16-byte input vector
+  static_assert(NV == 1 || (sizeof(TC) == 2 && sizeof(TI) == 4), "pairs: fp32 -> bf16 only");
+  constexpr int V = In16<TI>::N * NV;  // elements per thread
   const int b = blockIdx.y;
-  const int nv = E / V;           // vectors per row
+  const int nv = E / V;           // thread slots per row
   const int g = blockIdx.x * 256 + threadIdx.x;
   const int r = g / nv, e = (g - r * nv) * V;
   const int n = n_new ? min(n_new[b], C) : C;
@@ -148,8 +151,23 @@ __global__ __launch_bounds__(256) void k_append_chunk(TC* __restrict__ kc, TC* _
   if (r >= n || pos < 0 || pos >= T_cap) return;
   const size_t dst = ((size_t)b * T_cap + pos) * E + e;
   const size_t src = ((size_t)b * C + r) * E + e;
-  copy_vec<TC, TI>(kc + dst, kn + src);
-  copy_vec<TC, TI>(vc + dst, vn + src);
+  if constexpr (NV == 2) {
+    auto pack8 = [](TC* d, const float* sp) {
+      float f[8];
+      In16<float>::load(sp, f);
+      In16<float>::load(sp + 4, f + 4);
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)f32_to_bf16(f[2 * i]) | ((uint32_t)f32_to_bf16(f[2 * i + 1]) << 16);
+      *reinterpret_cast<uint4*>(d) = make_uint4(w[0], w[1], w[2], w[3]);
+    };
+    pack8(kc + dst, reinterpret_cast<const float*>(kn + src));
+    pack8(vc + dst, reinterpret_cast<const float*>(vn + src));
+  } else {
+    copy_vec<TC, TI>(kc + dst, kn + src);
+    copy_vec<TC, TI>(vc + dst, vn + src);
+  }
 }
 
 // Chunk append of rows whose E is not a multiple of 8: grid (tiles of C * E
@@ -265,7 +283,9 @@ extern "C" int skv_append_chunk(void* k_cache, void* v_cache, const void* k_new,
   // 16-byte vectors when every row is 16-byte aligned in both dtypes
   const bool vec = E % 8 == 0 && aligned16(k_cache) && aligned16(v_cache) && aligned16(k_new) &&
                    aligned16(v_new);
-  const int V = vec ? (in_dt == SKV_BF16 ? 8 : 4) : 1;  // elements per thread
+  // fp32 rows into a bf16 cache: 8 elements a thread (E % 8 == 0 here)
+  const bool pairs = vec && in_dt == SKV_F32 && cache_dt == SKV_BF16;
+  const int V = vec ? (in_dt == SKV_BF16 || pairs ? 8 : 4) : 1;  // elements per thread
   dim3 grid((unsigned)(((size_t)C * (E / V) + 255) / 256), B), block(256);
   hipStream_t s = (hipStream_t)stream;
 #define SKV_CHUNK_CASE(TC, TI)                                                                  \
@@ -281,6 +301,10 @@ extern "C" int skv_append_chunk(void* k_cache, void* v_cache, const void* k_new,
   } while (0)
   if (cache_dt == SKV_F32 && in_dt == SKV_F32) SKV_CHUNK_CASE(float, float);
   else if (cache_dt == SKV_F32 && in_dt == SKV_BF16) SKV_CHUNK_CASE(float, uint16_t);
+  else if (pairs)
+    hipLaunchKernelGGL((k_append_chunk<uint16_t, float, 2>), grid, block, 0, s,
+                       (uint16_t*)k_cache, (uint16_t*)v_cache, (const float*)k_new,
+                       (const float*)v_new, lens, n_new, C, E, T_cap);
   else if (cache_dt == SKV_BF16 && in_dt == SKV_F32) SKV_CHUNK_CASE(uint16_t, float);
   else SKV_CHUNK_CASE(uint16_t, uint16_t);
 #undef SKV_CHUNK_CASE
